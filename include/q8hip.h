@@ -1,0 +1,154 @@
+/*
+ * q8hip.h -- C ABI of libq8hip.so, the MI355X (gfx950) implementation of the
+ * INT8 group-quantized, weight-only (W8A32) linear-layer path.
+ *
+ * The reference keeps weights in one u16 "weight arena" and activations in
+ * one f32 "activation arena" and addresses tensors by element offsets into
+ * them (src/resident.mojo:15-58, src/llama_common.mojo:578-606).  This ABI
+ * keeps that convention: buffers are opaque handles, and every tensor is a
+ * (buffer, offset) pair with offsets in the arena's element units (u16 for
+ * weights, f32 for activations).  Only plain integers and pointers cross the
+ * boundary, so Mojo's sys.ffi (or ctypes, cgo, ...) can bind every entry
+ * point without struct-by-value.
+ *
+ * Packed row layout (qwen3_mojo/scripts/quantize.py:4-12,41-43):
+ *     [ (m/G) scales | m int8 codes ]          as little-endian u16 elements
+ * scale_dtype Q8_SCALE_F16 stores each scale as one binary16 (the reference
+ * layout, G = 64); Q8_SCALE_F32 stores each scale as an f32 (two u16).
+ * Supported group sizes: 32 and 64.
+ *
+ * Every call validates its arguments on the host before any HIP call and
+ * returns a status (0 = OK, < 0 = error); q8_last_error(ctx) gives the
+ * message.  Compute calls are asynchronous on the context's stream and a
+ * context must not be used from two threads at once (the reference runs one
+ * in-order queue per DeviceContext).
+ */
+#ifndef Q8HIP_H
+#define Q8HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- status codes ---------------------------------------------------- */
+#define Q8_OK              0
+#define Q8_ERR_ARG        -1   /* null handle, negative size, bad enum      */
+#define Q8_ERR_SHAPE      -2   /* m % G != 0, s/n/m out of range            */
+#define Q8_ERR_RANGE      -3   /* offset + extent beyond the buffer         */
+#define Q8_ERR_HIP        -4   /* HIP runtime error                         */
+#define Q8_ERR_NOMEM      -5   /* device allocation failed                  */
+#define Q8_ERR_NODEVICE   -6   /* arguments valid, but the context is a     */
+                               /* host-only validation context (device -1)  */
+#define Q8_ERR_UNSUPPORTED -7  /* valid request this build does not handle  */
+
+/* ---- enums ------------------------------------------------------------ */
+#define Q8_SCALE_F16 1         /* binary16 scale per group (reference)      */
+#define Q8_SCALE_F32 2         /* f32 scale per group                       */
+#define Q8_SRC_BF16  1         /* pack input dtype                          */
+#define Q8_SRC_F32   2
+
+#define Q8_DEVICE_NONE (-1)    /* q8_create: host-only validation context   */
+
+typedef struct q8_ctx q8_ctx;
+typedef struct q8_buf q8_buf;
+
+/* ---- library / context ------------------------------------------------ */
+
+/* ABI version of this header (major * 100 + minor). */
+int q8_version(void);
+
+/* Packed row length in u16 elements for m inputs; 0 if (m, G, scale_dtype)
+ * is invalid.  Replaces q8_rowstride (src/llama_q8.mojo:26-28). */
+uint64_t q8_rowstride_u16(int64_t m, int G, int scale_dtype);
+
+/* Create a context on HIP device `device_ordinal` owning one HIP stream.
+ * Q8_DEVICE_NONE creates a host-only context: buffers carry sizes only and
+ * compute calls validate their arguments and return Q8_ERR_NODEVICE.
+ * Replaces DeviceContext() + Q8Kernels(ctx) (src/llama_q8.mojo:115-121). */
+int q8_create(int device_ordinal, q8_ctx **out);
+void q8_destroy(q8_ctx *ctx);
+
+/* Run subsequent calls on an existing hipStream_t (NULL: the context's own
+ * stream).  The caller keeps ownership of the stream. */
+int q8_set_stream(q8_ctx *ctx, void *hip_stream);
+void *q8_get_stream(q8_ctx *ctx);
+
+/* Wait for all work queued on the context's stream (ctx.synchronize()). */
+int q8_sync(q8_ctx *ctx);
+
+/* Message of the last failing call on this context ("" if none).  With
+ * ctx == NULL: the last error of a failed q8_create on this thread. */
+const char *q8_last_error(q8_ctx *ctx);
+
+/* ---- buffers (arenas) --------------------------------------------------- */
+
+/* Library-owned device allocation (enqueue_create_buffer,
+ * src/resident.mojo:22, src/llama_common.mojo:588). */
+int q8_buf_alloc(q8_ctx *ctx, uint64_t nbytes, q8_buf **out);
+/* Non-owning view of caller device memory (e.g. a torch tensor). */
+int q8_buf_wrap(q8_ctx *ctx, void *device_ptr, uint64_t nbytes, q8_buf **out);
+void q8_buf_free(q8_ctx *ctx, q8_buf *buf);
+uint64_t q8_buf_size(const q8_buf *buf);
+void *q8_buf_device_ptr(const q8_buf *buf);
+
+/* Host <-> device copies, synchronous with respect to the host
+ * (map_to_host + memcpy, src/resident.mojo:32-58). */
+int q8_buf_upload(q8_ctx *ctx, q8_buf *buf, uint64_t byte_off,
+                  const void *src, uint64_t nbytes);
+int q8_buf_download(q8_ctx *ctx, q8_buf *buf, uint64_t byte_off,
+                    void *dst, uint64_t nbytes);
+
+/* ---- the Q8 path ---------------------------------------------------------- */
+
+/* Quantize and pack n rows of m weights (bf16 or f32, at element offset
+ * src_off of src) into packed rows at u16 offset dst_off of dst.  Codes and
+ * scales are bit-identical to pack_q8 (qwen3_mojo/scripts/quantize.py:31-43)
+ * for G = 64 / Q8_SCALE_F16.  Q8_SCALE_F32 keeps the scale in f32. */
+int q8_quantize_pack(q8_ctx *ctx, q8_buf *src, uint64_t src_off, int src_dtype,
+                     int64_t n, int64_t m, q8_buf *dst, uint64_t dst_off_u16,
+                     int G, int scale_dtype);
+
+/* y[s, n] = x[s, m] . deq(W[n, m])^T in f32, with x at f32 offset ox and y
+ * at f32 offset oy of the activation arena `a`, and W's packed rows at u16
+ * offset owt of the weight arena `w` -- the k_mm_q8 / mm_q8_op contract
+ * (src/llama_q8.mojo:54-93,124-141).  y must not overlap x.  The caller
+ * allocates y (Acts.alloc), as mm_q8_op does. */
+int q8_linear(q8_ctx *ctx, q8_buf *w, uint64_t owt_u16, q8_buf *a,
+              uint64_t ox_f32, uint64_t oy_f32, int64_t s, int64_t m, int64_t n,
+              int G, int scale_dtype);
+
+/* Prefill variant with bf16 activations: x bf16 [s, m] at element offset ox
+ * of buffer x, y f32 [s, n] at f32 offset oy of buffer y.  Runs on bf16 MFMA
+ * with exact int8 codes and a per-group f32 rescale.  No reference
+ * counterpart (the reference is W8A32 only); it is the M = 512 bf16-
+ * activation prefill case. */
+int q8_linear_bf16act(q8_ctx *ctx, q8_buf *w, uint64_t owt_u16, q8_buf *x,
+                      uint64_t ox_bf16, q8_buf *y, uint64_t oy_f32, int64_t s,
+                      int64_t m, int64_t n, int G, int scale_dtype);
+
+/* y[i, c] = f32(q[id_i, c]) * f32(scale[id_i, c / G]) for i < s, c < d:
+ * embedding rows gathered from packed rows (k_embed_gather_q8,
+ * src/llama_q8.mojo:96-109).  ids are int32 at element offset oids of `ids`;
+ * `vocab` is the number of packed rows at oemb.  An id outside [0, vocab)
+ * yields a row of NaN instead of an out-of-bounds read. */
+int q8_embed_gather(q8_ctx *ctx, q8_buf *w, uint64_t oemb_u16, q8_buf *ids,
+                    uint64_t oids_i32, q8_buf *a, uint64_t oy_f32, int64_t s,
+                    int64_t d, int64_t vocab, int G, int scale_dtype);
+
+/* ---- HIP graphs ------------------------------------------------------------ */
+
+/* Capture every call issued on the context's stream between begin and end
+ * into a hipGraph, then replay it with q8_graph_launch.  Used to amortise
+ * the launch cost of a whole decode step.  *graph is an opaque handle. */
+int q8_graph_begin(q8_ctx *ctx);
+int q8_graph_end(q8_ctx *ctx, void **graph);
+int q8_graph_launch(q8_ctx *ctx, void *graph);
+void q8_graph_destroy(void *graph);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* Q8HIP_H */

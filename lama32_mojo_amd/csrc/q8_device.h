@@ -1,0 +1,93 @@
+// q8_device.h -- device-side helpers shared by the gfx950 kernels.
+//
+// Packed rows (qwen3_mojo/scripts/quantize.py:4-12): [ (m/G) scales | m int8 ]
+// with each scale a binary16 (SCALE_F16, the reference layout) or an f32
+// (SCALE_F32).  All kernels address a row by its byte base and take the
+// scale section's size in bytes, so both layouts share one code path.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace q8 {
+
+enum ScaleKind { SCALE_F16 = 1, SCALE_F32 = 2 };
+
+template <int KIND> struct ScaleTraits;
+template <> struct ScaleTraits<SCALE_F16> { static constexpr int bytes = 2; };
+template <> struct ScaleTraits<SCALE_F32> { static constexpr int bytes = 4; };
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef short i16x8 __attribute__((ext_vector_type(8)));
+
+__device__ __forceinline__ float f16_bits_to_f32(uint16_t h) {
+  return (float)__builtin_bit_cast(_Float16, h);
+}
+
+// f32 -> binary16 with the hardware conversion (round to nearest even in the
+// default float mode; binary16 denormals are kept on gfx9).
+__device__ __forceinline__ uint16_t f32_to_f16_bits(float f) {
+  return __builtin_bit_cast(uint16_t, (_Float16)f);
+}
+
+__device__ __forceinline__ float bf16_bits_to_f32(uint32_t b) {
+  return __builtin_bit_cast(float, b << 16);
+}
+
+// Scale g of a packed row starting at byte pointer `row`.
+template <int KIND>
+__device__ __forceinline__ float load_scale(const uint8_t *row, int64_t g) {
+  if constexpr (KIND == SCALE_F16) {
+    return f16_bits_to_f32(*reinterpret_cast<const uint16_t *>(row + 2 * g));
+  } else {
+    // f32 scales sit at 2-byte alignment in general: assemble from halves.
+    const uint16_t *p = reinterpret_cast<const uint16_t *>(row + 4 * g);
+    return __builtin_bit_cast(float, (uint32_t)p[0] | ((uint32_t)p[1] << 16));
+  }
+}
+
+// Signed byte `i` (0..3) of a dword, converted to f32 exactly.
+template <int I>
+__device__ __forceinline__ float sbyte_to_f32(uint32_t w) {
+  return (float)(int32_t)((int32_t)(w << (24 - 8 * I)) >> 24);
+}
+
+// ---- wavefront reductions (wave64) --------------------------------------
+// DPP row operations reduce within each row of 16 lanes; the four row sums
+// are then combined with readlane.  Every lane returns the full sum.
+template <int CTRL>
+__device__ __forceinline__ float dpp_mov(float v) {
+  return __builtin_bit_cast(
+      float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL,
+                                         0xf, 0xf, false));
+}
+
+__device__ __forceinline__ float row16_sum(float v) {
+  v += dpp_mov<0xb1>(v);   // quad_perm [1,0,3,2]
+  v += dpp_mov<0x4e>(v);   // quad_perm [2,3,0,1]
+  v += dpp_mov<0x141>(v);  // row_half_mirror
+  v += dpp_mov<0x140>(v);  // row_mirror
+  return v;
+}
+
+__device__ __forceinline__ float wave_sum(float v) {
+  v = row16_sum(v);
+  float a = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 0));
+  float b = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 16));
+  float c = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 32));
+  float d = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 48));
+  return (a + b) + (c + d);
+}
+
+// Max of |.| with NaN propagation (numpy's max propagates NaN).
+__device__ __forceinline__ float nanmax(float a, float b) {
+  if (a != a) return a;
+  if (b != b) return b;
+  return a > b ? a : b;
+}
+
+}  // namespace q8

@@ -1,0 +1,500 @@
+// q8hip_api.cpp -- the C ABI of libq8hip.so (declared in include/q8hip.h).
+//
+// Host side of the Q8 path: contexts (one HIP stream each), buffers
+// (arenas addressed by element offsets, as the reference's Weights / Acts,
+// src/resident.mojo:15-58 and src/llama_common.mojo:578-606), argument
+// validation, kernel dispatch and HIP-graph capture.  Every entry point
+// validates all of its arguments before the first HIP call, so error paths
+// behave the same on a host-only context (device Q8_DEVICE_NONE) as on a GPU.
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <new>
+#include <string>
+
+#include "../../include/q8hip.h"
+#include "q8_launch.h"
+
+struct q8_ctx {
+  int device = -1;
+  bool host_only = true;
+  hipStream_t own = nullptr;
+  hipStream_t stream = nullptr;
+  std::string err;
+};
+
+struct q8_buf {
+  void *ptr = nullptr;
+  uint64_t size = 0;
+  bool owned = false;
+  q8_ctx *ctx = nullptr;
+};
+
+namespace {
+
+thread_local std::string g_create_err;
+
+int fail(q8_ctx *ctx, int code, const char *fmt, ...) {
+  char msg[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(msg, sizeof msg, fmt, ap);
+  va_end(ap);
+  if (ctx) ctx->err = msg;
+  else g_create_err = msg;
+  return code;
+}
+
+int ok(q8_ctx *ctx) {
+  if (ctx) ctx->err.clear();
+  return Q8_OK;
+}
+
+int hip_fail(q8_ctx *ctx, hipError_t e, const char *what) {
+  return fail(ctx, Q8_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
+}
+
+bool valid_layout(int G, int kind) {
+  return (G == 32 || G == 64) && (kind == Q8_SCALE_F16 || kind == Q8_SCALE_F32);
+}
+
+int64_t rowstride_u16(int64_t m, int G, int kind) {
+  return (m / G) * (kind == Q8_SCALE_F32 ? 2 : 1) + m / 2;
+}
+
+// a * b + c <= limit without overflow (all non-negative).
+bool fits(uint64_t off, uint64_t count, uint64_t elem, uint64_t limit_bytes) {
+  unsigned __int128 end = ((unsigned __int128)off + count) * elem;
+  return end <= limit_bytes;
+}
+
+bool overlaps(uint64_t a0, uint64_t a1, uint64_t b0, uint64_t b1) {
+  return a0 < b1 && b0 < a1;
+}
+
+int check_ctx(q8_ctx *ctx) {
+  if (!ctx) return fail(nullptr, Q8_ERR_ARG, "null context");
+  return Q8_OK;
+}
+
+int set_device(q8_ctx *ctx) {
+  hipError_t e = hipSetDevice(ctx->device);
+  if (e != hipSuccess) return hip_fail(ctx, e, "hipSetDevice");
+  return Q8_OK;
+}
+
+uint8_t *bytes(q8_buf *b, uint64_t off) {
+  return static_cast<uint8_t *>(b->ptr) + off;
+}
+
+int check_layout(q8_ctx *ctx, int64_t m, int G, int kind, const char *what) {
+  if (!valid_layout(G, kind))
+    return fail(ctx, Q8_ERR_ARG, "%s: unsupported layout G=%d scale_dtype=%d "
+                "(G must be 32 or 64, scale_dtype Q8_SCALE_F16 or Q8_SCALE_F32)",
+                what, G, kind);
+  if (m <= 0 || m % G != 0)
+    return fail(ctx, Q8_ERR_SHAPE, "%s: m=%lld must be a positive multiple of G=%d",
+                what, (long long)m, G);
+  return Q8_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int q8_version(void) { return 100; }
+
+uint64_t q8_rowstride_u16(int64_t m, int G, int scale_dtype) {
+  if (!valid_layout(G, scale_dtype) || m <= 0 || m % G != 0) return 0;
+  return (uint64_t)rowstride_u16(m, G, scale_dtype);
+}
+
+int q8_create(int device_ordinal, q8_ctx **out) {
+  if (!out) return fail(nullptr, Q8_ERR_ARG, "q8_create: null output pointer");
+  *out = nullptr;
+  if (device_ordinal < Q8_DEVICE_NONE)
+    return fail(nullptr, Q8_ERR_ARG, "q8_create: bad device ordinal %d", device_ordinal);
+  q8_ctx *ctx = new (std::nothrow) q8_ctx();
+  if (!ctx) return fail(nullptr, Q8_ERR_NOMEM, "q8_create: out of host memory");
+  ctx->device = device_ordinal;
+  ctx->host_only = device_ordinal == Q8_DEVICE_NONE;
+  if (!ctx->host_only) {
+    int count = 0;
+    hipError_t e = hipGetDeviceCount(&count);
+    if (e != hipSuccess || device_ordinal >= count) {
+      delete ctx;
+      return fail(nullptr, Q8_ERR_HIP, "q8_create: device %d not available (%s, %d devices)",
+                  device_ordinal, hipGetErrorString(e), count);
+    }
+    e = hipSetDevice(device_ordinal);
+    if (e == hipSuccess) e = hipStreamCreateWithFlags(&ctx->own, hipStreamNonBlocking);
+    if (e != hipSuccess) {
+      delete ctx;
+      return fail(nullptr, Q8_ERR_HIP, "q8_create: %s", hipGetErrorString(e));
+    }
+    ctx->stream = ctx->own;
+  }
+  *out = ctx;
+  return Q8_OK;
+}
+
+void q8_destroy(q8_ctx *ctx) {
+  if (!ctx) return;
+  if (!ctx->host_only) {
+    (void)hipSetDevice(ctx->device);
+    if (ctx->own) {
+      (void)hipStreamSynchronize(ctx->own);
+      (void)hipStreamDestroy(ctx->own);
+    }
+  }
+  delete ctx;
+}
+
+int q8_set_stream(q8_ctx *ctx, void *hip_stream) {
+  if (int rc = check_ctx(ctx)) return rc;
+  if (ctx->host_only) return fail(ctx, Q8_ERR_NODEVICE, "q8_set_stream: host-only context");
+  ctx->stream = hip_stream ? static_cast<hipStream_t>(hip_stream) : ctx->own;
+  return ok(ctx);
+}
+
+void *q8_get_stream(q8_ctx *ctx) { return ctx ? static_cast<void *>(ctx->stream) : nullptr; }
+
+int q8_sync(q8_ctx *ctx) {
+  if (int rc = check_ctx(ctx)) return rc;
+  if (ctx->host_only) return ok(ctx);
+  if (int rc = set_device(ctx)) return rc;
+  hipError_t e = hipStreamSynchronize(ctx->stream);
+  if (e != hipSuccess) return hip_fail(ctx, e, "q8_sync");
+  return ok(ctx);
+}
+
+const char *q8_last_error(q8_ctx *ctx) {
+  return ctx ? ctx->err.c_str() : g_create_err.c_str();
+}
+
+// ---- buffers -------------------------------------------------------------------
+
+int q8_buf_alloc(q8_ctx *ctx, uint64_t nbytes, q8_buf **out) {
+  if (int rc = check_ctx(ctx)) return rc;
+  if (!out) return fail(ctx, Q8_ERR_ARG, "q8_buf_alloc: null output pointer");
+  *out = nullptr;
+  q8_buf *b = new (std::nothrow) q8_buf();
+  if (!b) return fail(ctx, Q8_ERR_NOMEM, "q8_buf_alloc: out of host memory");
+  b->size = nbytes;
+  b->ctx = ctx;
+  b->owned = true;
+  if (!ctx->host_only && nbytes > 0) {
+    if (int rc = set_device(ctx)) { delete b; return rc; }
+    hipError_t e = hipMalloc(&b->ptr, nbytes);
+    if (e != hipSuccess) {
+      delete b;
+      return fail(ctx, Q8_ERR_NOMEM, "q8_buf_alloc(%llu bytes): %s",
+                  (unsigned long long)nbytes, hipGetErrorString(e));
+    }
+  }
+  *out = b;
+  return ok(ctx);
+}
+
+int q8_buf_wrap(q8_ctx *ctx, void *device_ptr, uint64_t nbytes, q8_buf **out) {
+  if (int rc = check_ctx(ctx)) return rc;
+  if (!out) return fail(ctx, Q8_ERR_ARG, "q8_buf_wrap: null output pointer");
+  *out = nullptr;
+  if (!device_ptr && nbytes > 0 && !ctx->host_only)
+    return fail(ctx, Q8_ERR_ARG, "q8_buf_wrap: null device pointer");
+  q8_buf *b = new (std::nothrow) q8_buf();
+  if (!b) return fail(ctx, Q8_ERR_NOMEM, "q8_buf_wrap: out of host memory");
+  b->ptr = device_ptr;
+  b->size = nbytes;
+  b->ctx = ctx;
+  b->owned = false;
+  *out = b;
+  return ok(ctx);
+}
+
+void q8_buf_free(q8_ctx *ctx, q8_buf *buf) {
+  if (!buf) return;
+  if (buf->owned && buf->ptr && ctx && !ctx->host_only) {
+    (void)hipSetDevice(ctx->device);
+    (void)hipStreamSynchronize(ctx->stream);
+    (void)hipFree(buf->ptr);
+  }
+  delete buf;
+}
+
+uint64_t q8_buf_size(const q8_buf *buf) { return buf ? buf->size : 0; }
+void *q8_buf_device_ptr(const q8_buf *buf) { return buf ? buf->ptr : nullptr; }
+
+int q8_buf_upload(q8_ctx *ctx, q8_buf *buf, uint64_t byte_off, const void *src, uint64_t nbytes) {
+  if (int rc = check_ctx(ctx)) return rc;
+  if (!buf || (!src && nbytes)) return fail(ctx, Q8_ERR_ARG, "q8_buf_upload: null argument");
+  if (!fits(byte_off, nbytes, 1, buf->size))
+    return fail(ctx, Q8_ERR_RANGE, "q8_buf_upload: [%llu, +%llu) exceeds buffer of %llu bytes",
+                (unsigned long long)byte_off, (unsigned long long)nbytes,
+                (unsigned long long)buf->size);
+  if (ctx->host_only) return fail(ctx, Q8_ERR_NODEVICE, "q8_buf_upload: host-only context");
+  if (nbytes == 0) return ok(ctx);
+  if (int rc = set_device(ctx)) return rc;
+  hipError_t e = hipMemcpyAsync(bytes(buf, byte_off), src, nbytes, hipMemcpyHostToDevice, ctx->stream);
+  if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+  if (e != hipSuccess) return hip_fail(ctx, e, "q8_buf_upload");
+  return ok(ctx);
+}
+
+int q8_buf_download(q8_ctx *ctx, q8_buf *buf, uint64_t byte_off, void *dst, uint64_t nbytes) {
+  if (int rc = check_ctx(ctx)) return rc;
+  if (!buf || (!dst && nbytes)) return fail(ctx, Q8_ERR_ARG, "q8_buf_download: null argument");
+  if (!fits(byte_off, nbytes, 1, buf->size))
+    return fail(ctx, Q8_ERR_RANGE, "q8_buf_download: [%llu, +%llu) exceeds buffer of %llu bytes",
+                (unsigned long long)byte_off, (unsigned long long)nbytes,
+                (unsigned long long)buf->size);
+  if (ctx->host_only) return fail(ctx, Q8_ERR_NODEVICE, "q8_buf_download: host-only context");
+  if (nbytes == 0) return ok(ctx);
+  if (int rc = set_device(ctx)) return rc;
+  hipError_t e = hipMemcpyAsync(dst, bytes(buf, byte_off), nbytes, hipMemcpyDeviceToHost, ctx->stream);
+  if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+  if (e != hipSuccess) return hip_fail(ctx, e, "q8_buf_download");
+  return ok(ctx);
+}
+
+// ---- Q8 path ------------------------------------------------------------------------
+
+int q8_quantize_pack(q8_ctx *ctx, q8_buf *src, uint64_t src_off, int src_dtype, int64_t n,
+                     int64_t m, q8_buf *dst, uint64_t dst_off_u16, int G, int scale_dtype) {
+  if (int rc = check_ctx(ctx)) return rc;
+  if (!src || !dst) return fail(ctx, Q8_ERR_ARG, "q8_quantize_pack: null buffer");
+  if (src_dtype != Q8_SRC_BF16 && src_dtype != Q8_SRC_F32)
+    return fail(ctx, Q8_ERR_ARG, "q8_quantize_pack: bad src_dtype %d", src_dtype);
+  if (int rc = check_layout(ctx, m, G, scale_dtype, "q8_quantize_pack")) return rc;
+  if (n < 0) return fail(ctx, Q8_ERR_SHAPE, "q8_quantize_pack: n=%lld < 0", (long long)n);
+  const uint64_t es = src_dtype == Q8_SRC_F32 ? 4 : 2;
+  const uint64_t rs = (uint64_t)rowstride_u16(m, G, scale_dtype);
+  const uint64_t ne = (uint64_t)n * (uint64_t)m;
+  if (!fits(src_off, ne, es, src->size))
+    return fail(ctx, Q8_ERR_RANGE, "q8_quantize_pack: source [%llu, +%llu) elements exceeds buffer",
+                (unsigned long long)src_off, (unsigned long long)ne);
+  if (!fits(dst_off_u16, (uint64_t)n * rs, 2, dst->size))
+    return fail(ctx, Q8_ERR_RANGE, "q8_quantize_pack: packed output [%llu, +%llu) u16 exceeds buffer",
+                (unsigned long long)dst_off_u16, (unsigned long long)((uint64_t)n * rs));
+  if (src == dst && overlaps(src_off * es, (src_off + ne) * es, dst_off_u16 * 2,
+                             (dst_off_u16 + (uint64_t)n * rs) * 2))
+    return fail(ctx, Q8_ERR_ARG, "q8_quantize_pack: source and destination overlap");
+  if (ctx->host_only) return fail(ctx, Q8_ERR_NODEVICE, "q8_quantize_pack: host-only context");
+  if (n == 0) return ok(ctx);
+  if (int rc = set_device(ctx)) return rc;
+  q8::PackArgs a;
+  a.src = bytes(src, src_off * es);
+  a.src_is_f32 = src_dtype == Q8_SRC_F32;
+  a.n = n;
+  a.m = m;
+  a.dst = bytes(dst, dst_off_u16 * 2);
+  a.dst_row_bytes = (int64_t)rs * 2;
+  a.G = G;
+  a.kind = scale_dtype;
+  hipError_t e = q8::launch_pack(a, ctx->stream);
+  if (e != hipSuccess) return hip_fail(ctx, e, "q8_quantize_pack launch");
+  return ok(ctx);
+}
+
+namespace {
+
+// Shapes and ranges shared by q8_linear and q8_linear_bf16act.
+int check_linear(q8_ctx *ctx, const char *what, q8_buf *w, uint64_t owt, int64_t s, int64_t m,
+                 int64_t n, int G, int kind) {
+  if (!w) return fail(ctx, Q8_ERR_ARG, "%s: null weight buffer", what);
+  if (int rc = check_layout(ctx, m, G, kind, what)) return rc;
+  if (s < 0 || n < 0)
+    return fail(ctx, Q8_ERR_SHAPE, "%s: s=%lld and n=%lld must be >= 0", what, (long long)s,
+                (long long)n);
+  const uint64_t rs = (uint64_t)rowstride_u16(m, G, kind);
+  if (!fits(owt, (uint64_t)n * rs, 2, w->size))
+    return fail(ctx, Q8_ERR_RANGE, "%s: weights [%llu, +%llu) u16 exceed the weight buffer (%llu bytes)",
+                what, (unsigned long long)owt, (unsigned long long)((uint64_t)n * rs),
+                (unsigned long long)w->size);
+  return Q8_OK;
+}
+
+bool gemm_aligned(const q8::LinearArgs &a) {
+  const int sb = a.kind == Q8_SCALE_F32 ? 4 : 2;
+  const uintptr_t xw = reinterpret_cast<uintptr_t>(a.x);
+  return reinterpret_cast<uintptr_t>(a.w) % 16 == 0 && a.row_bytes % 16 == 0 &&
+         ((a.m / a.G) * sb) % 16 == 0 && xw % 16 == 0 && a.m % 8 == 0;
+}
+
+// Activation rows at which the W8A32 path switches from the VALU GEMV to the
+// MFMA GEMM (f32 x split into two bf16 terms).
+constexpr int64_t kGemmMinRows = 32;
+
+}  // namespace
+
+int q8_linear(q8_ctx *ctx, q8_buf *w, uint64_t owt_u16, q8_buf *a, uint64_t ox_f32,
+              uint64_t oy_f32, int64_t s, int64_t m, int64_t n, int G, int scale_dtype) {
+  if (int rc = check_ctx(ctx)) return rc;
+  if (int rc = check_linear(ctx, "q8_linear", w, owt_u16, s, m, n, G, scale_dtype)) return rc;
+  if (!a) return fail(ctx, Q8_ERR_ARG, "q8_linear: null activation buffer");
+  const uint64_t nx = (uint64_t)s * (uint64_t)m, ny = (uint64_t)s * (uint64_t)n;
+  if (!fits(ox_f32, nx, 4, a->size))
+    return fail(ctx, Q8_ERR_RANGE, "q8_linear: x [%llu, +%llu) f32 exceeds the activation buffer",
+                (unsigned long long)ox_f32, (unsigned long long)nx);
+  if (!fits(oy_f32, ny, 4, a->size))
+    return fail(ctx, Q8_ERR_RANGE, "q8_linear: y [%llu, +%llu) f32 exceeds the activation buffer",
+                (unsigned long long)oy_f32, (unsigned long long)ny);
+  if (nx && ny && overlaps(ox_f32, ox_f32 + nx, oy_f32, oy_f32 + ny))
+    return fail(ctx, Q8_ERR_ARG, "q8_linear: x and y overlap");
+  if (ctx->host_only) return fail(ctx, Q8_ERR_NODEVICE, "q8_linear: host-only context");
+  if (s == 0 || n == 0) return ok(ctx);
+  if (int rc = set_device(ctx)) return rc;
+  q8::LinearArgs la;
+  la.w = bytes(w, owt_u16 * 2);
+  la.row_bytes = rowstride_u16(m, G, scale_dtype) * 2;
+  la.x = bytes(a, ox_f32 * 4);
+  la.x_is_bf16 = 0;
+  la.y = reinterpret_cast<float *>(bytes(a, oy_f32 * 4));
+  la.s = s;
+  la.m = m;
+  la.n = n;
+  la.G = G;
+  la.kind = scale_dtype;
+  hipError_t e = (s >= kGemmMinRows && gemm_aligned(la)) ? q8::launch_gemm(la, ctx->stream)
+                                                          : q8::launch_gemv(la, ctx->stream);
+  if (e != hipSuccess) return hip_fail(ctx, e, "q8_linear launch");
+  return ok(ctx);
+}
+
+int q8_linear_bf16act(q8_ctx *ctx, q8_buf *w, uint64_t owt_u16, q8_buf *x, uint64_t ox_bf16,
+                      q8_buf *y, uint64_t oy_f32, int64_t s, int64_t m, int64_t n, int G,
+                      int scale_dtype) {
+  if (int rc = check_ctx(ctx)) return rc;
+  if (int rc = check_linear(ctx, "q8_linear_bf16act", w, owt_u16, s, m, n, G, scale_dtype))
+    return rc;
+  if (!x || !y) return fail(ctx, Q8_ERR_ARG, "q8_linear_bf16act: null activation buffer");
+  const uint64_t nx = (uint64_t)s * (uint64_t)m, ny = (uint64_t)s * (uint64_t)n;
+  if (!fits(ox_bf16, nx, 2, x->size))
+    return fail(ctx, Q8_ERR_RANGE, "q8_linear_bf16act: x [%llu, +%llu) bf16 exceeds its buffer",
+                (unsigned long long)ox_bf16, (unsigned long long)nx);
+  if (!fits(oy_f32, ny, 4, y->size))
+    return fail(ctx, Q8_ERR_RANGE, "q8_linear_bf16act: y [%llu, +%llu) f32 exceeds its buffer",
+                (unsigned long long)oy_f32, (unsigned long long)ny);
+  if (x == y && nx && ny && overlaps(ox_bf16 * 2, (ox_bf16 + nx) * 2, oy_f32 * 4, (oy_f32 + ny) * 4))
+    return fail(ctx, Q8_ERR_ARG, "q8_linear_bf16act: x and y overlap");
+  if (ctx->host_only) return fail(ctx, Q8_ERR_NODEVICE, "q8_linear_bf16act: host-only context");
+  if (s == 0 || n == 0) return ok(ctx);
+  if (int rc = set_device(ctx)) return rc;
+  q8::LinearArgs la;
+  la.w = bytes(w, owt_u16 * 2);
+  la.row_bytes = rowstride_u16(m, G, scale_dtype) * 2;
+  la.x = bytes(x, ox_bf16 * 2);
+  la.x_is_bf16 = 1;
+  la.y = reinterpret_cast<float *>(bytes(y, oy_f32 * 4));
+  la.s = s;
+  la.m = m;
+  la.n = n;
+  la.G = G;
+  la.kind = scale_dtype;
+  hipError_t e = gemm_aligned(la) ? q8::launch_gemm(la, ctx->stream)
+                                  : q8::launch_gemv(la, ctx->stream);
+  if (e != hipSuccess) return hip_fail(ctx, e, "q8_linear_bf16act launch");
+  return ok(ctx);
+}
+
+int q8_embed_gather(q8_ctx *ctx, q8_buf *w, uint64_t oemb_u16, q8_buf *ids, uint64_t oids_i32,
+                    q8_buf *a, uint64_t oy_f32, int64_t s, int64_t d, int64_t vocab, int G,
+                    int scale_dtype) {
+  if (int rc = check_ctx(ctx)) return rc;
+  if (!w || !ids || !a) return fail(ctx, Q8_ERR_ARG, "q8_embed_gather: null buffer");
+  if (int rc = check_layout(ctx, d, G, scale_dtype, "q8_embed_gather")) return rc;
+  if (s < 0 || vocab < 0)
+    return fail(ctx, Q8_ERR_SHAPE, "q8_embed_gather: s=%lld and vocab=%lld must be >= 0",
+                (long long)s, (long long)vocab);
+  const uint64_t rs = (uint64_t)rowstride_u16(d, G, scale_dtype);
+  if (!fits(oemb_u16, (uint64_t)vocab * rs, 2, w->size))
+    return fail(ctx, Q8_ERR_RANGE, "q8_embed_gather: table of %lld rows exceeds the weight buffer",
+                (long long)vocab);
+  if (!fits(oids_i32, (uint64_t)s, 4, ids->size))
+    return fail(ctx, Q8_ERR_RANGE, "q8_embed_gather: ids [%llu, +%lld) exceed their buffer",
+                (unsigned long long)oids_i32, (long long)s);
+  if (!fits(oy_f32, (uint64_t)s * (uint64_t)d, 4, a->size))
+    return fail(ctx, Q8_ERR_RANGE, "q8_embed_gather: output exceeds the activation buffer");
+  if (ctx->host_only) return fail(ctx, Q8_ERR_NODEVICE, "q8_embed_gather: host-only context");
+  if (s == 0) return ok(ctx);
+  if (int rc = set_device(ctx)) return rc;
+  q8::GatherArgs ga;
+  ga.w = bytes(w, oemb_u16 * 2);
+  ga.row_bytes = (int64_t)rs * 2;
+  ga.ids = reinterpret_cast<const int32_t *>(bytes(ids, oids_i32 * 4));
+  ga.y = reinterpret_cast<float *>(bytes(a, oy_f32 * 4));
+  ga.s = s;
+  ga.d = d;
+  ga.vocab = vocab;
+  ga.G = G;
+  ga.kind = scale_dtype;
+  hipError_t e = q8::launch_embed_gather(ga, ctx->stream);
+  if (e != hipSuccess) return hip_fail(ctx, e, "q8_embed_gather launch");
+  return ok(ctx);
+}
+
+// ---- HIP graphs -------------------------------------------------------------------
+
+struct q8_graph {
+  hipGraph_t graph = nullptr;
+  hipGraphExec_t exec = nullptr;
+};
+
+int q8_graph_begin(q8_ctx *ctx) {
+  if (int rc = check_ctx(ctx)) return rc;
+  if (ctx->host_only) return fail(ctx, Q8_ERR_NODEVICE, "q8_graph_begin: host-only context");
+  if (int rc = set_device(ctx)) return rc;
+  hipError_t e = hipStreamBeginCapture(ctx->stream, hipStreamCaptureModeThreadLocal);
+  if (e != hipSuccess) return hip_fail(ctx, e, "q8_graph_begin");
+  return ok(ctx);
+}
+
+int q8_graph_end(q8_ctx *ctx, void **graph) {
+  if (int rc = check_ctx(ctx)) return rc;
+  if (!graph) return fail(ctx, Q8_ERR_ARG, "q8_graph_end: null output pointer");
+  *graph = nullptr;
+  if (ctx->host_only) return fail(ctx, Q8_ERR_NODEVICE, "q8_graph_end: host-only context");
+  if (int rc = set_device(ctx)) return rc;
+  q8_graph *g = new (std::nothrow) q8_graph();
+  hipGraph_t hg = nullptr;
+  hipError_t e = hipStreamEndCapture(ctx->stream, &hg);
+  if (!g) {
+    if (hg) (void)hipGraphDestroy(hg);
+    return fail(ctx, Q8_ERR_NOMEM, "q8_graph_end: out of host memory");
+  }
+  if (e != hipSuccess) {
+    delete g;
+    return hip_fail(ctx, e, "q8_graph_end (capture)");
+  }
+  g->graph = hg;
+  e = hipGraphInstantiate(&g->exec, hg, nullptr, nullptr, 0);
+  if (e != hipSuccess) {
+    (void)hipGraphDestroy(hg);
+    delete g;
+    return hip_fail(ctx, e, "q8_graph_end (instantiate)");
+  }
+  *graph = g;
+  return ok(ctx);
+}
+
+int q8_graph_launch(q8_ctx *ctx, void *graph) {
+  if (int rc = check_ctx(ctx)) return rc;
+  if (!graph) return fail(ctx, Q8_ERR_ARG, "q8_graph_launch: null graph");
+  if (ctx->host_only) return fail(ctx, Q8_ERR_NODEVICE, "q8_graph_launch: host-only context");
+  if (int rc = set_device(ctx)) return rc;
+  hipError_t e = hipGraphLaunch(static_cast<q8_graph *>(graph)->exec, ctx->stream);
+  if (e != hipSuccess) return hip_fail(ctx, e, "q8_graph_launch");
+  return ok(ctx);
+}
+
+void q8_graph_destroy(void *graph) {
+  if (!graph) return;
+  q8_graph *g = static_cast<q8_graph *>(graph);
+  if (g->exec) (void)hipGraphExecDestroy(g->exec);
+  if (g->graph) (void)hipGraphDestroy(g->graph);
+  delete g;
+}
+
+}  // extern "C"

@@ -1,0 +1,187 @@
+"""C ABI of libq8hip.so on the CPU: it loads, exports every symbol the header
+declares, and validates every argument before touching a device (a host-only
+context, Q8_DEVICE_NONE, returns Q8_ERR_NODEVICE only once the arguments are
+valid)."""
+
+import os
+import re
+
+import numpy as np
+import pytest
+
+from lama32_mojo_amd import q8, q8hip
+from lama32_mojo_amd.q8hip import (Q8_ERR_ARG, Q8_ERR_NODEVICE, Q8_ERR_RANGE, Q8_ERR_SHAPE,
+                                   Q8_SRC_BF16, Q8_SRC_F32, Q8Error)
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "q8hip.h")
+
+
+def declared_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(q8_\w+)\s*\(", text)))
+
+
+def test_header_symbols_exported():
+    lib = q8hip.lib()
+    names = declared_functions()
+    assert len(names) >= 20
+    for name in names:
+        assert hasattr(lib, name), name
+    assert set(names) == set(q8hip.SIGNATURES), set(names) ^ set(q8hip.SIGNATURES)
+
+
+def test_version_and_rowstride():
+    lib = q8hip.lib()
+    assert lib.q8_version() == 100
+    assert q8hip.rowstride_u16(2048) == 1056          # src/llama_q8.mojo:26-28
+    assert q8hip.rowstride_u16(14336) == 7392
+    assert q8hip.rowstride_u16(2048, 32, "f32") == 1152
+    assert lib.q8_rowstride_u16(100, 64, 1) == 0
+    assert lib.q8_rowstride_u16(2048, 48, 1) == 0
+    assert lib.q8_rowstride_u16(2048, 64, 3) == 0
+
+
+@pytest.fixture
+def hctx():
+    c = q8hip.Context(q8hip.Q8_DEVICE_NONE)
+    yield c
+    c.close()
+
+
+def code_of(fn, *args, **kw):
+    try:
+        fn(*args, **kw)
+    except Q8Error as e:
+        return e.code, e.msg
+    return 0, ""
+
+
+def test_linear_validation(hctx):
+    rs = q8hip.rowstride_u16(2048)
+    w = hctx.alloc(2 * (8 + 16 * rs))
+    a = hctx.alloc(4 * 10000)
+    L = q8hip.linear
+    # valid -> reaches the device step
+    assert code_of(L, hctx, w, 8, a, 0, 4096, 2, 2048, 16)[0] == Q8_ERR_NODEVICE
+    # m not a multiple of G
+    c, msg = code_of(L, hctx, w, 8, a, 0, 4096, 2, 2000, 16)
+    assert c == Q8_ERR_SHAPE and "multiple of G" in msg
+    # unsupported group size / scale dtype
+    assert code_of(L, hctx, w, 8, a, 0, 4096, 2, 2048, 16, G=48)[0] == Q8_ERR_ARG
+    assert code_of(L, hctx, w, 8, a, 0, 4096, 2, 2048, 16, scale=3)[0] == Q8_ERR_ARG
+    # negative sizes
+    assert code_of(L, hctx, w, 8, a, 0, 4096, -1, 2048, 16)[0] == Q8_ERR_SHAPE
+    assert code_of(L, hctx, w, 8, a, 0, 4096, 1, 2048, -16)[0] == Q8_ERR_SHAPE
+    # weights past the end of the weight buffer
+    assert code_of(L, hctx, w, 9, a, 0, 4096, 2, 2048, 16)[0] == Q8_ERR_RANGE
+    assert code_of(L, hctx, w, 8, a, 0, 4096, 2, 2048, 17)[0] == Q8_ERR_RANGE
+    # x / y past the end of the activation arena
+    assert code_of(L, hctx, w, 8, a, 6000, 0, 2, 2048, 16)[0] == Q8_ERR_RANGE
+    assert code_of(L, hctx, w, 8, a, 0, 9990, 2, 2048, 16)[0] == Q8_ERR_RANGE
+    # x and y overlap
+    assert code_of(L, hctx, w, 8, a, 0, 2048, 2, 2048, 16)[0] == Q8_ERR_ARG
+    # empty problems are valid no-ops
+    assert code_of(L, hctx, w, 8, a, 0, 4096, 0, 2048, 16)[0] == Q8_ERR_NODEVICE
+
+
+def test_linear_bf16act_validation(hctx):
+    rs = q8hip.rowstride_u16(1024, 32, "f32")
+    w = hctx.alloc(2 * 64 * rs)
+    x = hctx.alloc(2 * 512 * 1024)
+    y = hctx.alloc(4 * 512 * 64)
+    L = q8hip.linear_bf16act
+    assert code_of(L, hctx, w, 0, x, 0, y, 0, 512, 1024, 64, 32, "f32")[0] == Q8_ERR_NODEVICE
+    assert code_of(L, hctx, w, 0, x, 1, y, 0, 512, 1024, 64, 32, "f32")[0] == Q8_ERR_RANGE
+    assert code_of(L, hctx, w, 0, x, 0, y, 1, 512, 1024, 64, 32, "f32")[0] == Q8_ERR_RANGE
+    assert code_of(L, hctx, w, 0, x, 0, y, 0, 512, 1000, 64, 32, "f32")[0] == Q8_ERR_SHAPE
+
+
+def test_pack_validation(hctx):
+    n, m = 8, 256
+    rs = q8hip.rowstride_u16(m)
+    src = hctx.alloc(4 * n * m)
+    dst = hctx.alloc(2 * n * rs)
+    P = q8hip.quantize_pack
+    assert code_of(P, hctx, src, 0, Q8_SRC_F32, n, m, dst, 0)[0] == Q8_ERR_NODEVICE
+    assert code_of(P, hctx, src, 0, Q8_SRC_BF16, n, m, dst, 0)[0] == Q8_ERR_NODEVICE
+    assert code_of(P, hctx, src, 1, Q8_SRC_F32, n, m, dst, 0)[0] == Q8_ERR_RANGE
+    assert code_of(P, hctx, src, 0, Q8_SRC_F32, n, m, dst, 1)[0] == Q8_ERR_RANGE
+    assert code_of(P, hctx, src, 0, 7, n, m, dst, 0)[0] == Q8_ERR_ARG
+    assert code_of(P, hctx, src, 0, Q8_SRC_F32, n, 200, dst, 0)[0] == Q8_ERR_SHAPE
+    assert code_of(P, hctx, src, 0, Q8_SRC_F32, -1, m, dst, 0)[0] == Q8_ERR_SHAPE
+    # in-place packing would overwrite its own input
+    assert code_of(P, hctx, src, 0, Q8_SRC_F32, 2, m, src, 0)[0] == Q8_ERR_ARG
+
+
+def test_embed_validation(hctx):
+    d, vocab = 2048, 10
+    rs = q8hip.rowstride_u16(d)
+    w = hctx.alloc(2 * vocab * rs)
+    ids = hctx.alloc(4 * 4)
+    a = hctx.alloc(4 * 4 * d)
+    E = q8hip.embed_gather
+    assert code_of(E, hctx, w, 0, ids, 0, a, 0, 4, d, vocab)[0] == Q8_ERR_NODEVICE
+    assert code_of(E, hctx, w, 0, ids, 0, a, 0, 4, d, vocab + 1)[0] == Q8_ERR_RANGE
+    assert code_of(E, hctx, w, 0, ids, 1, a, 0, 4, d, vocab)[0] == Q8_ERR_RANGE
+    assert code_of(E, hctx, w, 0, ids, 0, a, 1, 4, d, vocab)[0] == Q8_ERR_RANGE
+    assert code_of(E, hctx, w, 0, ids, 0, a, 0, 4, 100, vocab)[0] == Q8_ERR_SHAPE
+
+
+def test_null_handles():
+    lib = q8hip.lib()
+    assert lib.q8_linear(None, None, 0, None, 0, 0, 1, 64, 1, 64, 1) == Q8_ERR_ARG
+    assert lib.q8_sync(None) == Q8_ERR_ARG
+    assert lib.q8_last_error(None) is not None
+
+
+def test_buffer_ranges(hctx):
+    b = hctx.alloc(64)
+    assert b.ptr == 0                      # host-only: sizes only
+    c, _ = code_of(b.upload, np.zeros(80, dtype=np.uint8))
+    assert c == Q8_ERR_RANGE
+    c, _ = code_of(b.upload, np.zeros(16, dtype=np.uint8), 60)
+    assert c == Q8_ERR_RANGE
+    c, _ = code_of(b.upload, np.zeros(16, dtype=np.uint8), 0)
+    assert c == Q8_ERR_NODEVICE
+
+
+def test_no_device_context_fails_cleanly():
+    import torch
+    if torch.cuda.device_count() > 0:
+        pytest.skip("a GPU is present")
+    with pytest.raises(Q8Error) as ei:
+        q8hip.Context(0)
+    assert ei.value.code == q8hip.Q8_ERR_HIP
+
+
+def test_acts_arena_semantics(hctx):
+    a = q8.Acts(hctx, 1000)
+    assert a.top == q8.PAD
+    o1 = a.alloc(100)
+    assert o1 == q8.PAD
+    mark = a.mark()
+    a.alloc(800)
+    with pytest.raises(RuntimeError, match="acts arena overflow"):
+        a.alloc(100)
+    a.reset(mark)
+    assert a.alloc(10) == mark
+
+
+def test_weights_arena_overflow(hctx):
+    w = q8.Weights(hctx, 100)
+    with pytest.raises(RuntimeError, match="weight arena overflow at big"):
+        w.upload_all({"big": np.zeros(80, dtype=np.uint16)}, ["big"])
+
+
+def test_mm_q8_op_allocates_output_then_validates(hctx):
+    rs = q8.q8_rowstride(2048)
+    w = q8.Weights(hctx, q8.PAD + 4 * rs)
+    a = q8.Acts(hctx, q8.PAD + 2048 + 4)
+    qk = q8.Q8Kernels(hctx)
+    ox = a.alloc(2048)
+    with pytest.raises(Q8Error) as ei:
+        q8.mm_q8_op(hctx, w, a, qk, ox, 1, 2048, q8.PAD, 4)
+    assert ei.value.code == Q8_ERR_NODEVICE
+    assert a.top == q8.PAD + 2048 + 4   # y was allocated, as mm_q8_op does

@@ -1,0 +1,325 @@
+"""GPU parity: libq8hip.so (through its C ABI) against the CPU oracle.
+
+Bars (written in each test):
+  * pack: codes and scales bit-exact (reference golden vectors and oracle);
+  * linear / GEMM: normwise max relative error  max|y - y*| / max|y*|
+    <= 1e-3 against the float64 closed form over the same codes, scales and
+    (bf16-rounded, for bf16 activations) inputs;
+  * one-hot inputs, fused-vs-separate calls and embedding gathers: bit-exact.
+"""
+
+import sys
+
+import numpy as np
+import pytest
+
+from lama32_mojo_amd import q8, q8hip
+from oracle.q8_oracle import (bf16_bits_to_f32, f32_to_bf16_bits, max_rel_err, rowstride_u16,
+                              synth_weights_bf16, synth_x, unpack_q8_np)
+
+pytestmark = pytest.mark.gpu
+TOL = 1e-3
+LAYOUTS = [(64, "f16"), (32, "f32")]
+
+
+def say(*a):
+    print(*a, flush=True)
+    sys.stdout.flush()
+
+
+def upload(ctx, arr):
+    arr = np.ascontiguousarray(arr)
+    b = ctx.alloc(max(arr.nbytes, 16))
+    b.upload(arr)
+    return b
+
+
+def gpu_linear(ctx, pk, x, G, scale, owt=0, pad_x=0):
+    """Run q8_linear on packed rows pk [n, rs] and x [s, m]; returns y [s, n]."""
+    n, rs = pk.shape
+    s, m = x.shape
+    wbuf = np.zeros(owt + n * rs, dtype=np.uint16)
+    wbuf[owt:] = pk.reshape(-1)
+    w = upload(ctx, wbuf)
+    ox = pad_x
+    oy = ox + s * m
+    a = ctx.alloc(4 * (oy + s * n))
+    a.upload(np.ascontiguousarray(x, dtype=np.float32), 4 * ox)
+    q8hip.linear(ctx, w, owt, a, ox, oy, s, m, n, G, scale)
+    y = a.download((s, n), np.float32, 4 * oy)
+    w.free()
+    a.free()
+    return y
+
+
+def gpu_linear_bf16(ctx, pk, xbits, G, scale):
+    n, rs = pk.shape
+    s, m = xbits.shape
+    w = upload(ctx, pk)
+    xb = upload(ctx, xbits)
+    yb = ctx.alloc(4 * s * n)
+    q8hip.linear_bf16act(ctx, w, 0, xb, 0, yb, 0, s, m, n, G, scale)
+    y = yb.download((s, n), np.float32)
+    for b in (w, xb, yb):
+        b.free()
+    return y
+
+
+# ---------------------------------------------------------------------------
+# quantize / pack
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("case", ["normal", "sweep", "edge", "tiny", "odd"])
+def test_pack_matches_reference_golden(ctx, golden, case):
+    say("pack golden", case)
+    wi, wo = golden[case + "_in"], golden[case + "_out"]
+    got = q8.pack_q8_bits(wi, 64, "f16", ctx)
+    assert np.array_equal(got, wo), np.argwhere(got != wo)[:5]
+
+
+@pytest.mark.parametrize("G,scale", LAYOUTS + [(32, "f16"), (64, "f32")])
+@pytest.mark.parametrize("src", ["bf16", "f32"])
+def test_pack_matches_oracle_llama_up_proj(ctx, cor, G, scale, src):
+    say("pack 8192x2048", G, scale, src)
+    wb = synth_weights_bf16(8192, 2048, seed=0)
+    if src == "bf16":
+        got = q8.pack_q8_bits(wb, G, scale, ctx)
+    else:
+        got = q8.pack_q8_bits(bf16_bits_to_f32(wb), G, scale, ctx, src_dtype="f32")
+    want = cor.pack_bf16(wb, G, scale)
+    assert np.array_equal(got, want)
+
+
+def test_pack_f32_wide_dynamic_range(ctx, cor):
+    """f32 inputs that are not bf16 values, spanning many binades."""
+    say("pack f32 wide range")
+    rng = np.random.default_rng(21)
+    w = (rng.standard_normal((257, 512)).astype(np.float32)
+         * np.exp(rng.uniform(-20, 12, (257, 1))).astype(np.float32))
+    for G, scale in LAYOUTS:
+        got = q8.pack_q8_bits(w, G, scale, ctx, src_dtype="f32")
+        assert np.array_equal(got, cor.pack_f32(w, G, scale))
+
+
+def test_pack_unaligned_offsets(ctx, cor):
+    """Odd source / destination offsets take the scalar load paths."""
+    say("pack unaligned")
+    n, m = 33, 192
+    wb = synth_weights_bf16(n, m, seed=22)
+    rs = rowstride_u16(m)
+    src = upload(ctx, np.concatenate([np.zeros(3, np.uint16), wb.reshape(-1)]))
+    dst = ctx.alloc(2 * (5 + n * rs))
+    q8hip.quantize_pack(ctx, src, 3, q8hip.Q8_SRC_BF16, n, m, dst, 5, 64, "f16")
+    got = dst.download((n, rs), np.uint16, 10)
+    assert np.array_equal(got, cor.pack_bf16(wb))
+    src.free()
+    dst.free()
+
+
+# ---------------------------------------------------------------------------
+# decode GEMV (q8_linear, small s)
+# ---------------------------------------------------------------------------
+
+SHAPES = [(8192, 2048), (3072, 2048), (2048, 8192), (1000, 1536), (1, 64), (7, 96)]
+
+
+@pytest.mark.parametrize("G,scale", LAYOUTS)
+@pytest.mark.parametrize("n,m", SHAPES)
+@pytest.mark.parametrize("s", [1, 2, 3, 4, 5, 16])
+def test_linear_matches_closed_form(ctx, cor, G, scale, n, m, s):
+    if m % G:
+        pytest.skip("m not a multiple of G")
+    say("linear", G, scale, n, m, s)
+    wb = synth_weights_bf16(n, m, seed=n + m)
+    pk = cor.pack_bf16(wb, G, scale)
+    x = synth_x(s, m, seed=s)
+    y = gpu_linear(ctx, pk, x, G, scale)
+    ref = cor.linear_f64(pk, x, G, scale)
+    err = max_rel_err(y, ref)
+    assert err <= TOL, err
+    assert err <= 1e-5, err      # fp32 accumulation is far inside the bar
+
+
+@pytest.mark.parametrize("G,scale", LAYOUTS)
+def test_linear_one_hot_exact(ctx, cor, G, scale):
+    say("linear one-hot", G, scale)
+    n, m = 512, 2048
+    pk = cor.pack_bf16(synth_weights_bf16(n, m, seed=31), G, scale)
+    codes, sc = unpack_q8_np(pk, m, G, scale)
+    for k in [0, 17, 1023, 1024, 2047]:
+        x = np.zeros((1, m), dtype=np.float32)
+        x[0, k] = 1.0
+        y = gpu_linear(ctx, pk, x, G, scale)
+        want = codes[:, k].astype(np.float32) * sc[:, k // G]
+        assert np.array_equal(y[0], want)
+
+
+def test_linear_zero_input(ctx, cor):
+    pk = cor.pack_bf16(synth_weights_bf16(300, 512, seed=32))
+    y = gpu_linear(ctx, pk, np.zeros((2, 512), np.float32), 64, "f16")
+    assert np.all(y == 0.0)
+
+
+@pytest.mark.parametrize("G,scale", LAYOUTS)
+def test_fused_qkv_equals_separate_calls(ctx, cor, G, scale):
+    """run_layer_q8 fuses q|k|v into one call over contiguous rows
+    (src/llama_q8.mojo:163-166); every output is independent, so the fused
+    result equals the separate calls bit for bit."""
+    say("fused qkv", G, scale)
+    H, QD, KVD = 2048, 2048, 512
+    rs = rowstride_u16(H, G, scale)
+    pk = cor.pack_bf16(synth_weights_bf16(QD + 2 * KVD, H, seed=33), G, scale)
+    w = upload(ctx, pk)
+    x = synth_x(1, H, seed=34)
+    a = ctx.alloc(4 * (H + 2 * (QD + 2 * KVD)))
+    a.upload(x)
+    q8hip.linear(ctx, w, 0, a, 0, H, 1, H, QD + 2 * KVD, G, scale)
+    o = H + QD + 2 * KVD
+    q8hip.linear(ctx, w, 0, a, 0, o, 1, H, QD, G, scale)
+    q8hip.linear(ctx, w, QD * rs, a, 0, o + QD, 1, H, KVD, G, scale)
+    q8hip.linear(ctx, w, (QD + KVD) * rs, a, 0, o + QD + KVD, 1, H, KVD, G, scale)
+    fused = a.download((QD + 2 * KVD,), np.float32, 4 * H)
+    sep = a.download((QD + 2 * KVD,), np.float32, 4 * o)
+    assert np.array_equal(fused, sep)
+    w.free()
+    a.free()
+
+
+@pytest.mark.parametrize("G,scale", LAYOUTS)
+def test_linear_unaligned_weights(ctx, cor, G, scale):
+    """A weight offset that is not 16-byte aligned takes the generic kernel."""
+    say("linear unaligned", G, scale)
+    n, m = 130, 512
+    pk = cor.pack_bf16(synth_weights_bf16(n, m, seed=35), G, scale)
+    x = synth_x(3, m, seed=36)
+    y = gpu_linear(ctx, pk, x, G, scale, owt=3, pad_x=1)
+    assert max_rel_err(y, cor.linear_f64(pk, x, G, scale)) <= TOL
+
+
+def test_linear_lm_head_full_size(ctx, cor):
+    """Llama-3.2-1B tied lm_head, 128256 x 2048, s = 1."""
+    say("lm_head full size")
+    n, m = 128256, 2048
+    pk = cor.pack_bf16(synth_weights_bf16(n, m, seed=37))
+    x = synth_x(1, m, seed=38)
+    y = gpu_linear(ctx, pk, x, 64, "f16")
+    ref = cor.linear_f64(pk, x)
+    assert max_rel_err(y, ref) <= TOL
+    assert np.argmax(y[0]) == np.argmax(ref[0])
+
+
+# ---------------------------------------------------------------------------
+# prefill GEMM (MFMA)
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("G,scale", LAYOUTS)
+@pytest.mark.parametrize("s,n,m", [(512, 2048, 2048), (512, 512, 2048), (512, 8192, 2048),
+                                   (512, 2048, 8192), (77, 200, 1024), (130, 96, 96),
+                                   (1, 64, 64)])
+def test_gemm_bf16act_matches_closed_form(ctx, cor, G, scale, s, n, m):
+    if m % G:
+        pytest.skip("m not a multiple of G")
+    say("gemm bf16", G, scale, s, n, m)
+    pk = cor.pack_bf16(synth_weights_bf16(n, m, seed=n + 3 * m), G, scale)
+    xbits = f32_to_bf16_bits(synth_x(s, m, seed=s + 1))
+    y = gpu_linear_bf16(ctx, pk, xbits, G, scale)
+    ref = cor.linear_f64(pk, bf16_bits_to_f32(xbits), G, scale)
+    err = max_rel_err(y, ref)
+    assert err <= TOL, err
+
+
+@pytest.mark.parametrize("G,scale", LAYOUTS)
+@pytest.mark.parametrize("s", [32, 64, 512])
+def test_gemm_f32act_matches_closed_form(ctx, cor, G, scale, s):
+    """q8_linear with many activation rows runs the MFMA GEMM on two bf16
+    terms of the f32 activations."""
+    say("gemm f32", G, scale, s)
+    n, m = 1024, 2048
+    pk = cor.pack_bf16(synth_weights_bf16(n, m, seed=41), G, scale)
+    x = synth_x(s, m, seed=42)
+    y = gpu_linear(ctx, pk, x, G, scale)
+    err = max_rel_err(y, cor.linear_f64(pk, x, G, scale))
+    assert err <= TOL, err
+    assert err <= 1e-4, err
+
+
+def test_gemm_bf16act_one_hot_exact(ctx, cor):
+    n, m, s = 256, 512, 64
+    pk = cor.pack_bf16(synth_weights_bf16(n, m, seed=43))
+    codes, sc = unpack_q8_np(pk, m)
+    ks = np.arange(s) * 7 % m
+    x = np.zeros((s, m), dtype=np.float32)
+    x[np.arange(s), ks] = 1.0
+    y = gpu_linear_bf16(ctx, pk, f32_to_bf16_bits(x), 64, "f16")
+    want = (codes[:, ks].astype(np.float32) * sc[:, ks // 64]).T
+    assert np.array_equal(y, want)
+
+
+# ---------------------------------------------------------------------------
+# embedding gather
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("G,scale", LAYOUTS)
+def test_embed_gather_exact(ctx, cor, G, scale):
+    say("embed", G, scale)
+    vocab, d = 1000, 2048
+    pk = cor.pack_bf16(synth_weights_bf16(vocab, d, seed=51), G, scale)
+    w = upload(ctx, pk)
+    ids = np.array([0, 999, 5, 5, 123, 7], dtype=np.int32)
+    ib = upload(ctx, ids)
+    a = ctx.alloc(4 * len(ids) * d)
+    q8hip.embed_gather(ctx, w, 0, ib, 0, a, 0, len(ids), d, vocab, G, scale)
+    got = a.download((len(ids), d), np.float32)
+    assert np.array_equal(got, cor.embed_gather(pk, ids, d, G, scale))
+    bad = upload(ctx, np.array([3, -1, vocab], dtype=np.int32))
+    q8hip.embed_gather(ctx, w, 0, bad, 0, a, 0, 3, d, vocab, G, scale)
+    got = a.download((3, d), np.float32)
+    assert np.array_equal(got[0], cor.embed_gather(pk, np.array([3], np.int32), d, G, scale)[0])
+    assert np.all(np.isnan(got[1:]))
+    for b in (w, ib, a, bad):
+        b.free()
+
+
+# ---------------------------------------------------------------------------
+# host mirror + graphs
+# ---------------------------------------------------------------------------
+
+def test_mm_q8_op_and_graph_replay(ctx, cor):
+    """mm_q8_op through the arenas, captured in a HIP graph and replayed with
+    new inputs written eagerly between replays; every replay matches the
+    eager result."""
+    say("graph replay")
+    H, N = 2048, 3072
+    pk = cor.pack_bf16(synth_weights_bf16(N, H, seed=61))
+    w = q8.Weights(ctx, q8.PAD + pk.size)
+    w.upload_all({"wq": pk}, ["wq"])
+    a = q8.Acts(ctx, q8.PAD + H + 2 * N + 64)
+    qk = q8.Q8Kernels(ctx)
+    ox = a.alloc(H)
+    ctx.graph_begin()
+    oy = q8.mm_q8_op(ctx, w, a, qk, ox, 1, H, w.o("wq"), N)
+    g = ctx.graph_end()
+    for rep in range(4):
+        x = synth_x(1, H, seed=70 + rep)
+        a.write(ox, x)
+        g.launch()
+        ctx.sync()
+        got = a.read(oy, N)
+        emark = a.mark()
+        oe = q8.mm_q8_op(ctx, w, a, qk, ox, 1, H, w.o("wq"), N)
+        ctx.sync()
+        eager = a.read(oe, N)
+        a.reset(emark)
+        assert oe != oy
+        assert np.array_equal(got, eager)
+        assert max_rel_err(got, cor.linear_f64(pk, x)[0]) <= TOL
+    g.destroy()
+
+
+def test_pack_q8_torch_signature(ctx, golden):
+    import torch
+    wi, wo = golden["normal_in"], golden["normal_out"]
+    t = torch.from_numpy(wi.view(np.int16).copy()).view(torch.bfloat16)
+    out = q8.pack_q8(t, ctx=ctx)
+    assert out.dtype == torch.float16 and tuple(out.shape) == wo.shape
+    assert np.array_equal(out.numpy().view(np.uint16), wo)
