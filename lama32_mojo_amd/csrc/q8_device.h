@@ -56,6 +56,27 @@ __device__ __forceinline__ float sbyte_to_f32(uint32_t w) {
   return (float)(int32_t)((int32_t)(w << (24 - 8 * I)) >> 24);
 }
 
+// Unscaled dot product of 16 signed codes (one dwordx4) with 16 f32 values.
+__device__ __forceinline__ float dot16(u32x4 q, f32x4 xa, f32x4 xb, f32x4 xc, f32x4 xd) {
+  float p = xa.x * sbyte_to_f32<0>(q.x);
+  p = __builtin_fmaf(xa.y, sbyte_to_f32<1>(q.x), p);
+  p = __builtin_fmaf(xa.z, sbyte_to_f32<2>(q.x), p);
+  p = __builtin_fmaf(xa.w, sbyte_to_f32<3>(q.x), p);
+  p = __builtin_fmaf(xb.x, sbyte_to_f32<0>(q.y), p);
+  p = __builtin_fmaf(xb.y, sbyte_to_f32<1>(q.y), p);
+  p = __builtin_fmaf(xb.z, sbyte_to_f32<2>(q.y), p);
+  p = __builtin_fmaf(xb.w, sbyte_to_f32<3>(q.y), p);
+  p = __builtin_fmaf(xc.x, sbyte_to_f32<0>(q.z), p);
+  p = __builtin_fmaf(xc.y, sbyte_to_f32<1>(q.z), p);
+  p = __builtin_fmaf(xc.z, sbyte_to_f32<2>(q.z), p);
+  p = __builtin_fmaf(xc.w, sbyte_to_f32<3>(q.z), p);
+  p = __builtin_fmaf(xd.x, sbyte_to_f32<0>(q.w), p);
+  p = __builtin_fmaf(xd.y, sbyte_to_f32<1>(q.w), p);
+  p = __builtin_fmaf(xd.z, sbyte_to_f32<2>(q.w), p);
+  p = __builtin_fmaf(xd.w, sbyte_to_f32<3>(q.w), p);
+  return p;
+}
+
 // ---- wavefront reductions (wave64) --------------------------------------
 // DPP row operations reduce within each row of 16 lanes; the four row sums
 // are then combined with readlane.  Every lane returns the full sum.

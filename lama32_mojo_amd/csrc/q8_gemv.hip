@@ -6,9 +6,11 @@
 //
 // The kernel is HBM-bound: every weight byte is read exactly once.  Layout
 // and mapping:
-//   * a wavefront owns R whole rows at a time; lane l owns the 16-byte code
-//     slices k = 16 l + 1024 i of every row, so each load instruction is one
-//     1 KiB fully coalesced run per row (global_load_dwordx4, non-temporal);
+//   * a wavefront owns R whole rows at a time (or, for rows longer than 4096
+//     codes, one K quarter of R rows shared by the workgroup's 4 waves); lane
+//     l owns the 16-byte code slices k = 16 l + 1024 i, so each load
+//     instruction is one 1 KiB fully coalesced run per row
+//     (global_load_dwordx4, non-temporal);
 //   * the R rows' loads are issued together, so a wave keeps R KiB in flight
 //     per step and many waves per CU cover HBM latency;
 //   * the lane's 16 codes lie inside one quantization group (16 | G), so one
@@ -30,15 +32,21 @@ namespace {
 constexpr int kWaves = 4;               // wavefronts per workgroup
 constexpr int kLdsFloats = 16384;       // x staged in LDS up to 64 KiB
 
-template <int G, int KIND, int S, int R, bool XLDS>
+template <int G, int KIND, int S, int R, int SPLITK, bool XLDS>
 __global__ __launch_bounds__(256) void gemv_kernel(
     const uint8_t *__restrict__ w, int64_t row_bytes, int64_t n,
     const float *__restrict__ x, int64_t m, float *__restrict__ y) {
   extern __shared__ float xs[];
+  __shared__ float part[SPLITK > 1 ? SPLITK : 1][R][S];
   constexpr int SB = ScaleTraits<KIND>::bytes;
   const int lane = threadIdx.x & 63;
   const int wid = threadIdx.x >> 6;
   const int64_t scale_bytes = (m / G) * SB;
+  // SPLITK == 1: each wave owns R rows over the whole K range.
+  // SPLITK == 4: the 4 waves of a workgroup share R rows, wave w owning the
+  // K range [w m/4, (w+1) m/4); partial sums meet in LDS.
+  const int64_t k_lo = SPLITK > 1 ? wid * (m / SPLITK) : 0;
+  const int64_t k_hi = SPLITK > 1 ? k_lo + m / SPLITK : m;
 
   const float *xp = x;
   if constexpr (XLDS) {
@@ -49,8 +57,10 @@ __global__ __launch_bounds__(256) void gemv_kernel(
     xp = xs;
   }
 
-  const int64_t stride_rows = (int64_t)gridDim.x * kWaves * R;
-  for (int64_t r0 = ((int64_t)blockIdx.x * kWaves + wid) * R; r0 < n; r0 += stride_rows) {
+  const int64_t rows_per_group = SPLITK > 1 ? R : (int64_t)kWaves * R;
+  const int64_t stride_rows = (int64_t)gridDim.x * rows_per_group;
+  int64_t r0 = (int64_t)blockIdx.x * rows_per_group + (SPLITK > 1 ? 0 : wid * R);
+  for (; r0 < n; r0 += stride_rows) {
     float acc[R][S];
 #pragma unroll
     for (int r = 0; r < R; ++r)
@@ -64,7 +74,7 @@ __global__ __launch_bounds__(256) void gemv_kernel(
       rowp[r] = w + j * row_bytes;
     }
 
-    for (int64_t k = 16 * lane; k < m; k += 1024) {
+    for (int64_t k = k_lo + 16 * lane; k < k_hi; k += 1024) {
       u32x4 q[R];
       float sc[R];
 #pragma unroll
@@ -78,35 +88,37 @@ __global__ __launch_bounds__(256) void gemv_kernel(
         const f32x4 *xv4 = reinterpret_cast<const f32x4 *>(xp + b * m + k);
         f32x4 xa = xv4[0], xb = xv4[1], xc = xv4[2], xd = xv4[3];
 #pragma unroll
-        for (int r = 0; r < R; ++r) {
-          float p = xa.x * sbyte_to_f32<0>(q[r].x);
-          p = __builtin_fmaf(xa.y, sbyte_to_f32<1>(q[r].x), p);
-          p = __builtin_fmaf(xa.z, sbyte_to_f32<2>(q[r].x), p);
-          p = __builtin_fmaf(xa.w, sbyte_to_f32<3>(q[r].x), p);
-          p = __builtin_fmaf(xb.x, sbyte_to_f32<0>(q[r].y), p);
-          p = __builtin_fmaf(xb.y, sbyte_to_f32<1>(q[r].y), p);
-          p = __builtin_fmaf(xb.z, sbyte_to_f32<2>(q[r].y), p);
-          p = __builtin_fmaf(xb.w, sbyte_to_f32<3>(q[r].y), p);
-          p = __builtin_fmaf(xc.x, sbyte_to_f32<0>(q[r].z), p);
-          p = __builtin_fmaf(xc.y, sbyte_to_f32<1>(q[r].z), p);
-          p = __builtin_fmaf(xc.z, sbyte_to_f32<2>(q[r].z), p);
-          p = __builtin_fmaf(xc.w, sbyte_to_f32<3>(q[r].z), p);
-          p = __builtin_fmaf(xd.x, sbyte_to_f32<0>(q[r].w), p);
-          p = __builtin_fmaf(xd.y, sbyte_to_f32<1>(q[r].w), p);
-          p = __builtin_fmaf(xd.z, sbyte_to_f32<2>(q[r].w), p);
-          p = __builtin_fmaf(xd.w, sbyte_to_f32<3>(q[r].w), p);
-          acc[r][b] = __builtin_fmaf(sc[r], p, acc[r][b]);
-        }
+        for (int r = 0; r < R; ++r)
+          acc[r][b] = __builtin_fmaf(sc[r], dot16(q[r], xa, xb, xc, xd), acc[r][b]);
       }
     }
 
+    if constexpr (SPLITK == 1) {
 #pragma unroll
-    for (int r = 0; r < R; ++r)
+      for (int r = 0; r < R; ++r)
 #pragma unroll
-      for (int b = 0; b < S; ++b) {
-        float v = wave_sum(acc[r][b]);
-        if (lane == 0 && r0 + r < n) y[b * n + r0 + r] = v;
+        for (int b = 0; b < S; ++b) {
+          float v = wave_sum(acc[r][b]);
+          if (lane == 0 && r0 + r < n) y[b * n + r0 + r] = v;
+        }
+    } else {
+#pragma unroll
+      for (int r = 0; r < R; ++r)
+#pragma unroll
+        for (int b = 0; b < S; ++b) {
+          float v = wave_sum(acc[r][b]);
+          if (lane == 0) part[wid][r][b] = v;
+        }
+      __syncthreads();
+      if (threadIdx.x < R * S) {
+        const int r = threadIdx.x / S, b = threadIdx.x % S;
+        float v = part[0][r][b];
+#pragma unroll
+        for (int u = 1; u < SPLITK; ++u) v += part[u][r][b];
+        if (r0 + r < n) y[b * n + r0 + r] = v;
       }
+      __syncthreads();
+    }
   }
 }
 
@@ -144,34 +156,38 @@ __global__ __launch_bounds__(256) void gemv_generic_kernel(
   }
 }
 
-int grid_for(int64_t tiles) {
-  // Enough workgroups to give every CU several, capped so large matrices
-  // stride over tiles instead of launching millions of workgroups.
-  const int64_t cap = 256 * 16;
+int grid_for(int64_t tiles, int64_t cap) {
   return (int)(tiles < cap ? (tiles > 0 ? tiles : 1) : cap);
 }
 
-template <int G, int KIND, int S, int R>
-hipError_t launch_fast(const LinearArgs &a, const float *x, float *y, hipStream_t st) {
-  const int64_t tiles = (a.n + kWaves * R - 1) / (kWaves * R);
-  dim3 grid(grid_for(tiles)), block(256);
-  if (S * a.m <= kLdsFloats && reinterpret_cast<uintptr_t>(x) % 16 == 0) {
+template <int G, int KIND, int S, int R, int SPLITK>
+hipError_t launch_fast(const LinearArgs &a, const float *x, float *y, int64_t cap,
+                       hipStream_t st) {
+  const int64_t rows_per_group = SPLITK > 1 ? R : kWaves * R;
+  const int64_t tiles = (a.n + rows_per_group - 1) / rows_per_group;
+  dim3 grid(grid_for(tiles, cap)), block(256);
+  if (S * a.m <= kLdsFloats) {
     size_t lds = (size_t)S * a.m * sizeof(float);
-    hipLaunchKernelGGL((gemv_kernel<G, KIND, S, R, true>), grid, block, lds, st,
+    hipLaunchKernelGGL((gemv_kernel<G, KIND, S, R, SPLITK, true>), grid, block, lds, st,
                        a.w, a.row_bytes, a.n, x, a.m, y);
   } else {
-    hipLaunchKernelGGL((gemv_kernel<G, KIND, S, R, false>), grid, block, 0, st,
+    hipLaunchKernelGGL((gemv_kernel<G, KIND, S, R, SPLITK, false>), grid, block, 0, st,
                        a.w, a.row_bytes, a.n, x, a.m, y);
   }
   return hipGetLastError();
 }
 
+// Shape classes (tuned on MI355X, decode shapes of Llama-3.2-1B / Qwen3-8B):
+//   long rows (m > 4096):         K split over the 4 waves, 4 rows per workgroup
+//   vocabulary heads (n >= 64K):  2 rows per wave, up to 8192 workgroups
+//   wide (n >= 8192):             4 rows per wave, up to 1024 workgroups
+//   small:                        1 row per wave
 template <int G, int KIND, int S>
 hipError_t launch_rows(const LinearArgs &a, const float *x, float *y, hipStream_t st) {
-  // Fewer rows per wave when n is small so the grid still covers the chip.
-  if (a.n >= 256 * kWaves * 4) return launch_fast<G, KIND, S, 4>(a, x, y, st);
-  if (a.n >= 256 * kWaves * 2) return launch_fast<G, KIND, S, 2>(a, x, y, st);
-  return launch_fast<G, KIND, S, 1>(a, x, y, st);
+  if (a.m > 4096 && a.m % 64 == 0) return launch_fast<G, KIND, S, 4, 4>(a, x, y, 1024, st);
+  if (a.n >= 65536) return launch_fast<G, KIND, S, 2, 1>(a, x, y, 8192, st);
+  if (a.n >= 8192) return launch_fast<G, KIND, S, 4, 1>(a, x, y, 1024, st);
+  return launch_fast<G, KIND, S, 1, 1>(a, x, y, 4096, st);
 }
 
 template <int G, int KIND>
@@ -183,7 +199,7 @@ hipError_t launch_g(const LinearArgs &a, hipStream_t st) {
                        reinterpret_cast<uintptr_t>(x) % 16 == 0;
   if (!aligned) {
     const int64_t tasks = a.s * a.n;
-    dim3 grid(grid_for((tasks + kWaves - 1) / kWaves)), block(256);
+    dim3 grid(grid_for((tasks + kWaves - 1) / kWaves, 4096)), block(256);
     if (a.x_is_bf16)
       hipLaunchKernelGGL((gemv_generic_kernel<G, KIND, true>), grid, block, 0, st,
                          a.w, a.row_bytes, a.n, a.x, a.s, a.m, a.y);
