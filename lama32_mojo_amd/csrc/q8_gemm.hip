@@ -101,7 +101,12 @@ template <> struct SlotScale<32, SCALE_F32> {
 template <int G, int KIND, bool XF32, int BM, int PB, int PA>
 __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void gemm_kernel(const uint8_t *__restrict__ w, int64_t row_bytes, const void *__restrict__ xv,
-                 float *__restrict__ y, int64_t s, int64_t m, int64_t n, int nit) {
+                 float *__restrict__ y, int64_t s, int64_t m, int64_t n, int nit,
+                 float *__restrict__ ws) {
+  // blockIdx.z selects a K range of nit iterations (split-K): with
+  // gridDim.z == 1 y is written directly, otherwise split z writes its
+  // partial sums to ws[z] and splitk_reduce_kernel adds them up.
+  const int it0 = (int)blockIdx.z * nit;
   constexpr int SB = ScaleTraits<KIND>::bytes;
   constexpr int TM = BM / 32;                 // 32-row MFMA tiles per wave
   constexpr int AU = BM * KT / 8 / NT;        // activation chunks (8 elements) per thread
@@ -116,9 +121,16 @@ void gemm_kernel(const uint8_t *__restrict__ w, int64_t row_bytes, const void *_
   const int lr = lane & 31, lh = lane >> 5;
   const int64_t m0 = (int64_t)blockIdx.y * BM;
   const int64_t col = (int64_t)blockIdx.x * BN + p * 32 + lr;
-  const uint8_t *wrow = w + (col < n ? col : n - 1) * row_bytes;   // clamped: loads stay in bounds
-  const int64_t scale_bytes = (m / G) * SB;
-  const int64_t nslot = (m + 63) / 64;
+  const uint8_t *wrow0 = w + (col < n ? col : n - 1) * row_bytes;   // clamped: loads stay in bounds
+  // Everything below is relative to this split's first K slot: codes and
+  // scales are addressed from shifted row pointers, activations from a
+  // shifted column, and mk / nslot / ngroups count what is left of the row.
+  const int64_t kbase = (int64_t)it0 * KT;
+  const uint8_t *codes = wrow0 + (m / G) * SB + kbase;
+  const uint8_t *wrow = wrow0 + (2 * (int64_t)it0) * (64 / G) * SB;
+  const int64_t mk = m - kbase;
+  const int64_t nslot = (mk + 63) / 64;
+  const int64_t ngroups = m / G - 2 * (int64_t)it0 * (64 / G);
 
   // activation chunk coordinates (iteration-independent rows)
   int64_t arow[AU];
@@ -152,14 +164,14 @@ void gemm_kernel(const uint8_t *__restrict__ w, int64_t row_bytes, const void *_
   const int chunk0 = G == 64 ? 32 * lh : 16 * lh;
   const int chunk1 = G == 64 ? 32 * lh + 16 : 32 + 16 * lh;
   auto load_b = [&](u32x4 (&q)[2], typename SS::raw &r, int it) {
-    int64_t slot = 2 * (int64_t)it + h;
-    slot = slot < nslot ? slot : nslot - 1;
+    int slot = 2 * it + h;
+    slot = slot < nslot ? slot : (int)nslot - 1;
     // the last slot of a G=32 row may hold only 32 codes: never read past the row
-    int64_t o0 = slot * 64 + chunk0, o1 = slot * 64 + chunk1;
-    o0 = o0 + 16 <= m ? o0 : m - 16;
-    o1 = o1 + 16 <= m ? o1 : m - 16;
-    q[0] = *reinterpret_cast<const u32x4 *>(wrow + scale_bytes + o0);
-    q[1] = *reinterpret_cast<const u32x4 *>(wrow + scale_bytes + o1);
+    int o0 = slot * 64 + chunk0, o1 = slot * 64 + chunk1;
+    o0 = o0 + 16 <= mk ? o0 : (int)mk - 16;
+    o1 = o1 + 16 <= mk ? o1 : (int)mk - 16;
+    q[0] = *reinterpret_cast<const u32x4 *>(codes + o0);
+    q[1] = *reinterpret_cast<const u32x4 *>(codes + o1);
     // reads the slot's scale(s); a missing second G=32 scale reads the first
     // code bytes of the row (in bounds) and is replaced by 0 below
     r = SS::load(wrow, slot);
@@ -167,13 +179,13 @@ void gemm_kernel(const uint8_t *__restrict__ w, int64_t row_bytes, const void *_
   auto load_a = [&](u32x4 *dst, int it) {
 #pragma unroll
     for (int u = 0; u < AU; ++u) {
-      int64_t k = (int64_t)it * KT + akc[u];
-      k = k < m ? k : m - 8;
+      int k = it * KT + akc[u];
+      k = k < mk ? k : (int)mk - 8;
       if constexpr (!XF32) {
-        const uint16_t *x = reinterpret_cast<const uint16_t *>(xv);
+        const uint16_t *x = reinterpret_cast<const uint16_t *>(xv) + kbase;
         dst[u] = *reinterpret_cast<const u32x4 *>(x + arow[u] * m + k);
       } else {
-        const float *x = reinterpret_cast<const float *>(xv);
+        const float *x = reinterpret_cast<const float *>(xv) + kbase;
         const u32x4 *pp = reinterpret_cast<const u32x4 *>(x + arow[u] * m + k);
         dst[2 * u] = pp[0];
         dst[2 * u + 1] = pp[1];
@@ -185,7 +197,7 @@ void gemm_kernel(const uint8_t *__restrict__ w, int64_t row_bytes, const void *_
     for (int u = 0; u < AU; ++u) {
       const int c = tid + NT * u;
       const int row = c / (KT / 8);
-      const bool ok = arow_ok[u] && (int64_t)it * KT + akc[u] < m;
+      const bool ok = arow_ok[u] && it * KT + akc[u] < mk;
       if constexpr (!XF32) {
         const u32x4 v = ok ? src[u] : u32x4{0u, 0u, 0u, 0u};
         *reinterpret_cast<u32x4 *>(&As[buf][0][row * LDA + akc[u]]) = v;
@@ -233,10 +245,10 @@ void gemm_kernel(const uint8_t *__restrict__ w, int64_t row_bytes, const void *_
       bf[3] = codes_to_bf16(qb[bs][1].z, qb[bs][1].w);
       // a slot beyond the last real one carries zero activations; its scale
       // is forced to 0 as well (its codes are a clamped re-read)
-      const int64_t slot = 2 * (int64_t)it + h;
+      const int slot = 2 * it + h;
       const bool live = slot < nslot;
       const float sc0 = live ? SS::get(sr[bs], 0) : 0.0f;
-      const float sc1 = (G == 32 && 2 * slot + 1 < m / G) ? SS::get(sr[bs], 1) : 0.0f;
+      const float sc1 = (G == 32 && 2 * slot + 1 < ngroups) ? SS::get(sr[bs], 1) : 0.0f;
       load_b(qb[bs], sr[bs], it + PB < nit ? it + PB : nit - 1);
 
       const uint16_t *A0 = As[buf][0];
@@ -244,45 +256,44 @@ void gemm_kernel(const uint8_t *__restrict__ w, int64_t row_bytes, const void *_
       auto acol = [&](int t) {
         return 64 * h + (G == 64 ? 32 * lh + 8 * t : 32 * (t >> 1) + 16 * lh + 8 * (t & 1));
       };
-      f32x16 tmp[TM];
-      bf16x8_t af[2][TM], al[2][TM];
+      // The TM row tiles of a group run as TM / TH passes of TH independent
+      // MFMA chains: TH = 2 keeps the per-group temporaries at 32 VGPRs so
+      // 128-row tiles fit the 256-VGPR budget of two waves per SIMD.
+      constexpr int TH = TM < 2 ? TM : 2;
 #pragma unroll
-      for (int i = 0; i < TM; ++i) {
-        af[0][i] = *reinterpret_cast<const bf16x8_t *>(&A0[(i * 32 + lr) * LDA + acol(0)]);
-        if constexpr (XF32)
-          al[0][i] = *reinterpret_cast<const bf16x8_t *>(&As[buf][XF32 ? 1 : 0][(i * 32 + lr) * LDA + acol(0)]);
-      }
+      for (int i0 = 0; i0 < TM; i0 += TH) {
+        f32x16 tmp[TH];
 #pragma unroll
-      for (int t = 0; t < 4; ++t) {
-        if (t < 3) {
+        for (int t = 0; t < 4; ++t) {
+          bf16x8_t af[TH], al[TH];
 #pragma unroll
-          for (int i = 0; i < TM; ++i) {
-            af[(t + 1) & 1][i] = *reinterpret_cast<const bf16x8_t *>(
-                &A0[(i * 32 + lr) * LDA + acol(t + 1)]);
+          for (int ii = 0; ii < TH; ++ii) {
+            af[ii] = *reinterpret_cast<const bf16x8_t *>(&A0[((i0 + ii) * 32 + lr) * LDA + acol(t)]);
             if constexpr (XF32)
-              al[(t + 1) & 1][i] = *reinterpret_cast<const bf16x8_t *>(
-                  &As[buf][XF32 ? 1 : 0][(i * 32 + lr) * LDA + acol(t + 1)]);
+              al[ii] = *reinterpret_cast<const bf16x8_t *>(
+                  &As[buf][XF32 ? 1 : 0][((i0 + ii) * 32 + lr) * LDA + acol(t)]);
           }
-        }
-        // G=64: one group over t = 0..3; G=32: groups t = 0..1 and 2..3
-        const bool fresh = (t == 0) || (G == 32 && t == 2);
+          // G=64: one group over t = 0..3; G=32: groups t = 0..1 and 2..3
+          const bool fresh = (t == 0) || (G == 32 && t == 2);
 #pragma unroll
-        for (int i = 0; i < TM; ++i) {
-          if (fresh) {
-            const f32x16 z = {};
-            tmp[i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[t & 1][i], bf[t], z, 0, 0, 0);
-          } else {
-            tmp[i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[t & 1][i], bf[t], tmp[i], 0, 0, 0);
+          for (int ii = 0; ii < TH; ++ii) {
+            if (fresh) {
+              const f32x16 z = {};
+              tmp[ii] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[ii], bf[t], z, 0, 0, 0);
+            } else {
+              tmp[ii] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[ii], bf[t], tmp[ii], 0, 0, 0);
+            }
+            if constexpr (XF32)
+              tmp[ii] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(al[ii], bf[t], tmp[ii], 0, 0, 0);
           }
-          if constexpr (XF32)
-            tmp[i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(al[t & 1][i], bf[t], tmp[i], 0, 0, 0);
-        }
-        if ((G == 32 && t == 1) || t == 3) {
-          const float sc = (G == 32 && t == 1) ? sc0 : (G == 32 ? sc1 : sc0);
+          if ((G == 32 && t == 1) || t == 3) {
+            const float sc = (G == 32 && t == 1) ? sc0 : (G == 32 ? sc1 : sc0);
 #pragma unroll
-          for (int i = 0; i < TM; ++i)
+            for (int ii = 0; ii < TH; ++ii)
 #pragma unroll
-            for (int v = 0; v < 16; ++v) acc[i][v] = __builtin_fmaf(sc, tmp[i][v], acc[i][v]);
+              for (int v = 0; v < 16; ++v)
+                acc[i0 + ii][v] = __builtin_fmaf(sc, tmp[ii][v], acc[i0 + ii][v]);
+          }
         }
       }
       store_a(ra[(j + 1) % PA], buf ^ 1, it + 1);
@@ -302,16 +313,39 @@ void gemm_kernel(const uint8_t *__restrict__ w, int64_t row_bytes, const void *_
       for (int v = 0; v < 16; ++v) red[((p * TM + i) * 16 + v) * 64 + lane] = acc[i][v];
   }
   __syncthreads();
+  const int splits = (int)gridDim.z;
   if (h == 0 && col < n) {
     // D layout of v_mfma_f32_32x32x16: lane -> column lane % 32,
     // element v -> row 8 (v / 4) + 4 (lane / 32) + v % 4.
+    float *out = (splits == 1 ? y : ws + (int64_t)blockIdx.z * s * n) + (m0 + lh * 4) * n + col;
+    const int rows_left = (int)(s - m0 - lh * 4);
 #pragma unroll
     for (int i = 0; i < TM; ++i)
 #pragma unroll
       for (int v = 0; v < 16; ++v) {
-        const int64_t row = m0 + i * 32 + (v >> 2) * 8 + lh * 4 + (v & 3);
-        if (row < s) y[row * n + col] = acc[i][v] + red[((p * TM + i) * 16 + v) * 64 + lane];
+        const int r = i * 32 + (v >> 2) * 8 + (v & 3);
+        if (r < rows_left)
+          out[(int64_t)r * n] = acc[i][v] + red[((p * TM + i) * 16 + v) * 64 + lane];
       }
+  }
+}
+
+// y[i] = sum over splits z (in order) of ws[z][i]; four outputs per thread.
+__global__ __launch_bounds__(256) void splitk_reduce_kernel(const float *__restrict__ ws,
+                                                            float *__restrict__ y, int64_t count,
+                                                            int splits) {
+  const int64_t i = 4 * ((int64_t)blockIdx.x * blockDim.x + threadIdx.x);
+  if (i >= count) return;
+  if (i + 4 <= count && (count & 3) == 0) {
+    f32x4 v = *reinterpret_cast<const f32x4 *>(ws + i);
+    for (int z = 1; z < splits; ++z) v += *reinterpret_cast<const f32x4 *>(ws + z * count + i);
+    *reinterpret_cast<f32x4 *>(y + i) = v;
+  } else {
+    for (int64_t e = i; e < i + 4 && e < count; ++e) {
+      float v = ws[e];
+      for (int z = 1; z < splits; ++z) v += ws[z * count + e];
+      y[e] = v;
+    }
   }
 }
 
@@ -319,22 +353,34 @@ template <int G, int KIND, bool XF32, int BM>
 hipError_t launch_bm(const LinearArgs &a, hipStream_t st) {
   constexpr int PB = 2, PA = 2, P = 2;
   const int64_t nslot = (a.m + 63) / 64;
-  int64_t nit = (nslot + 1) / 2;
+  const int64_t nit_all = (nslot + 1) / 2;
+  const int64_t gx = (a.n + BN - 1) / BN, gy = (a.s + BM - 1) / BM;
+  // Split K when the output tiles alone leave CUs idle (256 CUs, one 8-wave
+  // workgroup each); every split keeps at least 2 periods of iterations.
+  int64_t splits = 1;
+  if (a.ws) {
+    while (gx * gy * splits * 2 <= 256 && (nit_all + 2 * splits - 1) / (2 * splits) >= 2 * P &&
+           2 * splits * a.s * a.n <= a.ws_floats)
+      splits *= 2;
+  }
+  int64_t nit = (nit_all + splits - 1) / splits;
   nit = (nit + P - 1) / P * P;
-  dim3 grid((unsigned)((a.n + BN - 1) / BN), (unsigned)((a.s + BM - 1) / BM)), block(NT);
+  dim3 grid((unsigned)gx, (unsigned)gy, (unsigned)splits), block(NT);
   hipLaunchKernelGGL((gemm_kernel<G, KIND, XF32, BM, PB, PA>), grid, block, 0, st, a.w,
-                     a.row_bytes, a.x, a.y, a.s, a.m, a.n, (int)nit);
+                     a.row_bytes, a.x, a.y, a.s, a.m, a.n, (int)nit, a.ws);
+  if (splits > 1) {
+    const int64_t count = a.s * a.n;
+    const int64_t threads = (count + 3) / 4;
+    hipLaunchKernelGGL(splitk_reduce_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0,
+                       st, a.ws, a.y, count, (int)splits);
+  }
   return hipGetLastError();
 }
 
 template <int G, int KIND, bool XF32>
 hipError_t launch_x(const LinearArgs &a, hipStream_t st) {
-  // 128-row tiles when they alone fill the chip; 64-row tiles otherwise
-  // (and always for the two-term f32 path, whose extra operands would spill).
-  const int64_t tiles128 = ((a.n + BN - 1) / BN) * ((a.s + 127) / 128);
-  if constexpr (!XF32) {
-    if (tiles128 >= 256) return launch_bm<G, KIND, XF32, 128>(a, st);
-  }
+  // 64-row tiles: the largest that run two waves per SIMD without register
+  // spills; grids with few tiles are widened by splitting K.
   return launch_bm<G, KIND, XF32, 64>(a, st);
 }
 

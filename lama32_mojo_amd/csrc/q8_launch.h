@@ -28,6 +28,10 @@ struct LinearArgs {
   float *y;              // outputs [s, n] f32, row stride n
   int64_t s, m, n;
   int G, kind;
+  // Split-K workspace for the GEMM (null: no split): room for ws_floats
+  // partial sums.
+  float *ws = nullptr;
+  int64_t ws_floats = 0;
 };
 // Decode path (s small, f32 x): VALU GEMV.
 hipError_t launch_gemv(const LinearArgs &a, hipStream_t st);

@@ -23,7 +23,15 @@ struct q8_ctx {
   hipStream_t own = nullptr;
   hipStream_t stream = nullptr;
   std::string err;
+  // Split-K workspace of the prefill GEMM (partial sums).  A split only
+  // happens while tiles x splits stay within 256 workgroups of 64 x 128
+  // outputs, so 2 Mi floats always suffice; 4 Mi leaves room.
+  float *gemm_ws = nullptr;
 };
+
+namespace {
+constexpr int64_t kGemmWsFloats = (int64_t)4 << 20;
+}
 
 struct q8_buf {
   void *ptr = nullptr;
@@ -135,6 +143,13 @@ int q8_create(int device_ordinal, q8_ctx **out) {
       return fail(nullptr, Q8_ERR_HIP, "q8_create: %s", hipGetErrorString(e));
     }
     ctx->stream = ctx->own;
+    // Split-K workspace of the prefill GEMM, allocated up front so that
+    // calls captured into HIP graphs can use it too.
+    if (hipMalloc(&ctx->gemm_ws, kGemmWsFloats * sizeof(float)) != hipSuccess) {
+      (void)hipStreamDestroy(ctx->own);
+      delete ctx;
+      return fail(nullptr, Q8_ERR_NOMEM, "q8_create: cannot allocate the GEMM workspace");
+    }
   }
   *out = ctx;
   return Q8_OK;
@@ -148,6 +163,7 @@ void q8_destroy(q8_ctx *ctx) {
       (void)hipStreamSynchronize(ctx->own);
       (void)hipStreamDestroy(ctx->own);
     }
+    if (ctx->gemm_ws) (void)hipFree(ctx->gemm_ws);
   }
   delete ctx;
 }
@@ -327,6 +343,12 @@ bool gemm_aligned(const q8::LinearArgs &a) {
 // MFMA GEMM (f32 x split into two bf16 terms).
 constexpr int64_t kGemmMinRows = 32;
 
+// Attach the context's split-K workspace to a GEMM launch.
+void attach_gemm_workspace(q8_ctx *ctx, q8::LinearArgs &la) {
+  la.ws = ctx->gemm_ws;
+  la.ws_floats = kGemmWsFloats;
+}
+
 }  // namespace
 
 int q8_linear(q8_ctx *ctx, q8_buf *w, uint64_t owt_u16, q8_buf *a, uint64_t ox_f32,
@@ -357,8 +379,13 @@ int q8_linear(q8_ctx *ctx, q8_buf *w, uint64_t owt_u16, q8_buf *a, uint64_t ox_f
   la.n = n;
   la.G = G;
   la.kind = scale_dtype;
-  hipError_t e = (s >= kGemmMinRows && gemm_aligned(la)) ? q8::launch_gemm(la, ctx->stream)
-                                                          : q8::launch_gemv(la, ctx->stream);
+  hipError_t e;
+  if (s >= kGemmMinRows && gemm_aligned(la)) {
+    attach_gemm_workspace(ctx, la);
+    e = q8::launch_gemm(la, ctx->stream);
+  } else {
+    e = q8::launch_gemv(la, ctx->stream);
+  }
   if (e != hipSuccess) return hip_fail(ctx, e, "q8_linear launch");
   return ok(ctx);
 }
@@ -393,8 +420,13 @@ int q8_linear_bf16act(q8_ctx *ctx, q8_buf *w, uint64_t owt_u16, q8_buf *x, uint6
   la.n = n;
   la.G = G;
   la.kind = scale_dtype;
-  hipError_t e = gemm_aligned(la) ? q8::launch_gemm(la, ctx->stream)
-                                  : q8::launch_gemv(la, ctx->stream);
+  hipError_t e;
+  if (gemm_aligned(la)) {
+    attach_gemm_workspace(ctx, la);
+    e = q8::launch_gemm(la, ctx->stream);
+  } else {
+    e = q8::launch_gemv(la, ctx->stream);
+  }
   if (e != hipSuccess) return hip_fail(ctx, e, "q8_linear_bf16act launch");
   return ok(ctx);
 }
