@@ -77,6 +77,42 @@ __device__ __forceinline__ float dot16(u32x4 q, f32x4 xa, f32x4 xb, f32x4 xc, f3
   return p;
 }
 
+// ---- buffer loads and bf16 packing (MFMA kernels) -----------------------
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef __amdgpu_buffer_rsrc_t rsrc_t;
+
+// Raw buffer resource (stride 0, 32-bit data format).  Loads whose VGPR
+// offset lies at or past `bytes` return zeros, so every read of a ragged
+// edge is either inside the tensor or zero-filled.
+__device__ __forceinline__ rsrc_t make_rsrc(const void *base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, (int)bytes,
+                                           0x00020000);
+}
+__device__ __forceinline__ u32x4 bload16(rsrc_t r, uint32_t off) {
+  return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
+}
+constexpr uint32_t kOutOfRange = 0x80000000u;   // an offset past every tensor here
+
+__device__ __forceinline__ uint32_t pk_hi16(float lo, float hi) {
+  // Upper halves of two f32 whose values are exact in bf16.
+  return __builtin_amdgcn_perm(__builtin_bit_cast(uint32_t, hi), __builtin_bit_cast(uint32_t, lo),
+                               0x07060302u);
+}
+
+// 8 signed codes (two dwords) -> 8 bf16, exact.
+__device__ __forceinline__ bf16x8_t codes_to_bf16(uint32_t d0, uint32_t d1) {
+  u32x4 o = {pk_hi16(sbyte_to_f32<0>(d0), sbyte_to_f32<1>(d0)),
+             pk_hi16(sbyte_to_f32<2>(d0), sbyte_to_f32<3>(d0)),
+             pk_hi16(sbyte_to_f32<0>(d1), sbyte_to_f32<1>(d1)),
+             pk_hi16(sbyte_to_f32<2>(d1), sbyte_to_f32<3>(d1))};
+  return __builtin_bit_cast(bf16x8_t, o);
+}
+
+__device__ __forceinline__ uint32_t bf16_rne(float f) {
+  return __builtin_bit_cast(uint16_t, (__bf16)f);
+}
+
 // ---- wavefront reductions (wave64) --------------------------------------
 // DPP row operations reduce within each row of 16 lanes; the four row sums
 // are then combined with readlane.  Every lane returns the full sum.

@@ -37,6 +37,8 @@ struct LinearArgs {
 hipError_t launch_gemv(const LinearArgs &a, hipStream_t st);
 // Prefill path: MFMA GEMM (bf16 x, or f32 x split into two bf16 terms).
 hipError_t launch_gemm(const LinearArgs &a, hipStream_t st);
+// Small batches (2 <= s <= 32, f32 x): MFMA over zero-padded 16-row tiles.
+hipError_t launch_skinny(const LinearArgs &a, hipStream_t st);
 
 struct GatherArgs {
   const uint8_t *w;      // byte address of packed row 0 of the table

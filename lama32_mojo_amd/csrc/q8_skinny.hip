@@ -1,0 +1,338 @@
+// q8_skinny.hip -- decode-path Q8 linear for small batches (2 <= s < 32,
+// f32 activations) on gfx950 bf16 MFMA.
+//
+// y[b, j] = sum_g scale[j, g] * sum_{k in g} x[b, k] * q[j, k]
+// (k_mm_q8, src/llama_q8.mojo:54-93: unscaled dot per group, then one scale
+// multiply per group).
+//
+// With a few activation rows the layer is still HBM-bound, but a VALU GEMV
+// spends s FMAs and s LDS reads of x per code, which stops keeping up with
+// HBM at s of about 4.  Here the products run on v_mfma_f32_16x16x32_bf16 with
+// the batch rows zero-padded to 16 per row tile:
+//   * x is f32: each value is split into hi = bf16(x) and lo = bf16(x - hi)
+//     (x - hi is exact in f32), two MFMAs per k-step; the residual error is
+//     below 2^-17 |x|;
+//   * |q| <= 127 is exact in bf16; one MFMA k-step (32 codes) is exactly one
+//     G=32 group or half a G=64 group, each group's partial starts from 0 and
+//     is folded into the output with one f32 FMA;
+//   * lane (c, q) of a wave feeds weight row c of a 16-row tile; in k-step t
+//     (t = 0, 1) of a 64-code slot it supplies codes 32t + 4q .. +4 and
+//     32t + 16 + 4q .. +4 (so a k-step never leaves its group of 32), and the
+//     matching x[b][k] of batch row b = c of the row tile (read straight from
+//     memory, 64 contiguous bytes per row and load: x is a few KiB and stays
+//     in L2);
+//   * the codes and scales reach that layout through a small LDS region
+//     private to each wave: a chunk of 4 slots of 16 rows is read with loads
+//     in which each row is one contiguous 256-byte run (4 rows per
+//     instruction), the access pattern HBM streams best, and one more load
+//     brings the chunk's scales;
+//   * the KW waves of a workgroup split K into contiguous ranges of slots and
+//     meet in LDS; a workgroup covers NC tiles of 16 weight rows, NC chosen so
+//     that the grid still fills the chip.
+// All loads are range-checked buffer loads: batch rows past s and weight rows
+// past n read as zero.
+#include "q8_device.h"
+#include "q8_launch.h"
+
+#include <type_traits>
+
+namespace q8 {
+namespace {
+
+// Raw scales of one 64-code slot (G=64: one scale, G=32: two).
+template <int G, int KIND> struct SkinnyScale {
+  static constexpr int bytes = (64 / G) * ScaleTraits<KIND>::bytes;
+  uint32_t wd[bytes >= 4 ? bytes / 4 : 1];
+  __device__ __forceinline__ void load(rsrc_t r, uint32_t off) {
+    if constexpr (bytes == 8) {
+      const u32x2 v = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, 0));
+      wd[0] = v.x;
+      wd[1] = v.y;
+    } else if constexpr (bytes == 4) {
+      wd[0] = __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0);
+    } else {
+      wd[0] = __builtin_amdgcn_raw_buffer_load_b16(r, off, 0, 0);
+    }
+  }
+  __device__ __forceinline__ float get(int gi) const {
+    if constexpr (G == 64 && KIND == SCALE_F16) return f16_bits_to_f32((uint16_t)wd[0]);
+    else if constexpr (G == 64) return __builtin_bit_cast(float, wd[0]);
+    else if constexpr (KIND == SCALE_F16) return f16_bits_to_f32((uint16_t)(wd[0] >> (16 * gi)));
+    else return __builtin_bit_cast(float, wd[gi]);
+  }
+};
+
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+
+// Two f32 -> packed hi = bf16(x) and lo = bf16(x - hi), both rounded to
+// nearest even (v_cvt_pk_bf16_f32); x - hi is exact in f32.
+__device__ __forceinline__ void split2(uint32_t a, uint32_t b, uint32_t &hi, uint32_t &lo) {
+  const f32x2_t v = {__builtin_bit_cast(float, a), __builtin_bit_cast(float, b)};
+  const uint32_t h = __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2_t));
+  const f32x2_t hf = {__builtin_bit_cast(float, h << 16), __builtin_bit_cast(float, h & 0xffff0000u)};
+  lo = __builtin_bit_cast(uint32_t, __builtin_convertvector(v - hf, bf16x2_t));
+  hi = h;
+}
+
+// 8 f32 (two dwordx4) -> hi and lo bf16 halves.
+__device__ __forceinline__ void split_hi_lo(u32x4 a, u32x4 b, bf16x8_t &hi, bf16x8_t &lo) {
+  uint32_t h[4], l[4];
+  split2(a.x, a.y, h[0], l[0]);
+  split2(a.z, a.w, h[1], l[1]);
+  split2(b.x, b.y, h[2], l[2]);
+  split2(b.z, b.w, h[3], l[3]);
+  hi = __builtin_bit_cast(bf16x8_t, u32x4{h[0], h[1], h[2], h[3]});
+  lo = __builtin_bit_cast(bf16x8_t, u32x4{l[0], l[1], l[2], l[3]});
+}
+
+constexpr int CH = 4;                // 64-code slots per chunk
+constexpr int CRB = CH * 64 + 16;    // LDS bytes per weight row of a chunk (16-byte pad)
+
+// Scales of one chunk (CH slots) of one weight row: 8 (G=64 f16), 16 or 32
+// (G=32 f32) bytes.
+template <int G, int KIND> struct ChunkScale {
+  static constexpr int slot_bytes = (64 / G) * ScaleTraits<KIND>::bytes;
+  static constexpr int bytes = CH * slot_bytes;
+};
+
+template <int G, int KIND, int NC, int TR, int KW>
+__global__ __launch_bounds__(64 * KW) void skinny_kernel(const uint8_t *__restrict__ w,
+                                                         int64_t row_bytes,
+                                                         const float *__restrict__ x,
+                                                         float *__restrict__ y, int64_t s,
+                                                         int64_t m, int64_t n) {
+  constexpr int SB = ScaleTraits<KIND>::bytes;
+  typedef ChunkScale<G, KIND> CS;
+  typedef SkinnyScale<G, KIND> SS;
+  // per-wave staging of one chunk: codes [NC][16 rows][CRB], scales [NC][16 rows][CS::bytes]
+  __shared__ __attribute__((aligned(16))) uint8_t lcode[KW][NC][16 * CRB];
+  __shared__ __attribute__((aligned(16))) uint8_t lscale[KW][NC][16 * CS::bytes];
+  __shared__ f32x4 red[KW > 1 ? KW - 1 : 1][TR * NC][64];
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int c = lane & 15, q = lane >> 4;
+  const int64_t n0 = (int64_t)blockIdx.x * 16 * NC;
+
+  // slots [sl0, sl1) of this wave, processed in chunks of CH slots
+  const int nslot = (int)((m + 63) / 64);
+  const int per = ((nslot + KW - 1) / KW + CH - 1) / CH * CH;
+  const int sl0 = wid * per;
+  const int sl1 = sl0 + per < nslot ? sl0 + per : nslot;
+  const int cnt = sl1 > sl0 ? sl1 - sl0 : 0;
+
+  const int64_t nrows = n - n0 < 16 * NC ? n - n0 : 16 * NC;
+  const rsrc_t wr = make_rsrc(w + n0 * row_bytes, (uint32_t)(nrows * row_bytes));
+  // Chunk loads.  Codes: instruction u of a column tile reads rows 4u .. 4u+3,
+  // lane -> row 4u + lane / 16, bytes 16 (lane % 16) .. +16 of the chunk's
+  // 256 codes (each row a contiguous 256-byte run).  Scales: lane -> row
+  // (lane / (CS::bytes / 16)) % 16, 16 bytes at 16 (lane % (CS::bytes / 16))
+  // (for 8-byte chunks, row lane % 16): each row's chunk scales in one run.
+  constexpr int SLPR = CS::bytes >= 16 ? CS::bytes / 16 : 1;   // lanes per row for scales
+  uint32_t vcc[NC], vsc[NC];
+  const int srow = (lane / SLPR) % 16, spart = lane % SLPR;
+#pragma unroll
+  for (int ct = 0; ct < NC; ++ct) {
+    vcc[ct] = (uint32_t)((ct * 16 + (lane >> 4)) * row_bytes + (m / G) * SB + (lane & 15) * 16);
+    vsc[ct] = (uint32_t)((ct * 16 + srow) * row_bytes + spart * 16);
+  }
+  typedef typename std::conditional<CS::bytes >= 16, u32x4, u32x2>::type sraw_t;
+  auto load_chunk = [&](u32x4 (&cq)[NC][4], sraw_t (&sq)[NC], int sl) {
+#pragma unroll
+    for (int ct = 0; ct < NC; ++ct) {
+#pragma unroll
+      for (int u = 0; u < 4; ++u)
+        cq[ct][u] = bload16(wr, vcc[ct] + (uint32_t)(4 * u * row_bytes) + sl * 64);
+      if constexpr (CS::bytes >= 16)
+        sq[ct] = bload16(wr, vsc[ct] + sl * CS::slot_bytes);
+      else
+        sq[ct] = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(wr, vsc[ct] + sl * CS::slot_bytes, 0, 0));
+    }
+  };
+  // Staging puts a slot's codes in MFMA order: entry q (16 bytes) of a row's
+  // slot holds, for k-step t = 0, 1, the codes 32t + 4q .. +4 and
+  // 32t + 16 + 4q .. +4.  The loaded 16 codes [16p, 16p + 16) of a slot are
+  // dwords d = 0..3 with codes 16p + 4d .. +4, i.e. entry q = d, piece p.
+  auto stage_chunk = [&](const u32x4 (&cq)[NC][4], const sraw_t (&sq)[NC]) {
+    const int js = (lane & 15) >> 2, pp = lane & 3;
+#pragma unroll
+    for (int ct = 0; ct < NC; ++ct) {
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        uint8_t *d = &lcode[wid][ct][(4 * u + (lane >> 4)) * CRB + js * 64 + 4 * pp];
+        *reinterpret_cast<uint32_t *>(d) = cq[ct][u].x;
+        *reinterpret_cast<uint32_t *>(d + 16) = cq[ct][u].y;
+        *reinterpret_cast<uint32_t *>(d + 32) = cq[ct][u].z;
+        *reinterpret_cast<uint32_t *>(d + 48) = cq[ct][u].w;
+      }
+      *reinterpret_cast<sraw_t *>(&lscale[wid][ct][srow * CS::bytes + spart * 16]) = sq[ct];
+    }
+  };
+
+  const rsrc_t xr = make_rsrc(x, (uint32_t)(s * m * 4));
+  uint32_t vx[TR];
+#pragma unroll
+  for (int tr = 0; tr < TR; ++tr) vx[tr] = (uint32_t)(((tr * 16 + c) * m + 4 * q) * 4);
+  // activations of slot sl for lane (c, q), b = 16 tr + c, in the codes' MFMA
+  // order: x[b][64 sl + 16u + 4q .. +4] for u = 0..3 (u = 0, 1: k-step 0;
+  // u = 2, 3: k-step 1), each load 64 contiguous bytes per batch row; a slot
+  // past this wave's range or a second half past m reads zeros
+  auto load_x = [&](u32x4 (&xa)[TR][4], int sl) {
+    const bool lo_ok = sl < sl1;
+    const bool hi_ok = lo_ok && sl * 64 + 32 < m;
+#pragma unroll
+    for (int tr = 0; tr < TR; ++tr) {
+      const uint32_t o0 = lo_ok ? vx[tr] + sl * 256 : kOutOfRange;
+      const uint32_t o1 = hi_ok ? vx[tr] + sl * 256 + 128 : kOutOfRange;
+      xa[tr][0] = bload16(xr, o0);
+      xa[tr][1] = bload16(xr, o0 + 64);
+      xa[tr][2] = bload16(xr, o1);
+      xa[tr][3] = bload16(xr, o1 + 64);
+    }
+  };
+
+  f32x4 acc[TR][NC];
+#pragma unroll
+  for (int tr = 0; tr < TR; ++tr)
+#pragma unroll
+    for (int ct = 0; ct < NC; ++ct) acc[tr][ct] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+
+  u32x4 cq[NC][4];
+  sraw_t sq[NC];
+  u32x4 xa[2][TR][4];
+  load_chunk(cq, sq, sl0);
+  load_x(xa[0], sl0);
+  load_x(xa[1], sl0 + 1);
+
+  // Whole chunks: a slot past this wave's range meets zero activations (and
+  // finite codes) and has its scales forced to 0.
+  for (int i0 = 0; i0 < cnt; i0 += CH) {
+    const int slc = sl0 + i0;
+    // LDS is private to the wave and a wave's LDS operations run in order,
+    // so staging the next chunk after this chunk's reads needs no barrier.
+    stage_chunk(cq, sq);
+    load_chunk(cq, sq, slc + CH);
+#pragma unroll
+    for (int j = 0; j < CH; ++j) {
+      const int sl = slc + j;
+      const bool live = i0 + j < cnt;
+      bf16x8_t xh[TR][2], xl[TR][2];
+#pragma unroll
+      for (int tr = 0; tr < TR; ++tr) {
+        split_hi_lo(xa[j & 1][tr][0], xa[j & 1][tr][1], xh[tr][0], xl[tr][0]);
+        split_hi_lo(xa[j & 1][tr][2], xa[j & 1][tr][3], xh[tr][1], xl[tr][1]);
+      }
+      load_x(xa[j & 1], sl + 2);
+      const bool hi_ok = sl * 64 + 32 < m;
+#pragma unroll
+      for (int ct = 0; ct < NC; ++ct) {
+        const u32x4 qq = *reinterpret_cast<const u32x4 *>(&lcode[wid][ct][c * CRB + 64 * j + 16 * q]);
+        SS sc;
+        const uint8_t *sp = &lscale[wid][ct][c * CS::bytes + j * CS::slot_bytes];
+        if constexpr (SS::bytes == 8) {
+          const u32x2 v = *reinterpret_cast<const u32x2 *>(sp);
+          sc.wd[0] = v.x;
+          sc.wd[1] = v.y;
+        } else if constexpr (SS::bytes == 4) {
+          sc.wd[0] = *reinterpret_cast<const uint32_t *>(sp);
+        } else {
+          sc.wd[0] = *reinterpret_cast<const uint16_t *>(sp);
+        }
+        const bf16x8_t b0 = codes_to_bf16(qq.x, qq.y);
+        const bf16x8_t b1 = codes_to_bf16(qq.z, qq.w);
+        const float s0 = live ? sc.get(0) : 0.0f;
+        const float s1 = G == 32 ? (live && hi_ok ? sc.get(1) : 0.0f) : s0;
+#pragma unroll
+        for (int tr = 0; tr < TR; ++tr) {
+          const f32x4 z = {0.0f, 0.0f, 0.0f, 0.0f};
+          f32x4 t0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xh[tr][0], b0, z, 0, 0, 0);
+          t0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xl[tr][0], b0, t0, 0, 0, 0);
+          if constexpr (G == 32) {
+            f32x4 t1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xh[tr][1], b1, z, 0, 0, 0);
+            t1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xl[tr][1], b1, t1, 0, 0, 0);
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+              acc[tr][ct][v] = __builtin_fmaf(s0, t0[v], acc[tr][ct][v]);
+              acc[tr][ct][v] = __builtin_fmaf(s1, t1[v], acc[tr][ct][v]);
+            }
+          } else {
+            t0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xh[tr][1], b1, t0, 0, 0, 0);
+            t0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xl[tr][1], b1, t0, 0, 0, 0);
+#pragma unroll
+            for (int v = 0; v < 4; ++v) acc[tr][ct][v] = __builtin_fmaf(s0, t0[v], acc[tr][ct][v]);
+          }
+        }
+      }
+    }
+  }
+
+  // The KW K ranges meet in LDS; wave 0 adds them in order and stores.
+  if (wid > 0) {
+#pragma unroll
+    for (int tr = 0; tr < TR; ++tr)
+#pragma unroll
+      for (int ct = 0; ct < NC; ++ct) red[wid - 1][tr * NC + ct][lane] = acc[tr][ct];
+  }
+  __syncthreads();
+  if (wid == 0) {
+#pragma unroll
+    for (int tr = 0; tr < TR; ++tr)
+#pragma unroll
+      for (int ct = 0; ct < NC; ++ct) {
+        f32x4 v = acc[tr][ct];
+        for (int k = 0; k < KW - 1; ++k) v += red[k][tr * NC + ct][lane];
+        // D layout of v_mfma_f32_16x16x32: lane -> weight row lane % 16,
+        // element e -> batch row 4 (lane / 16) + e
+        const int64_t j = n0 + ct * 16 + c;
+        if (j < n) {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const int64_t b = tr * 16 + 4 * q + e;
+            if (b < s) y[b * n + j] = v[e];
+          }
+        }
+      }
+  }
+}
+
+template <int G, int KIND, int NC, int TR, int KW>
+hipError_t launch_nc(const LinearArgs &a, hipStream_t st) {
+  const int64_t blocks = (a.n + 16 * NC - 1) / (16 * NC);
+  hipLaunchKernelGGL((skinny_kernel<G, KIND, NC, TR, KW>), dim3((unsigned)blocks), dim3(64 * KW),
+                     0, st, a.w, a.row_bytes, static_cast<const float *>(a.x), a.y, a.s, a.m, a.n);
+  return hipGetLastError();
+}
+
+template <int G, int KIND, int TR>
+hipError_t launch_tr(const LinearArgs &a, hipStream_t st) {
+  // Two column tiles per wave (x is loaded and split once per tile pair)
+  // while that keeps >= 512 workgroups (two per CU); short weight matrices
+  // split K over 8 waves instead of 4.  (Four tiles per wave need 86 KiB of
+  // staging per workgroup, which halves the waves per CU and loses more than
+  // the shared x saves.)
+  const int64_t tiles = (a.n + 15) / 16;
+  if (tiles >= 2 * 512) return launch_nc<G, KIND, 2, TR, 4>(a, st);
+  if (tiles >= 256) return launch_nc<G, KIND, 1, TR, 4>(a, st);
+  return launch_nc<G, KIND, 1, TR, 8>(a, st);
+}
+
+template <int G, int KIND>
+hipError_t launch_g(const LinearArgs &a, hipStream_t st) {
+  if (a.s <= 16) return launch_tr<G, KIND, 1>(a, st);
+  return launch_tr<G, KIND, 2>(a, st);
+}
+
+}  // namespace
+
+hipError_t launch_skinny(const LinearArgs &a, hipStream_t st) {
+  if (a.s == 0 || a.n == 0) return hipSuccess;
+  if (a.s > 32 || a.x_is_bf16) return hipErrorInvalidValue;
+  if (a.G == 64 && a.kind == SCALE_F16) return launch_g<64, SCALE_F16>(a, st);
+  if (a.G == 64 && a.kind == SCALE_F32) return launch_g<64, SCALE_F32>(a, st);
+  if (a.G == 32 && a.kind == SCALE_F16) return launch_g<32, SCALE_F16>(a, st);
+  if (a.G == 32 && a.kind == SCALE_F32) return launch_g<32, SCALE_F32>(a, st);
+  return hipErrorInvalidValue;
+}
+
+}  // namespace q8

@@ -340,7 +340,9 @@ bool gemm_aligned(const q8::LinearArgs &a) {
 }
 
 // Activation rows at which the W8A32 path switches from the VALU GEMV to the
-// MFMA GEMM (f32 x split into two bf16 terms).
+// small-batch MFMA kernel, and from that to the MFMA GEMM (f32 x split into
+// two bf16 terms in both).
+constexpr int64_t kSkinnyMinRows = 2;
 constexpr int64_t kGemmMinRows = 32;
 
 // Attach the context's split-K workspace to a GEMM launch.
@@ -383,6 +385,8 @@ int q8_linear(q8_ctx *ctx, q8_buf *w, uint64_t owt_u16, q8_buf *a, uint64_t ox_f
   if (s >= kGemmMinRows && gemm_aligned(la)) {
     attach_gemm_workspace(ctx, la);
     e = q8::launch_gemm(la, ctx->stream);
+  } else if (s >= kSkinnyMinRows && gemm_aligned(la)) {
+    e = q8::launch_skinny(la, ctx->stream);
   } else {
     e = q8::launch_gemv(la, ctx->stream);
   }

@@ -125,7 +125,7 @@ SHAPES = [(8192, 2048), (3072, 2048), (2048, 8192), (1000, 1536), (1, 64), (7, 9
 
 @pytest.mark.parametrize("G,scale", LAYOUTS)
 @pytest.mark.parametrize("n,m", SHAPES)
-@pytest.mark.parametrize("s", [1, 2, 3, 4, 5, 16])
+@pytest.mark.parametrize("s", [1, 2, 3, 4, 5, 16, 24])
 def test_linear_matches_closed_form(ctx, cor, G, scale, n, m, s):
     if m % G:
         pytest.skip("m not a multiple of G")
