@@ -137,6 +137,82 @@ int q8_embed_gather(q8_ctx *ctx, q8_buf *w, uint64_t oemb_u16, q8_buf *ids,
                     uint64_t oids_i32, q8_buf *a, uint64_t oy_f32, int64_t s,
                     int64_t d, int64_t vocab, int G, int scale_dtype);
 
+/* ---- decode-step layer kernels ------------------------------------------------
+ * The non-linear parts of run_layer_q8 and of the token loop
+ * (src/llama_q8.mojo:144-230, qwen3_mojo/src/qwen_q8.mojo:127-162), over the
+ * same arenas: f32 activations at float offsets of `a`, bf16 norm vectors at
+ * u16 offsets of the weight arena `w`.  The KV cache is a separate binary16
+ * buffer `kv` (the reference keeps an f32 cache in the activation arena).
+ * Outputs may coincide exactly with an input (in place) but must not
+ * otherwise overlap one. */
+
+/* y = bf16(wn) * x / sqrt(mean(x^2) + eps) for `rows` rows of d, wn = d bf16
+ * values at owt (k_rmsnorm_w / rmsnorm_op, src/llama_common.mojo:197-225,
+ * 690-696). */
+int q8_rmsnorm(q8_ctx *ctx, q8_buf *w, uint64_t owt_u16, q8_buf *a,
+               uint64_t ox_f32, uint64_t oy_f32, int64_t rows, int64_t d,
+               float eps);
+
+/* h = x + o stored at oh, then y = rmsnorm(h): k_res_add then k_rmsnorm_w
+ * (src/llama_common.mojo:354-359,197-225) in one dispatch. */
+int q8_add_rmsnorm(q8_ctx *ctx, q8_buf *w, uint64_t owt_u16, q8_buf *a,
+                   uint64_t ox_f32, uint64_t oo_f32, uint64_t oh_f32,
+                   uint64_t oy_f32, int64_t rows, int64_t d, float eps);
+
+/* RoPE (rotate_half; head_dim/2 inverse frequencies at oinv) in place on
+ * q [s, nheads*head_dim] at oq and k [s, nkv*head_dim] at ok, and append the
+ * rotated k and the v [s, nkv*head_dim] at ov to cache rows pos0 .. pos0+s-1
+ * of the layer's K block (maxlen rows of nkv*head_dim binary16 at f16 offset
+ * okc of kv) and V block (at ovc) -- k_rope_qk_copy2
+ * (src/llama_common.mojo:299-342).  With posbuf != NULL the position is
+ * instead the int32 at element offset opos of posbuf, read by the kernel
+ * (a captured step then serves every position; rows past maxlen are dropped,
+ * and attention clamps its context to maxlen). */
+int q8_rope_kv(q8_ctx *ctx, q8_buf *a, uint64_t oq_f32, uint64_t ok_f32,
+               uint64_t ov_f32, uint64_t oinv_f32, q8_buf *kv, uint64_t okc_f16,
+               uint64_t ovc_f16, int64_t maxlen, int64_t s, int64_t pos0,
+               q8_buf *posbuf, uint64_t opos_i32, int nheads, int nkv,
+               int head_dim);
+
+/* Floats of activation-arena scratch q8_attention needs. */
+uint64_t q8_attention_scratch_floats(int64_t s, int nheads, int head_dim,
+                                     int64_t maxlen);
+
+/* out [s, nheads*head_dim] at oy = causal GQA attention of the rotated
+ * q at oq (query row i at position pos0 + i attends cache rows
+ * 0 .. pos0 + i; head h reads KV head h / (nheads / nkv); scores scaled by
+ * 1/sqrt(head_dim)) -- k_scores, k_softmax_rows and k_att_out
+ * (src/llama_common.mojo:402-473) with their score buffer replaced by
+ * q8_attention_scratch_floats() floats at oscratch.  head_dim 64 or 128,
+ * nheads / nkv in {1, 2, 4, 8}.  Position as in q8_rope_kv. */
+int q8_attention(q8_ctx *ctx, q8_buf *a, uint64_t oq_f32, q8_buf *kv,
+                 uint64_t okc_f16, uint64_t ovc_f16, int64_t maxlen,
+                 uint64_t oy_f32, uint64_t oscratch_f32, int64_t s, int64_t pos0,
+                 q8_buf *posbuf, uint64_t opos_i32, int nheads, int nkv,
+                 int head_dim);
+
+/* g = silu(g) * u in place over n values (k_swiglu_mul,
+ * src/llama_common.mojo:476-481). */
+int q8_swiglu(q8_ctx *ctx, q8_buf *a, uint64_t og_f32, uint64_t ou_f32, int64_t n);
+
+/* y = x + o (k_res_add, src/llama_common.mojo:354-359). */
+int q8_res_add(q8_ctx *ctx, q8_buf *a, uint64_t ox_f32, uint64_t oo_f32,
+               uint64_t oy_f32, int64_t n);
+
+/* y += x (k_add, src/llama_common.mojo:397-400). */
+int q8_add(q8_ctx *ctx, q8_buf *a, uint64_t ox_f32, uint64_t oy_f32, int64_t n);
+
+/* Index of the largest of n f32 at ox, stored as an int32 at element offset
+ * oid of ids (k_argmax / argmax_op, src/llama_common.mojo:493-519,783-789):
+ * a value must be strictly greater to win (NaN never wins), equal maxima go
+ * to the lowest index. */
+int q8_argmax(q8_ctx *ctx, q8_buf *a, uint64_t ox_f32, int64_t n, q8_buf *ids,
+              uint64_t oid_i32);
+
+/* The int32 position at element offset opos of posbuf += s, on the stream
+ * (the device side of n_cached += s, qwen3_mojo/src/qwen_q8.mojo:138). */
+int q8_pos_advance(q8_ctx *ctx, q8_buf *posbuf, uint64_t opos_i32, int64_t s);
+
 /* ---- HIP graphs ------------------------------------------------------------ */
 
 /* Capture every call issued on the context's stream between begin and end

@@ -5,6 +5,7 @@
 // only picks a kernel variant and a grid; it trusts its arguments.
 #pragma once
 
+#include <hip/hip_fp16.h>
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -49,5 +50,34 @@ struct GatherArgs {
   int G, kind;
 };
 hipError_t launch_embed_gather(const GatherArgs &a, hipStream_t st);
+
+// ---- decode-step layer kernels (q8_layer.hip) ------------------------------
+// RMSNorm of `rows` rows of d; with res != null the rows are x + res, also
+// stored to h_out.
+hipError_t launch_rmsnorm(const uint16_t *wn, const float *x, const float *res, float *h_out,
+                          float *y, int64_t rows, int64_t d, float eps, hipStream_t st);
+// RoPE on q [s, nheads*head_dim] and k [s, nkv*head_dim] in place; rotated k
+// and v go to binary16 cache rows pos0 .. pos0+s-1 (pos0 = *posp if posp).
+hipError_t launch_rope_kv(float *q, float *k, const float *v, __half *kc, __half *vc,
+                          const float *inv, int s, const int *posp, int pos0, int nheads, int nkv,
+                          int head_dim, int64_t maxlen, hipStream_t st);
+struct AttnArgs {
+  const float *q;        // [s, nheads * head_dim], rotated
+  const __half *kc, *vc; // [maxlen, nkv * head_dim]
+  float *part;           // scratch: s * nheads * nsplit * (head_dim + 2) floats
+  float *out;            // [s, nheads * head_dim]
+  int s, nheads, nkv, head_dim, nsplit;
+  const int *posp;       // device position (or null: pos0)
+  int pos0;
+  int maxlen;            // cache rows; positions past it are clamped
+};
+// Causal GQA attention of s query rows at positions pos0 .. pos0+s-1 over
+// cache rows 0 .. pos0+i; nsplit = ceil(maxlen / 64).
+hipError_t launch_attention(const AttnArgs &a, hipStream_t st);
+hipError_t launch_swiglu(float *g, const float *u, int64_t n, hipStream_t st);
+hipError_t launch_res_add(const float *x, const float *o, float *y, int64_t n, hipStream_t st);
+hipError_t launch_add(const float *x, float *y, int64_t n, hipStream_t st);
+hipError_t launch_argmax(const float *v, int64_t n, int32_t *out, hipStream_t st);
+hipError_t launch_pos_advance(int *pos, int s, hipStream_t st);
 
 }  // namespace q8

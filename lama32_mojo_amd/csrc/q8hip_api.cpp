@@ -6,9 +6,11 @@
 // validation, kernel dispatch and HIP-graph capture.  Every entry point
 // validates all of its arguments before the first HIP call, so error paths
 // behave the same on a host-only context (device Q8_DEVICE_NONE) as on a GPU.
+#include <hip/hip_fp16.h>
 #include <hip/hip_runtime.h>
 
 #include <cstdarg>
+#include <cstdint>
 #include <cstdio>
 #include <cstring>
 #include <new>
@@ -468,6 +470,277 @@ int q8_embed_gather(q8_ctx *ctx, q8_buf *w, uint64_t oemb_u16, q8_buf *ids, uint
   ga.kind = scale_dtype;
   hipError_t e = q8::launch_embed_gather(ga, ctx->stream);
   if (e != hipSuccess) return hip_fail(ctx, e, "q8_embed_gather launch");
+  return ok(ctx);
+}
+
+// ---- decode-step layer kernels -------------------------------------------------
+
+namespace {
+
+float *fptr(q8_buf *b, uint64_t off_f32) { return reinterpret_cast<float *>(bytes(b, off_f32 * 4)); }
+
+// An output range may coincide with an input range or be disjoint from it.
+bool bad_alias(uint64_t o0, uint64_t n, uint64_t i0, uint64_t m) {
+  return o0 != i0 && overlaps(o0, o0 + n, i0, i0 + m);
+}
+
+int check_f32(q8_ctx *ctx, q8_buf *a, uint64_t off, uint64_t count, const char *what,
+              const char *name) {
+  if (!fits(off, count, 4, a->size))
+    return fail(ctx, Q8_ERR_RANGE, "%s: %s [%llu, +%llu) f32 exceeds the activation buffer", what,
+                name, (unsigned long long)off, (unsigned long long)count);
+  return Q8_OK;
+}
+
+// Position source shared by q8_rope_kv and q8_attention.
+int check_pos(q8_ctx *ctx, q8_buf *posbuf, uint64_t opos, int64_t pos0, int64_t s, int64_t maxlen,
+              const char *what) {
+  if (posbuf) {
+    if (!fits(opos, 1, 4, posbuf->size))
+      return fail(ctx, Q8_ERR_RANGE, "%s: position offset %llu exceeds its buffer", what,
+                  (unsigned long long)opos);
+    return Q8_OK;
+  }
+  if (pos0 < 0 || pos0 + s > maxlen)
+    return fail(ctx, Q8_ERR_RANGE, "%s: rows %lld .. %lld exceed the KV cache of %lld rows "
+                "(KV cache full)", what, (long long)pos0, (long long)(pos0 + s),
+                (long long)maxlen);
+  return Q8_OK;
+}
+
+int check_heads(q8_ctx *ctx, int nheads, int nkv, int head_dim, const char *what) {
+  if (nheads <= 0 || nkv <= 0 || nheads % nkv != 0 || head_dim <= 0 || head_dim % 2 != 0)
+    return fail(ctx, Q8_ERR_SHAPE, "%s: nheads=%d, nkv=%d, head_dim=%d (need nkv | nheads and "
+                "an even head_dim)", what, nheads, nkv, head_dim);
+  return Q8_OK;
+}
+
+int64_t attn_nsplit(int64_t maxlen) { return (maxlen + 63) / 64; }
+
+}  // namespace
+
+int q8_rmsnorm(q8_ctx *ctx, q8_buf *w, uint64_t owt_u16, q8_buf *a, uint64_t ox_f32,
+               uint64_t oy_f32, int64_t rows, int64_t d, float eps) {
+  if (int rc = check_ctx(ctx)) return rc;
+  if (!w || !a) return fail(ctx, Q8_ERR_ARG, "q8_rmsnorm: null buffer");
+  if (rows < 0 || d <= 0)
+    return fail(ctx, Q8_ERR_SHAPE, "q8_rmsnorm: rows=%lld, d=%lld", (long long)rows, (long long)d);
+  const uint64_t n = (uint64_t)rows * (uint64_t)d;
+  if (!fits(owt_u16, (uint64_t)d, 2, w->size))
+    return fail(ctx, Q8_ERR_RANGE, "q8_rmsnorm: norm weights exceed the weight buffer");
+  if (int rc = check_f32(ctx, a, ox_f32, n, "q8_rmsnorm", "x")) return rc;
+  if (int rc = check_f32(ctx, a, oy_f32, n, "q8_rmsnorm", "y")) return rc;
+  if (bad_alias(oy_f32, n, ox_f32, n))
+    return fail(ctx, Q8_ERR_ARG, "q8_rmsnorm: y partially overlaps x");
+  if (ctx->host_only) return fail(ctx, Q8_ERR_NODEVICE, "q8_rmsnorm: host-only context");
+  if (rows == 0) return ok(ctx);
+  if (int rc = set_device(ctx)) return rc;
+  hipError_t e = q8::launch_rmsnorm(reinterpret_cast<const uint16_t *>(bytes(w, owt_u16 * 2)),
+                                    fptr(a, ox_f32), nullptr, nullptr, fptr(a, oy_f32), rows, d,
+                                    eps, ctx->stream);
+  if (e != hipSuccess) return hip_fail(ctx, e, "q8_rmsnorm launch");
+  return ok(ctx);
+}
+
+int q8_add_rmsnorm(q8_ctx *ctx, q8_buf *w, uint64_t owt_u16, q8_buf *a, uint64_t ox_f32,
+                   uint64_t oo_f32, uint64_t oh_f32, uint64_t oy_f32, int64_t rows, int64_t d,
+                   float eps) {
+  if (int rc = check_ctx(ctx)) return rc;
+  if (!w || !a) return fail(ctx, Q8_ERR_ARG, "q8_add_rmsnorm: null buffer");
+  if (rows < 0 || d <= 0)
+    return fail(ctx, Q8_ERR_SHAPE, "q8_add_rmsnorm: rows=%lld, d=%lld", (long long)rows,
+                (long long)d);
+  const uint64_t n = (uint64_t)rows * (uint64_t)d;
+  if (!fits(owt_u16, (uint64_t)d, 2, w->size))
+    return fail(ctx, Q8_ERR_RANGE, "q8_add_rmsnorm: norm weights exceed the weight buffer");
+  const uint64_t offs[4] = {ox_f32, oo_f32, oh_f32, oy_f32};
+  const char *names[4] = {"x", "o", "h", "y"};
+  for (int i = 0; i < 4; ++i)
+    if (int rc = check_f32(ctx, a, offs[i], n, "q8_add_rmsnorm", names[i])) return rc;
+  if (bad_alias(oh_f32, n, ox_f32, n) || bad_alias(oh_f32, n, oo_f32, n) ||
+      bad_alias(oy_f32, n, ox_f32, n) || bad_alias(oy_f32, n, oo_f32, n) ||
+      bad_alias(oy_f32, n, oh_f32, n))
+    return fail(ctx, Q8_ERR_ARG, "q8_add_rmsnorm: an output partially overlaps another range");
+  if (ctx->host_only) return fail(ctx, Q8_ERR_NODEVICE, "q8_add_rmsnorm: host-only context");
+  if (rows == 0) return ok(ctx);
+  if (int rc = set_device(ctx)) return rc;
+  hipError_t e = q8::launch_rmsnorm(reinterpret_cast<const uint16_t *>(bytes(w, owt_u16 * 2)),
+                                    fptr(a, ox_f32), fptr(a, oo_f32), fptr(a, oh_f32),
+                                    fptr(a, oy_f32), rows, d, eps, ctx->stream);
+  if (e != hipSuccess) return hip_fail(ctx, e, "q8_add_rmsnorm launch");
+  return ok(ctx);
+}
+
+int q8_rope_kv(q8_ctx *ctx, q8_buf *a, uint64_t oq_f32, uint64_t ok_f32, uint64_t ov_f32,
+               uint64_t oinv_f32, q8_buf *kv, uint64_t okc_f16, uint64_t ovc_f16, int64_t maxlen,
+               int64_t s, int64_t pos0, q8_buf *posbuf, uint64_t opos_i32, int nheads, int nkv,
+               int head_dim) {
+  if (int rc = check_ctx(ctx)) return rc;
+  if (!a || !kv) return fail(ctx, Q8_ERR_ARG, "q8_rope_kv: null buffer");
+  if (int rc = check_heads(ctx, nheads, nkv, head_dim, "q8_rope_kv")) return rc;
+  if (s < 0 || maxlen <= 0 || maxlen > INT32_MAX)
+    return fail(ctx, Q8_ERR_SHAPE, "q8_rope_kv: s=%lld, maxlen=%lld", (long long)s,
+                (long long)maxlen);
+  const uint64_t qn = (uint64_t)s * nheads * head_dim, kn = (uint64_t)s * nkv * head_dim;
+  const uint64_t cn = (uint64_t)maxlen * nkv * head_dim;
+  if (int rc = check_f32(ctx, a, oq_f32, qn, "q8_rope_kv", "q")) return rc;
+  if (int rc = check_f32(ctx, a, ok_f32, kn, "q8_rope_kv", "k")) return rc;
+  if (int rc = check_f32(ctx, a, ov_f32, kn, "q8_rope_kv", "v")) return rc;
+  if (int rc = check_f32(ctx, a, oinv_f32, (uint64_t)head_dim / 2, "q8_rope_kv", "inv_freq"))
+    return rc;
+  if (overlaps(oq_f32, oq_f32 + qn, ok_f32, ok_f32 + kn))
+    return fail(ctx, Q8_ERR_ARG, "q8_rope_kv: q and k overlap");
+  if (!fits(okc_f16, cn, 2, kv->size) || !fits(ovc_f16, cn, 2, kv->size))
+    return fail(ctx, Q8_ERR_RANGE, "q8_rope_kv: K or V cache block exceeds the KV buffer");
+  if (overlaps(okc_f16, okc_f16 + cn, ovc_f16, ovc_f16 + cn))
+    return fail(ctx, Q8_ERR_ARG, "q8_rope_kv: K and V cache blocks overlap");
+  if (int rc = check_pos(ctx, posbuf, opos_i32, pos0, s, maxlen, "q8_rope_kv")) return rc;
+  if (ctx->host_only) return fail(ctx, Q8_ERR_NODEVICE, "q8_rope_kv: host-only context");
+  if (s == 0) return ok(ctx);
+  if (int rc = set_device(ctx)) return rc;
+  __half *kvp = reinterpret_cast<__half *>(kv->ptr);
+  const int *posp = posbuf ? reinterpret_cast<const int *>(bytes(posbuf, opos_i32 * 4)) : nullptr;
+  hipError_t e = q8::launch_rope_kv(fptr(a, oq_f32), fptr(a, ok_f32), fptr(a, ov_f32),
+                                    kvp + okc_f16, kvp + ovc_f16, fptr(a, oinv_f32), (int)s, posp,
+                                    (int)pos0, nheads, nkv, head_dim, maxlen, ctx->stream);
+  if (e != hipSuccess) return hip_fail(ctx, e, "q8_rope_kv launch");
+  return ok(ctx);
+}
+
+uint64_t q8_attention_scratch_floats(int64_t s, int nheads, int head_dim, int64_t maxlen) {
+  if (s < 0 || nheads <= 0 || head_dim <= 0 || maxlen <= 0) return 0;
+  return (uint64_t)s * nheads * attn_nsplit(maxlen) * (uint64_t)(head_dim + 2);
+}
+
+int q8_attention(q8_ctx *ctx, q8_buf *a, uint64_t oq_f32, q8_buf *kv, uint64_t okc_f16,
+                 uint64_t ovc_f16, int64_t maxlen, uint64_t oy_f32, uint64_t oscratch_f32,
+                 int64_t s, int64_t pos0, q8_buf *posbuf, uint64_t opos_i32, int nheads, int nkv,
+                 int head_dim) {
+  if (int rc = check_ctx(ctx)) return rc;
+  if (!a || !kv) return fail(ctx, Q8_ERR_ARG, "q8_attention: null buffer");
+  if (int rc = check_heads(ctx, nheads, nkv, head_dim, "q8_attention")) return rc;
+  const int grp = nheads / nkv;
+  if ((head_dim != 64 && head_dim != 128) || (grp != 1 && grp != 2 && grp != 4 && grp != 8))
+    return fail(ctx, Q8_ERR_UNSUPPORTED, "q8_attention: head_dim=%d, nheads/nkv=%d "
+                "(supported: head_dim 64 or 128, nheads/nkv 1, 2, 4 or 8)", head_dim, grp);
+  if (s < 0 || s > 65535 || maxlen <= 0 || maxlen > INT32_MAX)
+    return fail(ctx, Q8_ERR_SHAPE, "q8_attention: s=%lld, maxlen=%lld", (long long)s,
+                (long long)maxlen);
+  const uint64_t qn = (uint64_t)s * nheads * head_dim;
+  const uint64_t cn = (uint64_t)maxlen * nkv * head_dim;
+  const uint64_t sn = q8_attention_scratch_floats(s, nheads, head_dim, maxlen);
+  if (int rc = check_f32(ctx, a, oq_f32, qn, "q8_attention", "q")) return rc;
+  if (int rc = check_f32(ctx, a, oy_f32, qn, "q8_attention", "out")) return rc;
+  if (int rc = check_f32(ctx, a, oscratch_f32, sn, "q8_attention", "scratch")) return rc;
+  if (overlaps(oy_f32, oy_f32 + qn, oq_f32, oq_f32 + qn) ||
+      overlaps(oscratch_f32, oscratch_f32 + sn, oq_f32, oq_f32 + qn) ||
+      overlaps(oscratch_f32, oscratch_f32 + sn, oy_f32, oy_f32 + qn))
+    return fail(ctx, Q8_ERR_ARG, "q8_attention: q, out and scratch must not overlap");
+  if (!fits(okc_f16, cn, 2, kv->size) || !fits(ovc_f16, cn, 2, kv->size))
+    return fail(ctx, Q8_ERR_RANGE, "q8_attention: K or V cache block exceeds the KV buffer");
+  if (int rc = check_pos(ctx, posbuf, opos_i32, pos0, s, maxlen, "q8_attention")) return rc;
+  if (ctx->host_only) return fail(ctx, Q8_ERR_NODEVICE, "q8_attention: host-only context");
+  if (s == 0) return ok(ctx);
+  if (int rc = set_device(ctx)) return rc;
+  const __half *kvp = reinterpret_cast<const __half *>(kv->ptr);
+  q8::AttnArgs aa;
+  aa.q = fptr(a, oq_f32);
+  aa.kc = kvp + okc_f16;
+  aa.vc = kvp + ovc_f16;
+  aa.part = fptr(a, oscratch_f32);
+  aa.out = fptr(a, oy_f32);
+  aa.s = (int)s;
+  aa.nheads = nheads;
+  aa.nkv = nkv;
+  aa.head_dim = head_dim;
+  aa.nsplit = (int)attn_nsplit(maxlen);
+  aa.posp = posbuf ? reinterpret_cast<const int *>(bytes(posbuf, opos_i32 * 4)) : nullptr;
+  aa.pos0 = (int)pos0;
+  aa.maxlen = (int)maxlen;
+  hipError_t e = q8::launch_attention(aa, ctx->stream);
+  if (e != hipSuccess) return hip_fail(ctx, e, "q8_attention launch");
+  return ok(ctx);
+}
+
+int q8_swiglu(q8_ctx *ctx, q8_buf *a, uint64_t og_f32, uint64_t ou_f32, int64_t n) {
+  if (int rc = check_ctx(ctx)) return rc;
+  if (!a) return fail(ctx, Q8_ERR_ARG, "q8_swiglu: null buffer");
+  if (n < 0) return fail(ctx, Q8_ERR_SHAPE, "q8_swiglu: n=%lld", (long long)n);
+  if (int rc = check_f32(ctx, a, og_f32, (uint64_t)n, "q8_swiglu", "g")) return rc;
+  if (int rc = check_f32(ctx, a, ou_f32, (uint64_t)n, "q8_swiglu", "u")) return rc;
+  if (overlaps(og_f32, og_f32 + n, ou_f32, ou_f32 + n))
+    return fail(ctx, Q8_ERR_ARG, "q8_swiglu: g and u overlap");
+  if (ctx->host_only) return fail(ctx, Q8_ERR_NODEVICE, "q8_swiglu: host-only context");
+  if (n == 0) return ok(ctx);
+  if (int rc = set_device(ctx)) return rc;
+  hipError_t e = q8::launch_swiglu(fptr(a, og_f32), fptr(a, ou_f32), n, ctx->stream);
+  if (e != hipSuccess) return hip_fail(ctx, e, "q8_swiglu launch");
+  return ok(ctx);
+}
+
+int q8_res_add(q8_ctx *ctx, q8_buf *a, uint64_t ox_f32, uint64_t oo_f32, uint64_t oy_f32,
+               int64_t n) {
+  if (int rc = check_ctx(ctx)) return rc;
+  if (!a) return fail(ctx, Q8_ERR_ARG, "q8_res_add: null buffer");
+  if (n < 0) return fail(ctx, Q8_ERR_SHAPE, "q8_res_add: n=%lld", (long long)n);
+  const uint64_t offs[3] = {ox_f32, oo_f32, oy_f32};
+  const char *names[3] = {"x", "o", "y"};
+  for (int i = 0; i < 3; ++i)
+    if (int rc = check_f32(ctx, a, offs[i], (uint64_t)n, "q8_res_add", names[i])) return rc;
+  if (bad_alias(oy_f32, n, ox_f32, n) || bad_alias(oy_f32, n, oo_f32, n))
+    return fail(ctx, Q8_ERR_ARG, "q8_res_add: y partially overlaps an input");
+  if (ctx->host_only) return fail(ctx, Q8_ERR_NODEVICE, "q8_res_add: host-only context");
+  if (n == 0) return ok(ctx);
+  if (int rc = set_device(ctx)) return rc;
+  hipError_t e = q8::launch_res_add(fptr(a, ox_f32), fptr(a, oo_f32), fptr(a, oy_f32), n,
+                                    ctx->stream);
+  if (e != hipSuccess) return hip_fail(ctx, e, "q8_res_add launch");
+  return ok(ctx);
+}
+
+int q8_add(q8_ctx *ctx, q8_buf *a, uint64_t ox_f32, uint64_t oy_f32, int64_t n) {
+  if (int rc = check_ctx(ctx)) return rc;
+  if (!a) return fail(ctx, Q8_ERR_ARG, "q8_add: null buffer");
+  if (n < 0) return fail(ctx, Q8_ERR_SHAPE, "q8_add: n=%lld", (long long)n);
+  if (int rc = check_f32(ctx, a, ox_f32, (uint64_t)n, "q8_add", "x")) return rc;
+  if (int rc = check_f32(ctx, a, oy_f32, (uint64_t)n, "q8_add", "y")) return rc;
+  if (bad_alias(oy_f32, n, ox_f32, n))
+    return fail(ctx, Q8_ERR_ARG, "q8_add: y partially overlaps x");
+  if (ctx->host_only) return fail(ctx, Q8_ERR_NODEVICE, "q8_add: host-only context");
+  if (n == 0) return ok(ctx);
+  if (int rc = set_device(ctx)) return rc;
+  hipError_t e = q8::launch_add(fptr(a, ox_f32), fptr(a, oy_f32), n, ctx->stream);
+  if (e != hipSuccess) return hip_fail(ctx, e, "q8_add launch");
+  return ok(ctx);
+}
+
+int q8_argmax(q8_ctx *ctx, q8_buf *a, uint64_t ox_f32, int64_t n, q8_buf *ids, uint64_t oid_i32) {
+  if (int rc = check_ctx(ctx)) return rc;
+  if (!a || !ids) return fail(ctx, Q8_ERR_ARG, "q8_argmax: null buffer");
+  if (n <= 0 || n > INT32_MAX) return fail(ctx, Q8_ERR_SHAPE, "q8_argmax: n=%lld", (long long)n);
+  if (int rc = check_f32(ctx, a, ox_f32, (uint64_t)n, "q8_argmax", "x")) return rc;
+  if (!fits(oid_i32, 1, 4, ids->size))
+    return fail(ctx, Q8_ERR_RANGE, "q8_argmax: id offset exceeds its buffer");
+  if (ctx->host_only) return fail(ctx, Q8_ERR_NODEVICE, "q8_argmax: host-only context");
+  if (int rc = set_device(ctx)) return rc;
+  hipError_t e = q8::launch_argmax(fptr(a, ox_f32), n,
+                                   reinterpret_cast<int32_t *>(bytes(ids, oid_i32 * 4)),
+                                   ctx->stream);
+  if (e != hipSuccess) return hip_fail(ctx, e, "q8_argmax launch");
+  return ok(ctx);
+}
+
+int q8_pos_advance(q8_ctx *ctx, q8_buf *posbuf, uint64_t opos_i32, int64_t s) {
+  if (int rc = check_ctx(ctx)) return rc;
+  if (!posbuf) return fail(ctx, Q8_ERR_ARG, "q8_pos_advance: null buffer");
+  if (s < 0 || s > INT32_MAX) return fail(ctx, Q8_ERR_SHAPE, "q8_pos_advance: s=%lld", (long long)s);
+  if (!fits(opos_i32, 1, 4, posbuf->size))
+    return fail(ctx, Q8_ERR_RANGE, "q8_pos_advance: offset exceeds its buffer");
+  if (ctx->host_only) return fail(ctx, Q8_ERR_NODEVICE, "q8_pos_advance: host-only context");
+  if (int rc = set_device(ctx)) return rc;
+  hipError_t e = q8::launch_pos_advance(reinterpret_cast<int *>(bytes(posbuf, opos_i32 * 4)),
+                                        (int)s, ctx->stream);
+  if (e != hipSuccess) return hip_fail(ctx, e, "q8_pos_advance launch");
   return ok(ctx);
 }
 

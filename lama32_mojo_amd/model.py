@@ -1,0 +1,406 @@
+"""Q8 Llama-family model runner on libq8hip (decode and prefill).
+
+Host side of the reference's Q8 model: configuration, weight-arena layout,
+the layer runner and the token loop, driving only libq8hip.so entry points:
+
+  Config, make_config             src/llama_common.mojo:27-52, src/llama_gpu.mojo:29-31
+  llama3_inv_freq                 src/llama_common.mojo:618-633
+  weight_names                    src/llama_gpu.mojo:33-47
+  LayerOffs                       src/llama_common.mojo:55-67
+  Q8Llama.layer (run_layer_q8)    src/llama_q8.mojo:144-230
+  Q8Llama.forward / forward_argmax  qwen3_mojo/src/qwen_q8.mojo:127-162
+  Q8Llama.embed                   qwen3_mojo/src/qwen_q8.mojo:110-124
+
+Differences from the reference host, on purpose:
+  * the KV cache is a binary16 buffer of its own (layers x {K, V} x maxlen x
+    kv_dim) rather than f32 blocks of the activation arena;
+  * residual add + post-attention RMSNorm run as one dispatch;
+  * a decode step can be captured once as a HIP graph that reads the token id
+    and the position from device memory and writes the argmax id and the next
+    position back, so generation replays one graph per token.
+"""
+
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass
+from typing import Mapping, Sequence
+
+import numpy as np
+
+from . import q8hip
+from .q8 import PAD, Acts, Q8Kernels, Weights, q8_rowstride
+from .q8hip import Buffer, Context
+
+
+@dataclass(frozen=True)
+class Config:
+    """Model dimensions (src/llama_common.mojo:27-52)."""
+    hidden: int
+    layers: int
+    n_heads: int
+    n_kv: int
+    head_dim: int
+    inter: int
+    vocab: int
+    eps: float
+    theta: float
+    rope_factor: float
+    low_ff: float
+    high_ff: float
+    orig_ctx: float
+    tied: bool = True          # lm_head = packed embed_tokens (Llama-3.2 / Qwen3 Q8 path)
+    name: str = "llama"
+
+    def group(self) -> int:
+        return self.n_heads // self.n_kv
+
+    def q_dim(self) -> int:
+        return self.n_heads * self.head_dim
+
+    def kv_dim(self) -> int:
+        return self.n_kv * self.head_dim
+
+    def half(self) -> int:
+        return self.head_dim // 2
+
+
+# Llama-3.2-1B (src/llama_gpu.mojo:29-31)
+LLAMA_32_1B = Config(2048, 16, 32, 8, 64, 8192, 128256, 1e-5, 500000.0, 32.0, 1.0, 4.0, 8192.0,
+                     tied=True, name="Llama-3.2-1B")
+# Llama-3.1-8B (llama31_mojo/src/llama_gpu.mojo:26-41: untied lm_head)
+LLAMA_31_8B = Config(4096, 32, 32, 8, 128, 14336, 128256, 1e-5, 500000.0, 8.0, 1.0, 4.0, 8192.0,
+                     tied=False, name="Llama-3.1-8B")
+
+
+def llama3_inv_freq(cfg: Config) -> np.ndarray:
+    """Per-dim RoPE inverse frequencies with llama3 wavelength scaling,
+    evaluated in float64 and stored as f32."""
+    out = np.empty(cfg.half(), dtype=np.float32)
+    for d in range(cfg.half()):
+        inv = 1.0 / (cfg.theta ** (2.0 * d / cfg.head_dim))
+        wavelen = 2.0 * 3.14159265358979323846 / inv
+        scaled = inv
+        if wavelen >= cfg.orig_ctx / cfg.high_ff:
+            if wavelen > cfg.orig_ctx / cfg.low_ff:
+                scaled = inv / cfg.rope_factor
+            else:
+                smooth = (cfg.orig_ctx / wavelen - cfg.low_ff) / (cfg.high_ff - cfg.low_ff)
+                scaled = (1.0 - smooth) * inv / cfg.rope_factor + smooth * inv
+        out[d] = np.float32(scaled)
+    return out
+
+
+def weight_names(cfg: Config) -> list[str]:
+    """Arena order: embed, final norm, then per layer norms and projections
+    (q|k|v and gate|up contiguous, which lets s == 1 fuse them)."""
+    names = ["model.embed_tokens.weight", "model.norm.weight"]
+    for L in range(cfg.layers):
+        p = f"model.layers.{L}."
+        names += [p + "input_layernorm.weight", p + "post_attention_layernorm.weight",
+                  p + "self_attn.q_proj.weight", p + "self_attn.k_proj.weight",
+                  p + "self_attn.v_proj.weight", p + "self_attn.o_proj.weight",
+                  p + "mlp.gate_proj.weight", p + "mlp.up_proj.weight",
+                  p + "mlp.down_proj.weight"]
+    if not cfg.tied:
+        names.append("lm_head.weight")
+    return names
+
+
+def tensor_shapes(cfg: Config) -> dict[str, tuple]:
+    """name -> (n, m) for Q8 matrices, (d,) for bf16 norm vectors."""
+    H, QD, KVD, I = cfg.hidden, cfg.q_dim(), cfg.kv_dim(), cfg.inter
+    shapes = {"model.embed_tokens.weight": (cfg.vocab, H), "model.norm.weight": (H,)}
+    for L in range(cfg.layers):
+        p = f"model.layers.{L}."
+        shapes.update({
+            p + "input_layernorm.weight": (H,), p + "post_attention_layernorm.weight": (H,),
+            p + "self_attn.q_proj.weight": (QD, H), p + "self_attn.k_proj.weight": (KVD, H),
+            p + "self_attn.v_proj.weight": (KVD, H), p + "self_attn.o_proj.weight": (H, QD),
+            p + "mlp.gate_proj.weight": (I, H), p + "mlp.up_proj.weight": (I, H),
+            p + "mlp.down_proj.weight": (H, I)})
+    if not cfg.tied:
+        shapes["lm_head.weight"] = (cfg.vocab, H)
+    return shapes
+
+
+def arena_elems(cfg: Config, G: int, scale: str) -> int:
+    """u16 elements of the packed weight arena (PAD head included)."""
+    total = PAD
+    for name, sh in tensor_shapes(cfg).items():
+        total += sh[0] * q8_rowstride(sh[1], G, scale) if len(sh) == 2 else sh[0]
+    return total
+
+
+@dataclass(frozen=True)
+class LayerOffs:
+    """u16 offsets of one layer's tensors in the weight arena."""
+    q: int
+    k: int
+    v: int
+    o: int
+    gate: int
+    up: int
+    down: int
+    in_norm: int
+    post_norm: int
+
+
+class Q8Llama:
+    """A Llama-style model with Q8 linears resident on one GPU.
+
+    weights: name -> array of raw stored values (packed u16 rows [n, rs] for
+    matrices, bf16 bit patterns [d] for norms), or None to build random-init
+    weights on the GPU (bf16 ~ N(0, std) packed in place, norms ~ 1)."""
+
+    def __init__(self, ctx: Context, cfg: Config, maxlen: int, G: int = 64, scale: str = "f16",
+                 weights: Mapping[str, np.ndarray] | None = None, seed: int = 0,
+                 std: float = 0.02, act_floats: int | None = None, max_prefill: int = 1):
+        self.ctx, self.cfg, self.maxlen = ctx, cfg, int(maxlen)
+        self.G, self.scale = G, scale
+        self.qk = Q8Kernels(ctx, G, scale)
+        names = weight_names(cfg)
+        self.w = Weights(ctx, arena_elems(cfg, G, scale))
+        if weights is not None:
+            self.w.upload_all(weights, names)
+        else:
+            self._random_weights(names, seed, std)
+        self.lo = []
+        for L in range(cfg.layers):
+            p = f"model.layers.{L}."
+            o = self.w.o
+            self.lo.append(LayerOffs(o(p + "self_attn.q_proj.weight"), o(p + "self_attn.k_proj.weight"),
+                                     o(p + "self_attn.v_proj.weight"), o(p + "self_attn.o_proj.weight"),
+                                     o(p + "mlp.gate_proj.weight"), o(p + "mlp.up_proj.weight"),
+                                     o(p + "mlp.down_proj.weight"), o(p + "input_layernorm.weight"),
+                                     o(p + "post_attention_layernorm.weight")))
+        H, QD, KVD, I = cfg.hidden, cfg.q_dim(), cfg.kv_dim(), cfg.inter
+        if act_floats is None:
+            # two residual rows sets, one layer's temporaries (the arena is
+            # reset after every layer), the head, and room for one captured
+            # decode step besides a forward pass
+            s = max(1, int(max_prefill))
+            att = q8hip.attention_scratch_floats(min(s, self.ATT_ROWS), cfg.n_heads, cfg.head_dim,
+                                                 self.maxlen)
+            layer = s * (4 * H + 2 * QD + 2 * KVD + 2 * I) + att
+            one = 2 * s * H + layer + H + cfg.vocab + 64
+            act_floats = PAD + cfg.half() + one + (2 * H + (4 * H + 2 * QD + 2 * KVD + 2 * I)
+                                                   + q8hip.attention_scratch_floats(
+                                                       1, cfg.n_heads, cfg.head_dim, self.maxlen)
+                                                   + H + cfg.vocab + 64)
+        self.a = Acts(ctx, act_floats)
+        self.oinv = self.a.alloc(cfg.half())
+        self.a.write(self.oinv, llama3_inv_freq(cfg))
+        kvd = cfg.kv_dim()
+        self.kv = Buffer.alloc(ctx, 2 * cfg.layers * 2 * self.maxlen * kvd)
+        self.okc = [(2 * L) * self.maxlen * kvd for L in range(cfg.layers)]
+        self.ovc = [(2 * L + 1) * self.maxlen * kvd for L in range(cfg.layers)]
+        self.ids = Buffer.alloc(ctx, 4 * max(self.maxlen, 16))
+        self.posbuf = Buffer.alloc(ctx, 16)
+        self.posbuf.upload(np.zeros(4, dtype=np.int32))
+        self.n_cached = 0
+        self.graph = None
+        self.graph_logits = None
+
+    # ---- weights -------------------------------------------------------------
+    def _random_weights(self, names: Sequence[str], seed: int, std: float) -> None:
+        import torch
+
+        cfg, G, scale = self.cfg, self.G, self.scale
+        shapes = tensor_shapes(cfg)
+        top = self.w.top
+        for i, name in enumerate(names):
+            sh = shapes[name]
+            self.w.offs[name] = top
+            gen = torch.Generator(device="cuda")
+            gen.manual_seed(seed * 100003 + i)
+            if len(sh) == 1:
+                t = (1.0 + 0.1 * torch.randn(sh, device="cuda", generator=gen)).to(torch.bfloat16)
+                torch.cuda.synchronize()
+                src = Buffer.wrap(self.ctx, t.data_ptr(), t.numel() * 2)
+                self._upload_from_device(src, top, t.numel())
+                top += sh[0]
+            else:
+                n, m = sh
+                t = (torch.randn((n, m), device="cuda", generator=gen) * std).to(torch.bfloat16)
+                torch.cuda.synchronize()
+                src = Buffer.wrap(self.ctx, t.data_ptr(), t.numel() * 2)
+                q8hip.quantize_pack(self.ctx, src, 0, q8hip.Q8_SRC_BF16, n, m, self.w.buf, top,
+                                    G, scale)
+                self.ctx.sync()
+                src.free()
+                top += n * q8_rowstride(m, G, scale)
+            del t
+        self.w.top = top
+
+    def _upload_from_device(self, src: Buffer, off_u16: int, count: int) -> None:
+        host = src.download((count,), np.uint16)
+        src.free()
+        self.w.buf.upload(host, 2 * off_u16)
+
+    # ---- layer runner (run_layer_q8) ---------------------------------------
+    ATT_ROWS = 256      # query rows per attention call (bounds the scratch)
+
+    def linear(self, ox: int, s: int, m: int, owt: int, n: int) -> int:
+        oy = self.a.alloc(s * n)
+        q8hip.linear(self.ctx, self.w.buf, owt, self.a.buf, ox, oy, s, m, n, self.G, self.scale)
+        return oy
+
+    def layer(self, L: int, ox: int, s: int, pos0: int, device_pos: bool = False,
+              oh: int | None = None) -> int:
+        """One block on the s rows at ox; the new residual rows go to oh
+        (allocated here when None); returns oh."""
+        cfg, ctx, a, w = self.cfg, self.ctx, self.a, self.w
+        lo = self.lo[L]
+        H, QD, KVD, I = cfg.hidden, cfg.q_dim(), cfg.kv_dim(), cfg.inter
+        rsH = q8_rowstride(H, self.G, self.scale)
+        pb = self.posbuf if device_pos else None
+        xn = a.alloc(s * H)
+        q8hip.rmsnorm(ctx, w.buf, lo.in_norm, a.buf, ox, xn, s, H, cfg.eps)
+        if s == 1 and lo.k == lo.q + QD * rsH and lo.v == lo.k + KVD * rsH:
+            oq = self.linear(xn, 1, H, lo.q, QD + 2 * KVD)
+            okk, ov = oq + QD, oq + QD + KVD
+        else:
+            oq = self.linear(xn, s, H, lo.q, QD)
+            okk = self.linear(xn, s, H, lo.k, KVD)
+            ov = self.linear(xn, s, H, lo.v, KVD)
+        q8hip.rope_kv(ctx, a.buf, oq, okk, ov, self.oinv, self.kv, self.okc[L], self.ovc[L],
+                      self.maxlen, s, pos0, cfg.n_heads, cfg.n_kv, cfg.head_dim, pb, 0)
+        oao = a.alloc(s * QD)
+        rows = min(s, self.ATT_ROWS)
+        osc = a.alloc(q8hip.attention_scratch_floats(rows, cfg.n_heads, cfg.head_dim, self.maxlen))
+        for r0 in range(0, s, rows):
+            r = min(rows, s - r0)
+            q8hip.attention(ctx, a.buf, oq + r0 * QD, self.kv, self.okc[L], self.ovc[L],
+                            self.maxlen, oao + r0 * QD, osc, r, pos0 + r0, cfg.n_heads, cfg.n_kv,
+                            cfg.head_dim, pb, 0)
+        oo = self.linear(oao, s, QD, lo.o, H)
+        if oh is None:
+            oh = a.alloc(s * H)
+        oz = a.alloc(s * H)
+        q8hip.add_rmsnorm(ctx, w.buf, lo.post_norm, a.buf, ox, oo, oh, oz, s, H, cfg.eps)
+        if s == 1 and lo.up == lo.gate + I * rsH:
+            og = self.linear(oz, 1, H, lo.gate, 2 * I)
+            ou = og + I
+        else:
+            og = self.linear(oz, s, H, lo.gate, I)
+            ou = self.linear(oz, s, H, lo.up, I)
+        q8hip.swiglu(ctx, a.buf, og, ou, s * I)
+        om = self.linear(og, s, I, lo.down, H)
+        q8hip.add(ctx, a.buf, om, oh, s * H)
+        return oh
+
+    # ---- token loop ----------------------------------------------------------
+    def embed(self, s: int) -> int:
+        """Gather s embedding rows for the ids already in self.ids."""
+        cfg = self.cfg
+        ox = self.a.alloc(s * cfg.hidden)
+        q8hip.embed_gather(self.ctx, self.w.buf, self.w.o("model.embed_tokens.weight"), self.ids, 0,
+                           self.a.buf, ox, s, cfg.hidden, cfg.vocab, self.G, self.scale)
+        return ox
+
+    def _head(self, oh: int, s: int) -> int:
+        cfg = self.cfg
+        onrm = self.a.alloc(cfg.hidden)
+        q8hip.rmsnorm(self.ctx, self.w.buf, self.w.o("model.norm.weight"), self.a.buf,
+                      oh + (s - 1) * cfg.hidden, onrm, 1, cfg.hidden, cfg.eps)
+        head = "model.embed_tokens.weight" if cfg.tied else "lm_head.weight"
+        return self.linear(onrm, 1, cfg.hidden, self.w.o(head), cfg.vocab)
+
+    def _run(self, s: int, pos0: int, device_pos: bool) -> int:
+        cur = self.embed(s)
+        nxt = self.a.alloc(s * self.cfg.hidden)
+        for L in range(self.cfg.layers):
+            mark = self.a.mark()
+            self.layer(L, cur, s, pos0, device_pos, oh=nxt)
+            self.a.reset(mark)
+            cur, nxt = nxt, cur
+        return self._head(cur, s)
+
+    def _check_room(self, s: int) -> None:
+        if self.n_cached + s > self.maxlen:
+            raise RuntimeError("KV cache full")
+
+    def forward(self, ids: Sequence[int]) -> np.ndarray:
+        """Logits (f32 [vocab]) of the last of `ids`, appending them to the cache."""
+        s = len(ids)
+        self._check_room(s)
+        self.ids.upload(np.asarray(ids, dtype=np.int32))
+        mark = self.a.mark()
+        olg = self._run(s, self.n_cached, False)
+        logits = self.a.read(olg, self.cfg.vocab)
+        self.a.reset(mark)
+        self.n_cached += s
+        self.posbuf.upload(np.array([self.n_cached], dtype=np.int32))
+        return logits
+
+    def forward_argmax(self, ids: Sequence[int]) -> int:
+        """Greedy next id after `ids` (GPU argmax, 4-byte readback)."""
+        s = len(ids)
+        self._check_room(s)
+        self.ids.upload(np.asarray(ids, dtype=np.int32))
+        mark = self.a.mark()
+        olg = self._run(s, self.n_cached, False)
+        q8hip.argmax(self.ctx, self.a.buf, olg, self.cfg.vocab, self.ids, 0)
+        nxt = int(self.ids.download((1,), np.int32)[0])
+        self.a.reset(mark)
+        self.n_cached += s
+        self.posbuf.upload(np.array([self.n_cached], dtype=np.int32))
+        return nxt
+
+    # ---- captured decode step -------------------------------------------------
+    def capture_decode(self) -> None:
+        """Capture one decode step as a HIP graph: read ids[0] and the device
+        position, run every layer, write argmax -> ids[0], position += 1."""
+        if self.graph is not None:
+            return
+        ctx = self.ctx
+        mark = self.a.mark()
+        self.ctx.graph_begin()
+        try:
+            olg = self._run(1, 0, True)
+            q8hip.argmax(ctx, self.a.buf, olg, self.cfg.vocab, self.ids, 0)
+            q8hip.pos_advance(ctx, self.posbuf, 0, 1)
+        finally:
+            self.graph = self.ctx.graph_end()
+        self.graph_logits = olg
+        self.graph_mark = mark
+        # the captured step owns its arena slice for the model's lifetime
+
+    def decode_steps(self, first_id: int, n: int) -> list[int]:
+        """Greedy-decode n tokens starting from first_id at the current
+        position by replaying the captured step; returns the n ids."""
+        if self.n_cached + n > self.maxlen:
+            raise RuntimeError("KV cache full")
+        self.capture_decode()
+        self.ids.upload(np.array([first_id], dtype=np.int32))
+        self.posbuf.upload(np.array([self.n_cached], dtype=np.int32))
+        out = []
+        for _ in range(n):
+            self.graph.launch()
+            out.append(int(self.ids.download((1,), np.int32)[0]))
+        self.n_cached += n
+        return out
+
+    def decode_steps_nosync(self, first_id: int, n: int) -> None:
+        """n replays of the captured step without host readback (timing)."""
+        if self.n_cached + n > self.maxlen:
+            raise RuntimeError("KV cache full")
+        self.capture_decode()
+        self.ids.upload(np.array([first_id], dtype=np.int32))
+        self.posbuf.upload(np.array([self.n_cached], dtype=np.int32))
+        for _ in range(n):
+            self.graph.launch()
+        self.n_cached += n
+
+    def reset(self) -> None:
+        """Forget the cached context (positions restart at 0)."""
+        self.n_cached = 0
+        self.posbuf.upload(np.zeros(4, dtype=np.int32))
+
+    def close(self) -> None:
+        if self.graph is not None:
+            self.graph.destroy()
+            self.graph = None
+        for b in (self.w.buf, self.a.buf, self.kv, self.ids, self.posbuf):
+            b.free()

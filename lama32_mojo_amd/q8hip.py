@@ -69,6 +69,19 @@ SIGNATURES = {
     "q8_linear": (_I, [_P, _P, _U64, _P, _U64, _U64, _I64, _I64, _I64, _I, _I]),
     "q8_linear_bf16act": (_I, [_P, _P, _U64, _P, _U64, _P, _U64, _I64, _I64, _I64, _I, _I]),
     "q8_embed_gather": (_I, [_P, _P, _U64, _P, _U64, _P, _U64, _I64, _I64, _I64, _I, _I]),
+    "q8_rmsnorm": (_I, [_P, _P, _U64, _P, _U64, _U64, _I64, _I64, ctypes.c_float]),
+    "q8_add_rmsnorm": (_I, [_P, _P, _U64, _P, _U64, _U64, _U64, _U64, _I64, _I64,
+                           ctypes.c_float]),
+    "q8_rope_kv": (_I, [_P, _P, _U64, _U64, _U64, _U64, _P, _U64, _U64, _I64, _I64, _I64, _P,
+                       _U64, _I, _I, _I]),
+    "q8_attention_scratch_floats": (_U64, [_I64, _I, _I, _I64]),
+    "q8_attention": (_I, [_P, _P, _U64, _P, _U64, _U64, _I64, _U64, _U64, _I64, _I64, _P, _U64,
+                         _I, _I, _I]),
+    "q8_swiglu": (_I, [_P, _P, _U64, _U64, _I64]),
+    "q8_res_add": (_I, [_P, _P, _U64, _U64, _U64, _I64]),
+    "q8_add": (_I, [_P, _P, _U64, _U64, _I64]),
+    "q8_argmax": (_I, [_P, _P, _U64, _I64, _P, _U64]),
+    "q8_pos_advance": (_I, [_P, _P, _U64, _I64]),
     "q8_graph_begin": (_I, [_P]),
     "q8_graph_end": (_I, [_P, ctypes.POINTER(_P)]),
     "q8_graph_launch": (_I, [_P, _P]),
@@ -252,3 +265,64 @@ def embed_gather(ctx: Context, w: Buffer, oemb_u16: int, ids: Buffer, oids_i32: 
     ctx.check(ctx._lib.q8_embed_gather(ctx.h, w.h, int(oemb_u16), ids.h, int(oids_i32), a.h,
                                        int(oy_f32), int(s), int(d), int(vocab), int(G),
                                        scale_code(scale)))
+
+
+# ---- decode-step layer kernels ---------------------------------------------------
+
+def _h(buf):
+    return None if buf is None else buf.h
+
+
+def rmsnorm(ctx: Context, w: Buffer, owt_u16: int, a: Buffer, ox_f32: int, oy_f32: int,
+            rows: int, d: int, eps: float) -> None:
+    ctx.check(ctx._lib.q8_rmsnorm(ctx.h, w.h, int(owt_u16), a.h, int(ox_f32), int(oy_f32),
+                                  int(rows), int(d), float(eps)))
+
+
+def add_rmsnorm(ctx: Context, w: Buffer, owt_u16: int, a: Buffer, ox_f32: int, oo_f32: int,
+                oh_f32: int, oy_f32: int, rows: int, d: int, eps: float) -> None:
+    ctx.check(ctx._lib.q8_add_rmsnorm(ctx.h, w.h, int(owt_u16), a.h, int(ox_f32), int(oo_f32),
+                                      int(oh_f32), int(oy_f32), int(rows), int(d), float(eps)))
+
+
+def rope_kv(ctx: Context, a: Buffer, oq: int, ok: int, ov: int, oinv: int, kv: Buffer,
+            okc_f16: int, ovc_f16: int, maxlen: int, s: int, pos0: int, nheads: int, nkv: int,
+            head_dim: int, posbuf: Buffer | None = None, opos_i32: int = 0) -> None:
+    ctx.check(ctx._lib.q8_rope_kv(ctx.h, a.h, int(oq), int(ok), int(ov), int(oinv), kv.h,
+                                  int(okc_f16), int(ovc_f16), int(maxlen), int(s), int(pos0),
+                                  _h(posbuf), int(opos_i32), int(nheads), int(nkv),
+                                  int(head_dim)))
+
+
+def attention_scratch_floats(s: int, nheads: int, head_dim: int, maxlen: int) -> int:
+    return int(lib().q8_attention_scratch_floats(int(s), int(nheads), int(head_dim),
+                                                 int(maxlen)))
+
+
+def attention(ctx: Context, a: Buffer, oq: int, kv: Buffer, okc_f16: int, ovc_f16: int,
+              maxlen: int, oy: int, oscratch: int, s: int, pos0: int, nheads: int, nkv: int,
+              head_dim: int, posbuf: Buffer | None = None, opos_i32: int = 0) -> None:
+    ctx.check(ctx._lib.q8_attention(ctx.h, a.h, int(oq), kv.h, int(okc_f16), int(ovc_f16),
+                                    int(maxlen), int(oy), int(oscratch), int(s), int(pos0),
+                                    _h(posbuf), int(opos_i32), int(nheads), int(nkv),
+                                    int(head_dim)))
+
+
+def swiglu(ctx: Context, a: Buffer, og: int, ou: int, n: int) -> None:
+    ctx.check(ctx._lib.q8_swiglu(ctx.h, a.h, int(og), int(ou), int(n)))
+
+
+def res_add(ctx: Context, a: Buffer, ox: int, oo: int, oy: int, n: int) -> None:
+    ctx.check(ctx._lib.q8_res_add(ctx.h, a.h, int(ox), int(oo), int(oy), int(n)))
+
+
+def add(ctx: Context, a: Buffer, ox: int, oy: int, n: int) -> None:
+    ctx.check(ctx._lib.q8_add(ctx.h, a.h, int(ox), int(oy), int(n)))
+
+
+def argmax(ctx: Context, a: Buffer, ox: int, n: int, ids: Buffer, oid_i32: int) -> None:
+    ctx.check(ctx._lib.q8_argmax(ctx.h, a.h, int(ox), int(n), ids.h, int(oid_i32)))
+
+
+def pos_advance(ctx: Context, posbuf: Buffer, opos_i32: int, s: int) -> None:
+    ctx.check(ctx._lib.q8_pos_advance(ctx.h, posbuf.h, int(opos_i32), int(s)))
