@@ -1,21 +1,23 @@
 #!/usr/bin/env python3
-"""Benchmark of the Q8 (INT8 group-quantized, W8A32) linear path on one MI355X.
+"""Benchmark of the Q8 (INT8 group-quantized, W8A32) path on one MI355X.
 
-Default workload -- Llama-3.2-1B decode step, batch 1: every Q8 linear of
-one decode step, as run_layer_q8 issues them (src/llama_q8.mojo:159-225,
-qwen3_mojo/src/qwen_q8.mojo:139-145):
-    16 layers x [ fused q|k|v 2048->3072, o 2048->2048,
-                  fused gate|up 2048->16384, down 8192->2048 ]
-    + tied lm_head 2048->128256
-= 65 Q8 GEMVs streaming 1.274 GB of packed weights (G=64, f16 scales).
-Weights are random bf16 ~N(0, 0.02) per tensor, packed on the GPU by
-q8_quantize_pack into one weight arena (PAD head, tensors contiguous, so
-q|k|v and gate|up run fused); activations are synthetic ~N(0, 1).
+Default workload -- Llama-3.2-1B decode step, batch 1, at a KV context of
+1024 tokens: the whole token step of the reference's Q8 model
+(qwen3_mojo/src/qwen_q8.mojo:127-162 with run_layer_q8,
+src/llama_q8.mojo:144-230) on libq8hip -- embedding gather, 16 layers of
+[rmsnorm, fused q|k|v GEMV 2048->3072, RoPE + fp16 KV append, attention,
+o GEMV 2048->2048, add + rmsnorm, fused gate|up GEMV 2048->16384, swiglu,
+down GEMV 8192->2048, add], final rmsnorm, tied lm_head GEMV 2048->128256 and
+argmax.  Weights are random bf16 ~N(0, 0.02) per tensor, packed on the GPU by
+q8_quantize_pack into one weight arena (G=64, f16 scales: the reference
+layout); norms ~1; the 1024-token KV context is random fp16.
 
-A step is one pass over all 65 GEMVs, replayed from one HIP graph.  `value`
-is weight-stream throughput in GB/s: algorithmic bytes per step
-(sum over GEMVs of n*(m + (m/G)*scale_bytes) + 4*s*m + 4*s*n) divided by the
-time per step (HIP events on the library's stream around K replays).
+A step is one token: one replay of a HIP graph that reads the token id and
+the position from device memory and writes the argmax id and the next
+position back.  `value` is the step's streaming throughput in GB/s: packed
+weight bytes (1.274 GB) plus the KV bytes read at the step's context length,
+divided by the time per token (HIP events on the library's stream around K
+replays); config.tok_s is tokens per second.
 
 `roofline` is for the lm_head GEMV (the largest launch, 128256 x 2048):
 its algorithmic bytes per launch divided by its average launch duration,
@@ -26,11 +28,12 @@ two copies of the table (542 MB, more than the 256 MB Infinity Cache).
 (oracle/q8_oracle.c, OpenMP) over the same packed weights on the host cores.
 
 Other workloads (--workload):
+  decode-linears  only the 65 Q8 GEMVs of the Llama-3.2-1B step, one graph
   linear   one Q8 linear 8192x2048, x f32 [1, 2048], weights rotated over
            >= 64 copies (>= 1.1 GB) so no launch reads a cached matrix
   prefill  Llama-3.2-1B prefill linears, M = 512 bf16 activations, all 16
-           layers x 7 unfused projections on the MFMA GEMM (TFLOP/s)
-  qwen8b   Qwen3-8B decode step, --batch 1 / 4 / 16
+           layers x 7 unfused projections on the MFMA GEMM (TFLOP/s), group 32
+  qwen8b   Qwen3-8B decode linears, --batch 1 / 4 / 16, group 32
 """
 
 from __future__ import annotations
@@ -62,7 +65,7 @@ def parse():
     p.add_argument("--steps", type=int, default=50)
     p.add_argument("--warmup", type=int, default=5)
     p.add_argument("--workload", default="decode",
-                   choices=["decode", "linear", "prefill", "qwen8b"])
+                   choices=["decode", "decode-linears", "linear", "prefill", "qwen8b"])
     p.add_argument("--layout", default=None, choices=["g64f16", "g32f32"],
                    help="packed layout (default: g64f16; g32f32 for --workload linear)")
     p.add_argument("--batch", type=int, default=1)
@@ -261,6 +264,100 @@ def run_decode(B: Bench, cfg):
 
 
 # ---------------------------------------------------------------------------
+# full decode step (Llama-3.2-1B model on the layer kernels, captured graph)
+# ---------------------------------------------------------------------------
+
+def run_decode_model(B: Bench, ctxlen: int = 1024):
+    from lama32_mojo_amd import model as gm
+
+    args, q8hip, ctx, torch = B.args, B.q8hip, B.ctx, B.torch
+    G, scale, sb = B.G, B.scale, B.sb
+    cfg = gm.LLAMA_32_1B
+    K, W = args.steps, args.warmup
+    maxlen = ctxlen + W + K + 8
+    m = gm.Q8Llama(ctx, cfg, maxlen, G, scale, seed=7)
+    # a context of ctxlen cached tokens: random binary16 K/V rows (their
+    # values do not change the work of a step)
+    kvd = cfg.kv_dim()
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(11)
+    kvt = torch.empty(2 * cfg.layers * maxlen * kvd, dtype=torch.float16, device="cuda")
+    kvt.normal_(generator=gen)
+    torch.cuda.synchronize()
+    src = q8hip.Buffer.wrap(ctx, kvt.data_ptr(), kvt.numel() * 2)
+    # copy through the host once (the cache is a library buffer)
+    m.kv.upload(src.download((kvt.numel(),), np.float16))
+    src.free()
+    del kvt
+    m.n_cached = ctxlen
+    m.capture_decode()
+    m.ids.upload(np.array([128000 % cfg.vocab], dtype=np.int32))
+    m.posbuf.upload(np.array([ctxlen], dtype=np.int32))
+    ms, wall = B.time_steps(lambda: m.graph.launch(), K, W)
+    pos_end = int(m.posbuf.download((1,), np.int32)[0])
+    assert pos_end == ctxlen + W + K, pos_end
+    weight_bytes = 2 * (m.w.top - 32)
+    mean_ctx = ctxlen + W + (K + 1) / 2.0
+    kv_bytes = int(cfg.layers * 2 * mean_ctx * kvd * 2)
+    step_bytes = weight_bytes + kv_bytes
+    value = step_bytes / (ms * 1e-3) / 1e9
+    tok_s = 1000.0 / ms
+
+    # roofline kernel: the lm_head GEMV (tied embed table), back-to-back over
+    # two copies so the 256 MB MALL cannot serve it
+    n_h, m_h = cfg.vocab, cfg.hidden
+    w2, offs2 = B.pack_arena([(n_h, m_h), (n_h, m_h)], [5, 6])
+    xa = B.activations(32 + m_h + n_h, 1)
+    a = q8hip.Buffer.wrap(ctx, xa.data_ptr(), 4 * (32 + m_h + n_h))
+    heads = [(lambda o=o: q8hip.linear(ctx, w2, o, a, 32, 32 + m_h, 1, m_h, n_h, G, scale))
+             for o in offs2]
+    kk = max(K, 20)
+    head_ms, _ = B.time_steps(lambda: [h() for h in heads], kk // 2, 2)
+    head_ms /= 2
+    head_bytes = linear_bytes(1, m_h, n_h, G, sb)
+    achieved = head_bytes / (head_ms * 1e-3) / 1e9
+    w2.free()
+
+    cpu = None
+    if not args.no_cpu:
+        lo = m.lo[0]
+        H, QD, KVD, I = cfg.hidden, cfg.q_dim(), cfg.kv_dim(), cfg.inter
+        packs = []
+        for off, n, mm in [(lo.q, QD + 2 * KVD, H), (lo.o, H, QD), (lo.gate, 2 * I, H),
+                           (lo.down, H, I), (m.w.o("model.embed_tokens.weight"), n_h, m_h)]:
+            rs = q8hip.rowstride_u16(mm, G, scale)
+            packs.append((m.w.buf.download((n, rs), np.uint16, 2 * off), 1, mm))
+        cpu = cpu_baseline(packs, G, scale, args.cpu_seconds,
+                           "(layer-0 q|k|v, o, gate|up, down + lm_head)")
+    m.close()
+    return {
+        "metric": f"Q8 GEMV GB/s (% of HBM peak); decode tok/s batch 1, {cfg.name} Q8",
+        "value": round(value, 1),
+        "unit": "GB/s",
+        "ms_per_step": round(ms, 4),
+        "higher_is_better": True,
+        "dtype": "int8xf32",
+        "data": "synthetic (random-init N(0,0.02) bf16 weights packed on GPU, norms ~1; "
+                "random fp16 KV context)",
+        "config": {"workload": f"{cfg.name} decode step batch 1 at KV context {ctxlen}: "
+                               f"embedding gather, {cfg.layers} layers (rmsnorm, fused q|k|v "
+                               "GEMV, RoPE + fp16 KV append, attention, o GEMV, add+rmsnorm, "
+                               "fused gate|up GEMV, swiglu, down GEMV, add), final norm, "
+                               f"lm_head GEMV {n_h}x{m_h}, argmax; one HIP graph per token",
+                   "layout": f"G={G} {scale} scales", "batch": 1, "tok_s": round(tok_s, 1),
+                   "weight_bytes_per_token": weight_bytes, "kv_bytes_per_token": kv_bytes,
+                   "pct_hbm_peak": round(100 * value / HBM_PEAK_GBS, 1),
+                   "graph": True, "wall_s": round(wall, 3)},
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+                     "traffic": None,
+                     "kernel": f"lm_head GEMV {n_h}x{m_h}: {head_bytes} B/launch, "
+                               f"{head_ms * 1e3:.2f} us avg over {kk} launches"},
+        "cpu_baseline": cpu,
+    }
+
+
+# ---------------------------------------------------------------------------
 # single linear (8192 x 2048, rotated copies)
 # ---------------------------------------------------------------------------
 
@@ -398,12 +495,16 @@ def main():
                                    "GPU; multi-GPU runs are not part of this build"}))
         sys.exit(2)
     if args.layout is None:
-        args.layout = "g32f32" if args.workload == "linear" else "g64f16"
+        # the reference layout for the Llama-3.2-1B decode step; group 32
+        # with f32 scales where the workload is defined with it
+        args.layout = "g64f16" if args.workload in ("decode", "decode-linears") else "g32f32"
     import torch
     from lama32_mojo_amd import q8hip
     ctx = q8hip.Context(0)
     B = Bench(args, ctx, torch)
     if args.workload == "decode":
+        res = run_decode_model(B)
+    elif args.workload == "decode-linears":
         res = run_decode(B, LLAMA_1B)
     elif args.workload == "qwen8b":
         res = run_decode(B, QWEN3_8B)

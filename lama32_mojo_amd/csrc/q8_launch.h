@@ -74,6 +74,32 @@ struct AttnArgs {
 // Causal GQA attention of s query rows at positions pos0 .. pos0+s-1 over
 // cache rows 0 .. pos0+i; nsplit = ceil(maxlen / 64).
 hipError_t launch_attention(const AttnArgs &a, hipStream_t st);
+struct DecodeAttnArgs {
+  const float *q, *k, *v;  // one new token: q [nheads*hd], k, v [nkv*hd] (unrotated)
+  const float *inv;        // head_dim / 2 inverse frequencies
+  __half *kc, *vc;         // cache blocks [maxlen, nkv*hd]
+  float *out;              // [nheads*hd]
+  float *part;             // scratch: nsplit * nheads * (hd + 2) floats
+  int nheads, nkv, head_dim, nsplit;
+  const int *posp;         // device position (or null: pos0)
+  int pos0, maxlen;
+};
+// RoPE of q and k, append of k and v at cache row pos0 and attention of the
+// one new token over rows 0 .. pos0: one launch of nsplit x nkv blocks over
+// context splits, then a merge launch.  Calls that share `part` must not
+// overlap.
+// Keys per chunk (one wave's unit of work) and the split count: one chunk
+// per block up to 32 chunks of context, then more chunks per block.  Every
+// launched block reads the position before it can leave, so more splits
+// than that cost more than they save (measured at 1024 and 2304 keys).
+constexpr int kDecodeAttnMaxSplit = 64;   // bound of the merge's LDS staging
+constexpr int decode_attn_chunk(int head_dim) { return head_dim > 64 ? 32 : 64; }
+inline int decode_attn_nsplit(int64_t maxlen, int head_dim) {
+  const int64_t kc = decode_attn_chunk(head_dim);
+  const int64_t n = (maxlen + kc - 1) / kc;
+  return (int)(n < 1 ? 1 : n > 32 ? 32 : n);
+}
+hipError_t launch_decode_attention(const DecodeAttnArgs &a, hipStream_t st);
 hipError_t launch_swiglu(float *g, const float *u, int64_t n, hipStream_t st);
 hipError_t launch_res_add(const float *x, const float *o, float *y, int64_t n, hipStream_t st);
 hipError_t launch_add(const float *x, float *y, int64_t n, hipStream_t st);

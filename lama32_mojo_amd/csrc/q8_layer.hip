@@ -38,6 +38,26 @@ __device__ __forceinline__ float wave_max(float v) {
   return fmaxf(fmaxf(a, b), fmaxf(c, d));
 }
 
+// cos and sin of a RoPE angle through one sincosf call, so every kernel that
+// rotates gets bit-identical values (separate cosf / sinf calls may be
+// lowered differently from one kernel to the next).
+__device__ __forceinline__ void rope_cs(float freq, float &c, float &sn) {
+  sincosf(freq, &sn, &c);
+}
+
+// RoPE of one pair, written with explicit FMAs so every kernel that rotates
+// (rope_kv_kernel, attn_decode_kernel) rounds identically.  The rotated pair
+// is pinned in f32 registers (empty asm): otherwise the compiler may merge
+// the last FMA with a later binary16 conversion (v_fma_mix*), rounding once
+// to f16 where another kernel rounds to f32 first.
+__device__ __forceinline__ void rotate(float x0, float x1, float c, float sn, float &y0, float &y1) {
+  float a = __builtin_fmaf(x0, c, -(x1 * sn));
+  float b = __builtin_fmaf(x1, c, x0 * sn);
+  __asm__ volatile("" : "+v"(a), "+v"(b));
+  y0 = a;
+  y1 = b;
+}
+
 // Sum over a 256-thread block (4 waves); every thread gets the total.
 __device__ __forceinline__ float block_sum256(float v, float *red) {
   v = wave_sum(v);
@@ -97,17 +117,19 @@ __global__ __launch_bounds__(256) void rope_kv_kernel(float *q, float *k, const 
     const int r = (int)(idx % (nall * half));
     const int h = r / half, d = r % half;
     const float freq = (float)(pos0 + i) * inv[d];
-    const float c = cosf(freq), sn = sinf(freq);
+    float c, sn;
+    rope_cs(freq, c, sn);
     if (h < nheads) {
       float *base = q + (int64_t)i * qdim + h * head_dim;
-      const float x0 = base[d], x1 = base[half + d];
-      base[d] = x0 * c - x1 * sn;
-      base[half + d] = x1 * c + x0 * sn;
+      float y0, y1;
+      rotate(base[d], base[half + d], c, sn, y0, y1);
+      base[d] = y0;
+      base[half + d] = y1;
     } else {
       const int hk = h - nheads;
       float *base = k + (int64_t)i * kvdim + hk * head_dim;
-      const float x0 = base[d], x1 = base[half + d];
-      const float y0 = x0 * c - x1 * sn, y1 = x1 * c + x0 * sn;
+      float y0, y1;
+      rotate(base[d], base[half + d], c, sn, y0, y1);
       base[d] = y0;
       base[half + d] = y1;
       const int64_t row = pos0 + i;
@@ -223,6 +245,297 @@ __global__ __launch_bounds__(64) void attn_combine_kernel(const float *__restric
     out[(int64_t)i * nheads * HD + h * HD + threadIdx.x + 64 * e] = o[e] * il;
 }
 
+// ---- decode attention: RoPE + KV append + attention of one new token --------
+// Sum over aligned groups of N consecutive lanes (N = 8 or 16), in every lane.
+template <int N>
+__device__ __forceinline__ float lane_group_sum(float v) {
+  v += dpp_mov<0xb1>(v);                    // quad_perm [1,0,3,2]
+  v += dpp_mov<0x4e>(v);                    // quad_perm [2,3,0,1]
+  v += dpp_mov<0x141>(v);                   // row_half_mirror
+  if constexpr (N == 16) v += dpp_mov<0x140>(v);   // row_mirror
+  return v;
+}
+
+// Grid (nsplit, nkv), 4 waves.  Block (split, g) serves KV head g and its GRP
+// query heads over the key chunks [split * cpb, (split + 1) * cpb) of 64
+// keys, cpb = max(waves per head, ceil(chunks / nsplit)).  A wave serves one
+// query head (two when GRP = 8; with GRP < 4 the waves of one head take
+// alternate chunks), so each wave's work per chunk is short and the block's
+// waves share the chunk's K and V rows through the cache.  Rows are read as
+// 16-byte pieces, HD/8 lanes per row (full 128- or 256-byte runs): a lane
+// multiplies its 8 dims of a key by the query and the row's lanes sum with
+// DPP; for P V a lane accumulates its 8 dims over its rows.  Online softmax
+// per wave; the block merges its waves (and their row slots) in LDS.  With
+// one active block per KV head the block writes the output; otherwise it
+// writes one partial record (o[HD], m, l) per head and attn_merge_kernel,
+// the next launch, merges the records.
+//
+// Every block rotates q and the new k itself and takes cache row pos0 from
+// LDS (rounded to binary16 exactly as cached); split 0 writes the new k and
+// v to cache row pos0, and no block reads that row from memory.  The first
+// chunk's loads are issued before the rotation.
+template <int HD, int GRP>
+__global__ __launch_bounds__(256) void attn_decode_kernel(
+    const float *__restrict__ q, const float *__restrict__ k, const float *__restrict__ v,
+    const float *__restrict__ inv, __half *__restrict__ kc, __half *__restrict__ vc,
+    float *__restrict__ part, float *__restrict__ out, int nkv, const int *posp, int pos0_host,
+    int maxlen) {
+  constexpr int KC = decode_attn_chunk(HD), NW = 4;
+  constexpr int LPR = HD / 8;           // lanes per row (8 dims each)
+  constexpr int RPI = 64 / LPR;         // rows per load instruction (row slots)
+  constexpr int NI = KC / RPI;          // load instructions per chunk
+  constexpr int half = HD / 2;
+  constexpr int PR = HD + 2;            // partial record per head: o[HD], m, l
+  constexpr int HS = GRP < NW ? GRP : NW;   // head slots per block
+  constexpr int HPW = GRP / HS;             // heads per wave
+  constexpr int WPH = NW / HS;              // waves per head
+  __shared__ float qs[GRP][HD];
+  __shared__ __align__(16) __half kn[HD], vn[HD];
+  __shared__ float ps[NW][HPW][64];
+  __shared__ float wm[NW][HPW], wl[NW][HPW];
+  __shared__ __align__(16) float wo[NW][HPW][RPI][HD];
+  const int split = blockIdx.x, g = blockIdx.y, nsplit = gridDim.x;
+  const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int hs = w % HS, kg = w / HS;
+  const int kvdim = nkv * HD;
+  const int rl = lane / LPR;            // row slot within an instruction's rows
+  const int dd = (lane % LPR) * 8;      // this lane's 8 dims
+  const uint32_t cache_bytes = (uint32_t)maxlen * (uint32_t)kvdim * 2u;
+  const rsrc_t krs = make_rsrc(kc, cache_bytes), vrs = make_rsrc(vc, cache_bytes);
+  // 8 binary16 values of row r at this lane's dims; rows past maxlen read as
+  // zeros (offset out of range)
+  auto row_off = [&](int r) -> uint32_t {
+    return r < maxlen ? ((uint32_t)r * (uint32_t)kvdim + (uint32_t)(g * HD + dd)) * 2u
+                      : kOutOfRange;
+  };
+  u32x4 kr[NI], vr[NI];
+  auto load_chunk = [&](int cc, bool with_v) {
+#pragma unroll
+    for (int u = 0; u < NI; ++u) kr[u] = bload16(krs, row_off(cc * KC + u * RPI + rl));
+    if (with_v) {
+#pragma unroll
+      for (int u = 0; u < NI; ++u) vr[u] = bload16(vrs, row_off(cc * KC + u * RPI + rl));
+    }
+  };
+  // The first chunk is loaded before the position is known, on the guess
+  // that the block spans WPH chunks (true while chunks <= nsplit * WPH).
+  const int c_guess = split * WPH + kg;
+  load_chunk(c_guess, true);
+
+  const int pos0 = posp ? *posp : pos0_host;
+  const bool room = pos0 < maxlen;
+  const int nctx = room ? pos0 + 1 : maxlen;
+  const int chunks = (nctx + KC - 1) / KC;
+  const int cpb = max(WPH, (chunks + nsplit - 1) / nsplit);
+  const int active = (chunks + cpb - 1) / cpb;
+  if (split >= active) return;
+  const int c_end = min((split + 1) * cpb, chunks);
+  int c = split * cpb + kg;
+  if (c != c_guess && c < c_end) load_chunk(c, true);
+  // row r as read, with rows past the context zeroed and row pos0 from LDS
+  auto fix_row = [&](u32x4 raw, const __half *fresh, int r) -> u32x4 {
+    if (r == pos0) return *reinterpret_cast<const u32x4 *>(fresh + dd);
+    return r < nctx ? raw : u32x4{0u, 0u, 0u, 0u};
+  };
+
+  // prologue: rotate the group's query heads and the new k; round k, v
+  for (int t = threadIdx.x; t < GRP * half; t += 256) {
+    const int hh = t / half, d = t % half;
+    const int h = g * GRP + hh;
+    float cs, sn;
+    rope_cs((float)pos0 * inv[d], cs, sn);
+    rotate(q[h * HD + d], q[h * HD + half + d], cs, sn, qs[hh][d], qs[hh][half + d]);
+  }
+  for (int d = threadIdx.x; d < half; d += 256) {
+    float cs, sn, r0, r1;
+    rope_cs((float)pos0 * inv[d], cs, sn);
+    rotate(k[g * HD + d], k[g * HD + half + d], cs, sn, r0, r1);
+    const __half y0 = __float2half_rn(r0), y1 = __float2half_rn(r1);
+    kn[d] = y0;
+    kn[half + d] = y1;
+    if (room && split == 0) {
+      kc[(int64_t)pos0 * kvdim + g * HD + d] = y0;
+      kc[(int64_t)pos0 * kvdim + g * HD + half + d] = y1;
+    }
+  }
+  for (int d = threadIdx.x; d < HD; d += 256) {
+    const __half y = __float2half_rn(v[g * HD + d]);
+    vn[d] = y;
+    if (room && split == 0) vc[(int64_t)pos0 * kvdim + g * HD + d] = y;
+  }
+  __syncthreads();
+
+  const float rd = sqrtf((float)HD);
+  float qv[HPW][8];
+#pragma unroll
+  for (int j = 0; j < HPW; ++j)
+#pragma unroll
+    for (int i = 0; i < 8; ++i) qv[j][i] = qs[hs + HS * j][dd + i];
+  float m_run[HPW], l_run[HPW], o_run[HPW][8];
+#pragma unroll
+  for (int j = 0; j < HPW; ++j) {
+    m_run[j] = -INFINITY;
+    l_run[j] = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) o_run[j][i] = 0.0f;
+  }
+
+  for (; c < c_end; c += WPH) {
+    const int j0 = c * KC;
+    // scores of the chunk's rows
+#pragma unroll
+    for (int u = 0; u < NI; ++u) {
+      const u32x4 kw = fix_row(kr[u], kn, j0 + u * RPI + rl);
+      const uint32_t rw[4] = {kw.x, kw.y, kw.z, kw.w};
+#pragma unroll
+      for (int j = 0; j < HPW; ++j) {
+        float dot = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float2 kf = __half22float2(__builtin_bit_cast(__half2, rw[i]));
+          dot = __builtin_fmaf(qv[j][2 * i], kf.x, dot);
+          dot = __builtin_fmaf(qv[j][2 * i + 1], kf.y, dot);
+        }
+        dot = lane_group_sum<LPR>(dot);
+        if (lane % LPR == 0) ps[w][j][u * RPI + rl] = dot / rd;
+      }
+    }
+    const int cn = c + WPH;             // this wave's next chunk
+    if (cn < c_end) load_chunk(cn, false);
+    __builtin_amdgcn_wave_barrier();
+    // softmax pieces: lane i < KC holds key j0 + i
+    const bool key_ok = lane < KC && j0 + lane < nctx;
+    float pnew[HPW], fa[HPW];
+#pragma unroll
+    for (int j = 0; j < HPW; ++j) {
+      const float sc = key_ok ? ps[w][j][lane] : -INFINITY;
+      const float mx = wave_max(sc);
+      const float p = key_ok ? expf(sc - mx) : 0.0f;
+      const float l = wave_sum(p);
+      const float mn = fmaxf(m_run[j], mx);
+      fa[j] = expf(m_run[j] - mn);
+      const float fb = expf(mx - mn);
+      l_run[j] = __builtin_fmaf(l_run[j], fa[j], l * fb);
+      m_run[j] = mn;
+      pnew[j] = p * fb;
+    }
+    __builtin_amdgcn_wave_barrier();
+#pragma unroll
+    for (int j = 0; j < HPW; ++j) ps[w][j][lane] = pnew[j];
+    __builtin_amdgcn_wave_barrier();
+    // P V: this lane's 8 dims over its rows of the chunk
+#pragma unroll
+    for (int j = 0; j < HPW; ++j)
+#pragma unroll
+      for (int i = 0; i < 8; ++i) o_run[j][i] *= fa[j];
+#pragma unroll
+    for (int u = 0; u < NI; ++u) {
+      const u32x4 vw = fix_row(vr[u], vn, j0 + u * RPI + rl);
+      const uint32_t rw[4] = {vw.x, vw.y, vw.z, vw.w};
+#pragma unroll
+      for (int j = 0; j < HPW; ++j) {
+        const float p = ps[w][j][u * RPI + rl];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float2 vf = __half22float2(__builtin_bit_cast(__half2, rw[i]));
+          o_run[j][2 * i] = __builtin_fmaf(p, vf.x, o_run[j][2 * i]);
+          o_run[j][2 * i + 1] = __builtin_fmaf(p, vf.y, o_run[j][2 * i + 1]);
+        }
+      }
+    }
+    if (cn < c_end) {
+#pragma unroll
+      for (int u = 0; u < NI; ++u) vr[u] = bload16(vrs, row_off(cn * KC + u * RPI + rl));
+    }
+    __builtin_amdgcn_wave_barrier();
+  }
+  // per wave: row-slot partial sums of o, and m, l (l = 0: no keys)
+#pragma unroll
+  for (int j = 0; j < HPW; ++j) {
+    float4 *dst = reinterpret_cast<float4 *>(&wo[w][j][rl][dd]);
+    dst[0] = make_float4(o_run[j][0], o_run[j][1], o_run[j][2], o_run[j][3]);
+    dst[1] = make_float4(o_run[j][4], o_run[j][5], o_run[j][6], o_run[j][7]);
+  }
+  if (lane == 0) {
+#pragma unroll
+    for (int j = 0; j < HPW; ++j) {
+      wm[w][j] = m_run[j];
+      wl[w][j] = l_run[j];
+    }
+  }
+  __syncthreads();
+  // the block's waves of each head -> one record per head
+  float *rec = part + ((int64_t)g * nsplit + split) * (GRP * PR);
+  for (int t = threadIdx.x; t < GRP * HD; t += 256) {
+    const int hh = t / HD, d = t % HD;
+    const int s0 = hh % HS, j = hh / HS;       // waves s0 + HS * x serve head hh
+    float mx = -INFINITY;
+#pragma unroll
+    for (int x = 0; x < WPH; ++x) mx = fmaxf(mx, wm[s0 + HS * x][j]);
+    float l = 0.0f, o = 0.0f;
+#pragma unroll
+    for (int x = 0; x < WPH; ++x) {
+      const int wx = s0 + HS * x;
+      if (wl[wx][j] == 0.0f) continue;
+      float os = 0.0f;
+#pragma unroll
+      for (int r = 0; r < RPI; ++r) os += wo[wx][j][r][d];
+      const float f = expf(wm[wx][j] - mx);
+      l = __builtin_fmaf(wl[wx][j], f, l);
+      o = __builtin_fmaf(os, f, o);
+    }
+    if (active == 1) {
+      out[(g * GRP + hh) * HD + d] = o / l;
+    } else {                             // merged by attn_merge_kernel
+      rec[hh * PR + d] = o;
+      if (d == 0) {
+        rec[hh * PR + HD] = mx;
+        rec[hh * PR + HD + 1] = l;
+      }
+    }
+  }
+}
+
+// Merge of the partial records of attn_decode_kernel: block h (256 threads)
+// stages head h's records of all nsplit splits in LDS (independent loads,
+// issued before the position is known), then thread d < HD forms o[d] / l
+// over the active splits.  Does nothing when one block per KV head was
+// active (it wrote the output itself).
+template <int HD, int GRP>
+__global__ __launch_bounds__(256) void attn_merge_kernel(const float *__restrict__ part,
+                                                         float *__restrict__ out, int nsplit,
+                                                         const int *posp, int pos0_host,
+                                                         int maxlen) {
+  constexpr int KC = decode_attn_chunk(HD), NW = 4;
+  constexpr int PR = HD + 2;
+  constexpr int WPH = NW / (GRP < NW ? GRP : NW);
+  __shared__ float rs[kDecodeAttnMaxSplit * PR];
+  const int h = blockIdx.x, g = h / GRP, hh = h % GRP;
+  const float *recs = part + (int64_t)g * nsplit * (GRP * PR) + hh * PR;
+  for (int t = threadIdx.x; t < nsplit * PR; t += 256) {
+    const int x = t / PR, e = t % PR;
+    rs[t] = recs[x * GRP * PR + e];
+  }
+  const int pos0 = posp ? *posp : pos0_host;
+  const int nctx = pos0 < maxlen ? pos0 + 1 : maxlen;
+  const int chunks = (nctx + KC - 1) / KC;
+  const int cpb = max(WPH, (chunks + nsplit - 1) / nsplit);
+  const int active = (chunks + cpb - 1) / cpb;
+  if (active <= 1) return;
+  __syncthreads();
+  for (int d = threadIdx.x; d < HD; d += 256) {
+    float mx = -INFINITY;
+    for (int x = 0; x < active; ++x) mx = fmaxf(mx, rs[x * PR + HD]);
+    float l = 0.0f, o = 0.0f;
+    for (int x = 0; x < active; ++x) {
+      const float f = expf(rs[x * PR + HD] - mx);
+      l = __builtin_fmaf(rs[x * PR + HD + 1], f, l);
+      o = __builtin_fmaf(rs[x * PR + d], f, o);
+    }
+    out[h * HD + d] = o / l;
+  }
+}
+
 // ---- elementwise (k_swiglu_mul, k_res_add, k_add) ----------------------------
 __global__ __launch_bounds__(256) void swiglu_kernel(float *g, const float *u, int64_t n) {
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -253,7 +566,20 @@ __global__ __launch_bounds__(1024) void argmax_kernel(const float *__restrict__ 
   __shared__ int32_t bi[16];
   float best = v[0];
   int32_t bidx = 0;
-  for (int64_t k = threadIdx.x; k < n; k += 1024) {
+  // 8 independent loads in flight per thread, then the scan in index order
+  int64_t k = threadIdx.x;
+  for (; k + 7 * 1024 < n; k += 8 * 1024) {
+    float x[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) x[u] = v[k + u * 1024];
+#pragma unroll
+    for (int u = 0; u < 8; ++u)
+      if (x[u] > best) {
+        best = x[u];
+        bidx = (int32_t)(k + u * 1024);
+      }
+  }
+  for (; k < n; k += 1024) {
     const float x = v[k];
     if (x > best) {
       best = x;
@@ -338,6 +664,33 @@ hipError_t launch_attention(const AttnArgs &a, hipStream_t st) {
   if (a.s == 0) return hipSuccess;
   if (a.head_dim == 64) return launch_attn_hd<64>(a, st);
   if (a.head_dim == 128) return launch_attn_hd<128>(a, st);
+  return hipErrorInvalidValue;
+}
+
+template <int HD, int GRP>
+hipError_t launch_decode_attn_t(const DecodeAttnArgs &a, hipStream_t st) {
+  hipLaunchKernelGGL((attn_decode_kernel<HD, GRP>), dim3((unsigned)a.nsplit, (unsigned)a.nkv),
+                     dim3(256), 0, st, a.q, a.k, a.v, a.inv, a.kc, a.vc, a.part, a.out, a.nkv,
+                     a.posp, a.pos0, a.maxlen);
+  hipLaunchKernelGGL((attn_merge_kernel<HD, GRP>), dim3((unsigned)a.nheads), dim3(256), 0, st,
+                     a.part, a.out, a.nsplit, a.posp, a.pos0, a.maxlen);
+  return hipGetLastError();
+}
+
+hipError_t launch_decode_attention(const DecodeAttnArgs &a, hipStream_t st) {
+  const int grp = a.nheads / a.nkv;
+  if (a.nsplit < 1 || a.nsplit > kDecodeAttnMaxSplit) return hipErrorInvalidValue;
+  if (a.head_dim == 64) {
+    if (grp == 1) return launch_decode_attn_t<64, 1>(a, st);
+    if (grp == 2) return launch_decode_attn_t<64, 2>(a, st);
+    if (grp == 4) return launch_decode_attn_t<64, 4>(a, st);
+    if (grp == 8) return launch_decode_attn_t<64, 8>(a, st);
+  } else if (a.head_dim == 128) {
+    if (grp == 1) return launch_decode_attn_t<128, 1>(a, st);
+    if (grp == 2) return launch_decode_attn_t<128, 2>(a, st);
+    if (grp == 4) return launch_decode_attn_t<128, 4>(a, st);
+    if (grp == 8) return launch_decode_attn_t<128, 8>(a, st);
+  }
   return hipErrorInvalidValue;
 }
 

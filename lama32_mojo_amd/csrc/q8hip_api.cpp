@@ -28,6 +28,8 @@ struct q8_ctx {
   // Split-K workspace of the prefill GEMM (partial sums).  A split only
   // happens while tiles x splits stay within 256 workgroups of 64 x 128
   // outputs, so 2 Mi floats always suffice; 4 Mi leaves room.
+  // The decode attention's partial records use it too: both run in stream
+  // order on this context.
   float *gemm_ws = nullptr;
 };
 
@@ -152,6 +154,7 @@ int q8_create(int device_ordinal, q8_ctx **out) {
       delete ctx;
       return fail(nullptr, Q8_ERR_NOMEM, "q8_create: cannot allocate the GEMM workspace");
     }
+
   }
   *out = ctx;
   return Q8_OK;
@@ -659,6 +662,67 @@ int q8_attention(q8_ctx *ctx, q8_buf *a, uint64_t oq_f32, q8_buf *kv, uint64_t o
   aa.maxlen = (int)maxlen;
   hipError_t e = q8::launch_attention(aa, ctx->stream);
   if (e != hipSuccess) return hip_fail(ctx, e, "q8_attention launch");
+  return ok(ctx);
+}
+
+int q8_decode_attention(q8_ctx *ctx, q8_buf *a, uint64_t oq_f32, uint64_t ok_f32,
+                        uint64_t ov_f32, uint64_t oinv_f32, q8_buf *kv, uint64_t okc_f16,
+                        uint64_t ovc_f16, int64_t maxlen, uint64_t oy_f32, int64_t pos0,
+                        q8_buf *posbuf, uint64_t opos_i32, int nheads, int nkv, int head_dim) {
+  if (int rc = check_ctx(ctx)) return rc;
+  if (!a || !kv) return fail(ctx, Q8_ERR_ARG, "q8_decode_attention: null buffer");
+  if (int rc = check_heads(ctx, nheads, nkv, head_dim, "q8_decode_attention")) return rc;
+  const int grp = nheads / nkv;
+  if ((head_dim != 64 && head_dim != 128) || (grp != 1 && grp != 2 && grp != 4 && grp != 8))
+    return fail(ctx, Q8_ERR_UNSUPPORTED, "q8_decode_attention: head_dim=%d, nheads/nkv=%d "
+                "(supported: head_dim 64 or 128, nheads/nkv 1, 2, 4 or 8)", head_dim, grp);
+  const uint64_t qn = (uint64_t)nheads * head_dim, kn = (uint64_t)nkv * head_dim;
+  // cache rows are read through 32-bit buffer offsets
+  if (maxlen <= 0 || (uint64_t)maxlen * kn * 2 >= ((uint64_t)1 << 31))
+    return fail(ctx, Q8_ERR_SHAPE, "q8_decode_attention: maxlen=%lld (a cache block must stay "
+                "under 2 GiB)", (long long)maxlen);
+  const uint64_t cn = (uint64_t)maxlen * kn;
+  const int nsplit = q8::decode_attn_nsplit(maxlen, head_dim);
+  if ((uint64_t)nheads * nsplit * (head_dim + 2) > (uint64_t)kGemmWsFloats)
+    return fail(ctx, Q8_ERR_UNSUPPORTED, "q8_decode_attention: nheads=%d exceeds the context's "
+                "attention scratch", nheads);
+  if (int rc = check_f32(ctx, a, oq_f32, qn, "q8_decode_attention", "q")) return rc;
+  if (int rc = check_f32(ctx, a, ok_f32, kn, "q8_decode_attention", "k")) return rc;
+  if (int rc = check_f32(ctx, a, ov_f32, kn, "q8_decode_attention", "v")) return rc;
+  if (int rc = check_f32(ctx, a, oinv_f32, (uint64_t)head_dim / 2, "q8_decode_attention",
+                         "inv_freq"))
+    return rc;
+  if (int rc = check_f32(ctx, a, oy_f32, qn, "q8_decode_attention", "out")) return rc;
+  if (overlaps(oy_f32, oy_f32 + qn, oq_f32, oq_f32 + qn) ||
+      overlaps(oy_f32, oy_f32 + qn, ok_f32, ok_f32 + kn) ||
+      overlaps(oy_f32, oy_f32 + qn, ov_f32, ov_f32 + kn))
+    return fail(ctx, Q8_ERR_ARG, "q8_decode_attention: out overlaps q, k or v");
+  if (!fits(okc_f16, cn, 2, kv->size) || !fits(ovc_f16, cn, 2, kv->size))
+    return fail(ctx, Q8_ERR_RANGE, "q8_decode_attention: K or V cache block exceeds the KV buffer");
+  if (overlaps(okc_f16, okc_f16 + cn, ovc_f16, ovc_f16 + cn))
+    return fail(ctx, Q8_ERR_ARG, "q8_decode_attention: K and V cache blocks overlap");
+  if (int rc = check_pos(ctx, posbuf, opos_i32, pos0, 1, maxlen, "q8_decode_attention")) return rc;
+  if (ctx->host_only) return fail(ctx, Q8_ERR_NODEVICE, "q8_decode_attention: host-only context");
+  if (int rc = set_device(ctx)) return rc;
+  __half *kvp = reinterpret_cast<__half *>(kv->ptr);
+  q8::DecodeAttnArgs da;
+  da.q = fptr(a, oq_f32);
+  da.k = fptr(a, ok_f32);
+  da.v = fptr(a, ov_f32);
+  da.inv = fptr(a, oinv_f32);
+  da.kc = kvp + okc_f16;
+  da.vc = kvp + ovc_f16;
+  da.out = fptr(a, oy_f32);
+  da.part = ctx->gemm_ws;
+  da.nheads = nheads;
+  da.nkv = nkv;
+  da.head_dim = head_dim;
+  da.nsplit = nsplit;
+  da.posp = posbuf ? reinterpret_cast<const int *>(bytes(posbuf, opos_i32 * 4)) : nullptr;
+  da.pos0 = (int)pos0;
+  da.maxlen = (int)maxlen;
+  hipError_t e = q8::launch_decode_attention(da, ctx->stream);
+  if (e != hipSuccess) return hip_fail(ctx, e, "q8_decode_attention launch");
   return ok(ctx);
 }
 

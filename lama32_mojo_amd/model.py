@@ -264,16 +264,22 @@ class Q8Llama:
             oq = self.linear(xn, s, H, lo.q, QD)
             okk = self.linear(xn, s, H, lo.k, KVD)
             ov = self.linear(xn, s, H, lo.v, KVD)
-        q8hip.rope_kv(ctx, a.buf, oq, okk, ov, self.oinv, self.kv, self.okc[L], self.ovc[L],
-                      self.maxlen, s, pos0, cfg.n_heads, cfg.n_kv, cfg.head_dim, pb, 0)
         oao = a.alloc(s * QD)
-        rows = min(s, self.ATT_ROWS)
-        osc = a.alloc(q8hip.attention_scratch_floats(rows, cfg.n_heads, cfg.head_dim, self.maxlen))
-        for r0 in range(0, s, rows):
-            r = min(rows, s - r0)
-            q8hip.attention(ctx, a.buf, oq + r0 * QD, self.kv, self.okc[L], self.ovc[L],
-                            self.maxlen, oao + r0 * QD, osc, r, pos0 + r0, cfg.n_heads, cfg.n_kv,
-                            cfg.head_dim, pb, 0)
+        if s == 1:
+            q8hip.decode_attention(ctx, a.buf, oq, okk, ov, self.oinv, self.kv, self.okc[L],
+                                   self.ovc[L], self.maxlen, oao, pos0, cfg.n_heads, cfg.n_kv,
+                                   cfg.head_dim, pb, 0)
+        else:
+            q8hip.rope_kv(ctx, a.buf, oq, okk, ov, self.oinv, self.kv, self.okc[L], self.ovc[L],
+                          self.maxlen, s, pos0, cfg.n_heads, cfg.n_kv, cfg.head_dim, pb, 0)
+            rows = min(s, self.ATT_ROWS)
+            osc = a.alloc(q8hip.attention_scratch_floats(rows, cfg.n_heads, cfg.head_dim,
+                                                         self.maxlen))
+            for r0 in range(0, s, rows):
+                r = min(rows, s - r0)
+                q8hip.attention(ctx, a.buf, oq + r0 * QD, self.kv, self.okc[L], self.ovc[L],
+                                self.maxlen, oao + r0 * QD, osc, r, pos0 + r0, cfg.n_heads,
+                                cfg.n_kv, cfg.head_dim, pb, 0)
         oo = self.linear(oao, s, QD, lo.o, H)
         if oh is None:
             oh = a.alloc(s * H)

@@ -77,6 +77,8 @@ SIGNATURES = {
     "q8_attention_scratch_floats": (_U64, [_I64, _I, _I, _I64]),
     "q8_attention": (_I, [_P, _P, _U64, _P, _U64, _U64, _I64, _U64, _U64, _I64, _I64, _P, _U64,
                          _I, _I, _I]),
+    "q8_decode_attention": (_I, [_P, _P, _U64, _U64, _U64, _U64, _P, _U64, _U64, _I64, _U64,
+                                _I64, _P, _U64, _I, _I, _I]),
     "q8_swiglu": (_I, [_P, _P, _U64, _U64, _I64]),
     "q8_res_add": (_I, [_P, _P, _U64, _U64, _U64, _I64]),
     "q8_add": (_I, [_P, _P, _U64, _U64, _I64]),
@@ -306,6 +308,16 @@ def attention(ctx: Context, a: Buffer, oq: int, kv: Buffer, okc_f16: int, ovc_f1
                                     int(maxlen), int(oy), int(oscratch), int(s), int(pos0),
                                     _h(posbuf), int(opos_i32), int(nheads), int(nkv),
                                     int(head_dim)))
+
+
+def decode_attention(ctx: Context, a: Buffer, oq: int, ok: int, ov: int, oinv: int, kv: Buffer,
+                     okc_f16: int, ovc_f16: int, maxlen: int, oy: int, pos0: int, nheads: int,
+                     nkv: int, head_dim: int, posbuf: Buffer | None = None,
+                     opos_i32: int = 0) -> None:
+    ctx.check(ctx._lib.q8_decode_attention(ctx.h, a.h, int(oq), int(ok), int(ov), int(oinv), kv.h,
+                                           int(okc_f16), int(ovc_f16), int(maxlen), int(oy),
+                                           int(pos0), _h(posbuf), int(opos_i32), int(nheads),
+                                           int(nkv), int(head_dim)))
 
 
 def swiglu(ctx: Context, a: Buffer, og: int, ou: int, n: int) -> None:

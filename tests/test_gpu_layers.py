@@ -146,6 +146,53 @@ def test_attention(ctx, head_dim, nh, nkv, s, pos0):
         b.free()
 
 
+@pytest.mark.parametrize("head_dim,nh,nkv", [(64, 32, 8), (128, 32, 8), (64, 16, 16), (128, 8, 1)])
+@pytest.mark.parametrize("pos0", [0, 1, 63, 64, 500, 1023, 1500])
+def test_decode_attention_equals_rope_then_attention(ctx, head_dim, nh, nkv, pos0):
+    """The one-launch token step writes the same cache bits as q8_rope_kv and
+    matches q8_rope_kv + q8_attention within 2e-6 (it sums the splits in
+    another order).  maxlen 1536 gives 6 context splits: pos0 <= 255 is
+    served by one block, larger pos0 by 2 .. 6 blocks merged by the last to
+    arrive; a second call must reproduce the first (its counters are back at
+    zero)."""
+    say("decode attention", head_dim, nh, nkv, pos0)
+    rng = np.random.default_rng(4)
+    maxlen = 1536
+    qd, kvd = nh * head_dim, nkv * head_dim
+    inv = mo.llama3_inv_freq(head_dim, 500000.0, 32.0, 1.0, 4.0, 8192.0)
+    cache = rng.standard_normal((2, maxlen, kvd)).astype(np.float16)
+    q = rng.standard_normal(qd).astype(np.float32)
+    k = rng.standard_normal(kvd).astype(np.float32)
+    v = rng.standard_normal(kvd).astype(np.float32)
+    oq, ok, ov, oinv, oy = 0, qd, qd + kvd, qd + 2 * kvd, qd + 2 * kvd + head_dim
+    osc = oy + qd
+    a = arena(ctx, osc + q8hip.attention_scratch_floats(1, nh, head_dim, maxlen))
+    kv1, kv2 = ctx.alloc(cache.nbytes), ctx.alloc(cache.nbytes)
+    kv1.upload(cache)
+    kv2.upload(cache)
+    for buf, x in [(oq, q), (ok, k), (ov, v), (oinv, inv)]:
+        put(a, buf, x)
+    q8hip.decode_attention(ctx, a, oq, ok, ov, oinv, kv1, 0, maxlen * kvd, maxlen, oy, pos0, nh,
+                           nkv, head_dim)
+    fused = get(a, oy, (qd,))
+    put(a, oy, np.zeros(qd, np.float32))
+    q8hip.decode_attention(ctx, a, oq, ok, ov, oinv, kv1, 0, maxlen * kvd, maxlen, oy, pos0, nh,
+                           nkv, head_dim)
+    assert np.array_equal(get(a, oy, (qd,)), fused)
+    q8hip.rope_kv(ctx, a, oq, ok, ov, oinv, kv2, 0, maxlen * kvd, maxlen, 1, pos0, nh, nkv,
+                  head_dim)
+    q8hip.attention(ctx, a, oq, kv2, 0, maxlen * kvd, maxlen, oy, osc, 1, pos0, nh, nkv, head_dim)
+    sep = get(a, oy, (qd,))
+    c1 = kv1.download((2, maxlen, kvd), np.float16)
+    assert np.array_equal(c1, kv2.download((2, maxlen, kvd), np.float16))
+    assert np.all(np.isfinite(fused)) and max_rel_err(fused, sep) <= 2e-6
+    ref = mo.attention(get(a, oq, (1, qd)).astype(np.float64), c1[0].astype(np.float64),
+                       c1[1].astype(np.float64), pos0, nh, nkv, head_dim)
+    assert max_rel_err(fused, ref[0]) <= 1e-5
+    for b in (a, kv1, kv2):
+        b.free()
+
+
 def test_elementwise_and_argmax(ctx):
     say("elementwise")
     rng = np.random.default_rng(3)
