@@ -146,6 +146,37 @@ int q8_embed_gather(q8_ctx *ctx, q8_buf *w, uint64_t oemb_u16, q8_buf *ids,
  * Outputs may coincide exactly with an input (in place) but must not
  * otherwise overlap one. */
 
+/* One-row Q8 linear with its neighbours folded into the same launch (the
+ * decode step's s = 1 GEMVs).  How x is read (pre):
+ *   Q8_PRE_NONE:    x (m floats)
+ *   Q8_PRE_RMSNORM: rmsnorm(x) as q8_rmsnorm, with the d = m bf16 weights at
+ *                   onorm of `w` and eps; the norm factor is applied to each
+ *                   output (W (wn x / r) = (W (wn x)) / r), so results match
+ *                   q8_rmsnorm + q8_linear to float rounding, not to the bit
+ *   Q8_PRE_SWIGLU:  x = [g | u] (2m floats), read as silu(g) * u (as q8_swiglu)
+ * What is stored (post):
+ *   Q8_POST_STORE:    y = W x~ (n floats)
+ *   Q8_POST_RESIDUAL: y = res + W x~, res = n floats at ores, may be y itself
+ *   Q8_POST_SWIGLU:   rows [0, n/2) are gate rows and [n/2, n) up rows (the
+ *                     fused gate|up weights); y = silu(W_g x~) * (W_u x~), n/2
+ *                     floats (as q8_linear + q8_swiglu)
+ * x must not overlap y.  Without Q8_PRE_RMSNORM the results equal the
+ * separate calls to the bit.  Needs m <= 16384, m % 32 == 0, 16-byte
+ * aligned rows and x and 8-byte aligned norm weights (Q8_ERR_UNSUPPORTED
+ * otherwise).
+ * Replaces rmsnorm_op + mm_q8_op, mm_q8_op + swiglu_mul_op and mm_q8_op +
+ * res_add_op / add_op of run_layer_q8 (src/llama_q8.mojo:144-230). */
+#define Q8_PRE_NONE 0
+#define Q8_PRE_RMSNORM 1
+#define Q8_PRE_SWIGLU 2
+#define Q8_POST_STORE 0
+#define Q8_POST_RESIDUAL 1
+#define Q8_POST_SWIGLU 2
+int q8_linear_fused(q8_ctx *ctx, q8_buf *w, uint64_t owt_u16, q8_buf *a,
+                    uint64_t ox_f32, uint64_t oy_f32, int64_t m, int64_t n, int G,
+                    int scale_dtype, int pre, uint64_t onorm_u16, float eps,
+                    int post, uint64_t ores_f32);
+
 /* y = bf16(wn) * x / sqrt(mean(x^2) + eps) for `rows` rows of d, wn = d bf16
  * values at owt (k_rmsnorm_w / rmsnorm_op, src/llama_common.mojo:197-225,
  * 690-696). */

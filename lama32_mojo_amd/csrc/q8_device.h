@@ -140,6 +140,18 @@ __device__ __forceinline__ float wave_sum(float v) {
   return (a + b) + (c + d);
 }
 
+// Sum over a 256-thread block (4 waves), the same value in every thread:
+// wave sums, then (w0 + w1) + (w2 + w3).  red: 4 floats of LDS.
+__device__ __forceinline__ float block_sum256(float v, float *red) {
+  v = wave_sum(v);
+  const int wid = threadIdx.x >> 6;
+  if ((threadIdx.x & 63) == 0) red[wid] = v;
+  __syncthreads();
+  const float t = (red[0] + red[1]) + (red[2] + red[3]);
+  __syncthreads();
+  return t;
+}
+
 // Max of |.| with NaN propagation (numpy's max propagates NaN).
 __device__ __forceinline__ float nanmax(float a, float b) {
   if (a != a) return a;

@@ -32,12 +32,18 @@ namespace {
 constexpr int kWaves = 4;               // wavefronts per workgroup
 constexpr int kLdsFloats = 16384;       // x staged in LDS up to 64 KiB
 
-template <int G, int KIND, int S, int R, int SPLITK, bool XLDS>
+template <int G, int KIND, int S, int R, int SPLITK, bool XLDS, int PRE = PRE_NONE,
+          int POST = POST_STORE, int NPF = 1>
 __global__ __launch_bounds__(256) void gemv_kernel(
     const uint8_t *__restrict__ w, int64_t row_bytes, int64_t n,
-    const float *__restrict__ x, int64_t m, float *__restrict__ y) {
+    const float *__restrict__ x, int64_t m, float *y, const uint16_t *__restrict__ wn,
+    float eps, const float *res) {
   extern __shared__ float xs[];
   __shared__ float part[SPLITK > 1 ? SPLITK : 1][R][S];
+  __shared__ float red[4];
+  static_assert(PRE == PRE_NONE || (XLDS && S == 1), "fused prologues stage one x row in LDS");
+  static_assert(POST != POST_SWIGLU || (SPLITK == 1 && R % 2 == 0 && S == 1),
+                "the swiglu epilogue pairs gate and up rows within a wave");
   constexpr int SB = ScaleTraits<KIND>::bytes;
   const int lane = threadIdx.x & 63;
   const int wid = threadIdx.x >> 6;
@@ -45,62 +51,159 @@ __global__ __launch_bounds__(256) void gemv_kernel(
   // SPLITK == 1: each wave owns R rows over the whole K range.
   // SPLITK == 4: the 4 waves of a workgroup share R rows, wave w owning the
   // K range [w m/4, (w+1) m/4); partial sums meet in LDS.
+  // POST_SWIGLU: a wave's R rows are R/2 gate rows j.. and the matching up
+  // rows n/2 + j..; it stores the R/2 outputs silu(gate) * up.
+  constexpr int RO = POST == POST_SWIGLU ? R / 2 : R;   // outputs per wave tile
+  const int64_t nout = POST == POST_SWIGLU ? n / 2 : n;
+  const int64_t rows_per_group = SPLITK > 1 ? RO : (int64_t)kWaves * RO;
+  const int64_t stride_rows = (int64_t)gridDim.x * rows_per_group;
+  int64_t r0 = (int64_t)blockIdx.x * rows_per_group + (SPLITK > 1 ? 0 : wid * RO);
   const int64_t k_lo = SPLITK > 1 ? wid * (m / SPLITK) : 0;
   const int64_t k_hi = SPLITK > 1 ? k_lo + m / SPLITK : m;
+  const int64_t k_first = k_lo + 16 * lane;
+  // weight row of slot r for output tile r0 (clamped: tail slots recompute
+  // the last row)
+  auto row_of = [&](int64_t t0, int r) -> int64_t {
+    if constexpr (POST == POST_SWIGLU) {
+      const int64_t o = t0 + (r % RO) < nout ? t0 + (r % RO) : nout - 1;
+      return r < RO ? o : nout + o;
+    } else {
+      return t0 + r < n ? t0 + r : n - 1;
+    }
+  };
 
+  // A wave loads up to NPF steps (1 KiB per row each) of its R rows at once,
+  // then computes: a tile with m / SPLITK <= 4096 waits on memory once.  The
+  // first tile's first loads do not depend on x and are issued before x is
+  // staged.
+  u32x4 q[NPF][R];
+  float sc[NPF][R];
+  auto load_chunk = [&](const uint8_t *const *rowp, int64_t kc) {
+#pragma unroll
+    for (int p = 0; p < NPF; ++p) {
+      const int64_t k = kc + 1024 * p;
+      if (k < k_hi) {
+#pragma unroll
+        for (int r = 0; r < R; ++r)
+          q[p][r] = __builtin_nontemporal_load(
+              reinterpret_cast<const u32x4 *>(rowp[r] + scale_bytes + k));
+#pragma unroll
+        for (int r = 0; r < R; ++r) sc[p][r] = load_scale<KIND>(rowp[r], k / G);
+      }
+    }
+  };
+  const uint8_t *rowp[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) rowp[r] = w + row_of(r0, r) * row_bytes;
+  if (r0 < nout) load_chunk(rowp, k_first);
+
+  // PRE_RMSNORM: x is staged as bf16(wn) * x and every output is scaled by
+  // 1 / sqrt(mean(x^2) + eps) at the end (W (wn x inv) = inv W (wn x)); the
+  // squares are summed from the loaded values, so the norm adds no pass.
+  float inv = 1.0f;
   const float *xp = x;
   if constexpr (XLDS) {
     const int64_t tot = S * m;   // multiple of 4 (m % 32 == 0)
-    for (int64_t i = 4 * threadIdx.x; i < tot; i += 4 * blockDim.x)
-      *reinterpret_cast<f32x4 *>(xs + i) = *reinterpret_cast<const f32x4 *>(x + i);
+    float ss = 0.0f;
+    for (int64_t i = 4 * threadIdx.x; i < tot; i += 4 * blockDim.x) {
+      if constexpr (PRE == PRE_SWIGLU) {
+        // x holds [gate | up]: 2m floats
+        const f32x4 gv = *reinterpret_cast<const f32x4 *>(x + i);
+        const f32x4 uv = *reinterpret_cast<const f32x4 *>(x + m + i);
+        f32x4 o;
+        o.x = (gv.x / (1.0f + expf(-gv.x))) * uv.x;
+        o.y = (gv.y / (1.0f + expf(-gv.y))) * uv.y;
+        o.z = (gv.z / (1.0f + expf(-gv.z))) * uv.z;
+        o.w = (gv.w / (1.0f + expf(-gv.w))) * uv.w;
+        *reinterpret_cast<f32x4 *>(xs + i) = o;
+      } else if constexpr (PRE == PRE_RMSNORM) {
+        const f32x4 xv = *reinterpret_cast<const f32x4 *>(x + i);
+        const uint2 wb = *reinterpret_cast<const uint2 *>(wn + i);
+        ss = __builtin_fmaf(xv.x, xv.x, ss);
+        ss = __builtin_fmaf(xv.y, xv.y, ss);
+        ss = __builtin_fmaf(xv.z, xv.z, ss);
+        ss = __builtin_fmaf(xv.w, xv.w, ss);
+        f32x4 o;
+        o.x = bf16_bits_to_f32(wb.x & 0xffffu) * xv.x;
+        o.y = bf16_bits_to_f32(wb.x >> 16) * xv.y;
+        o.z = bf16_bits_to_f32(wb.y & 0xffffu) * xv.z;
+        o.w = bf16_bits_to_f32(wb.y >> 16) * xv.w;
+        *reinterpret_cast<f32x4 *>(xs + i) = o;
+      } else {
+        *reinterpret_cast<f32x4 *>(xs + i) = *reinterpret_cast<const f32x4 *>(x + i);
+      }
+    }
+    if constexpr (PRE == PRE_RMSNORM) {
+      ss = wave_sum(ss);
+      if (lane == 0) red[wid] = ss;
+    }
     __syncthreads();
+    if constexpr (PRE == PRE_RMSNORM)
+      inv = 1.0f / sqrtf(((red[0] + red[1]) + (red[2] + red[3])) / (float)m + eps);
     xp = xs;
   }
 
-  const int64_t rows_per_group = SPLITK > 1 ? R : (int64_t)kWaves * R;
-  const int64_t stride_rows = (int64_t)gridDim.x * rows_per_group;
-  int64_t r0 = (int64_t)blockIdx.x * rows_per_group + (SPLITK > 1 ? 0 : wid * R);
-  for (; r0 < n; r0 += stride_rows) {
+  // one finished output (value v of tile slot r) -> memory
+  auto store = [&](int64_t t0, int r, int b, float v, float v_up) {
+    const int64_t o = t0 + r;
+    if (o >= nout) return;
+    if constexpr (POST == POST_SWIGLU) {
+      const float g = inv * v, u = inv * v_up;
+      y[o] = (g / (1.0f + expf(-g))) * u;
+    } else {
+      v = inv * v;
+      if constexpr (POST == POST_RESIDUAL) v = res[b * n + o] + v;
+      y[b * n + o] = v;
+    }
+  };
+
+  bool first = true;
+  for (; r0 < nout; r0 += stride_rows) {
     float acc[R][S];
 #pragma unroll
     for (int r = 0; r < R; ++r)
 #pragma unroll
       for (int b = 0; b < S; ++b) acc[r][b] = 0.0f;
-
-    const uint8_t *rowp[R];
+    if (!first) {
 #pragma unroll
-    for (int r = 0; r < R; ++r) {
-      int64_t j = r0 + r < n ? r0 + r : n - 1;   // clamp: tail rows recompute row n-1
-      rowp[r] = w + j * row_bytes;
+      for (int r = 0; r < R; ++r) rowp[r] = w + row_of(r0, r) * row_bytes;
     }
 
-    for (int64_t k = k_lo + 16 * lane; k < k_hi; k += 1024) {
-      u32x4 q[R];
-      float sc[R];
+    for (int64_t kc = k_first; kc < k_hi; kc += 1024 * NPF) {
+      if (first)
+        first = false;                   // loaded before x was staged
+      else
+        load_chunk(rowp, kc);
 #pragma unroll
-      for (int r = 0; r < R; ++r)
-        q[r] = __builtin_nontemporal_load(
-            reinterpret_cast<const u32x4 *>(rowp[r] + scale_bytes + k));
+      for (int p = 0; p < NPF; ++p) {
+        const int64_t k = kc + 1024 * p;
+        if (k < k_hi) {
 #pragma unroll
-      for (int r = 0; r < R; ++r) sc[r] = load_scale<KIND>(rowp[r], k / G);
+          for (int b = 0; b < S; ++b) {
+            const f32x4 *xv4 = reinterpret_cast<const f32x4 *>(xp + b * m + k);
+            f32x4 xa = xv4[0], xb = xv4[1], xc = xv4[2], xd = xv4[3];
 #pragma unroll
-      for (int b = 0; b < S; ++b) {
-        const f32x4 *xv4 = reinterpret_cast<const f32x4 *>(xp + b * m + k);
-        f32x4 xa = xv4[0], xb = xv4[1], xc = xv4[2], xd = xv4[3];
-#pragma unroll
-        for (int r = 0; r < R; ++r)
-          acc[r][b] = __builtin_fmaf(sc[r], dot16(q[r], xa, xb, xc, xd), acc[r][b]);
+            for (int r = 0; r < R; ++r)
+              acc[r][b] =
+                  __builtin_fmaf(sc[p][r], dot16(q[p][r], xa, xb, xc, xd), acc[r][b]);
+          }
+        }
       }
     }
 
     if constexpr (SPLITK == 1) {
+      float v[R][S];
 #pragma unroll
       for (int r = 0; r < R; ++r)
 #pragma unroll
-        for (int b = 0; b < S; ++b) {
-          float v = wave_sum(acc[r][b]);
-          if (lane == 0 && r0 + r < n) y[b * n + r0 + r] = v;
-        }
+        for (int b = 0; b < S; ++b) v[r][b] = wave_sum(acc[r][b]);
+      if (lane == 0) {
+#pragma unroll
+        for (int r = 0; r < RO; ++r)
+#pragma unroll
+          for (int b = 0; b < S; ++b)
+            store(r0, r, b, v[r][b], POST == POST_SWIGLU ? v[(r + RO) % R][b] : 0.0f);
+      }
     } else {
 #pragma unroll
       for (int r = 0; r < R; ++r)
@@ -115,7 +218,7 @@ __global__ __launch_bounds__(256) void gemv_kernel(
         float v = part[0][r][b];
 #pragma unroll
         for (int u = 1; u < SPLITK; ++u) v += part[u][r][b];
-        if (r0 + r < n) y[b * n + r0 + r] = v;
+        store(r0, r, b, v, 0.0f);
       }
       __syncthreads();
     }
@@ -160,7 +263,11 @@ int grid_for(int64_t tiles, int64_t cap) {
   return (int)(tiles < cap ? (tiles > 0 ? tiles : 1) : cap);
 }
 
-template <int G, int KIND, int S, int R, int SPLITK>
+// NPF: K steps in flight per wave (registers against occupancy: one step for
+// the many-round vocabulary heads, two for 4-row waves, four for 1-row waves)
+template <int R, int S> constexpr int npf_for() { return R * S >= 8 ? 1 : R * S >= 4 ? 2 : 4; }
+
+template <int G, int KIND, int S, int R, int SPLITK, int NPF = npf_for<R, S>()>
 hipError_t launch_fast(const LinearArgs &a, const float *x, float *y, int64_t cap,
                        hipStream_t st) {
   const int64_t rows_per_group = SPLITK > 1 ? R : kWaves * R;
@@ -168,11 +275,12 @@ hipError_t launch_fast(const LinearArgs &a, const float *x, float *y, int64_t ca
   dim3 grid(grid_for(tiles, cap)), block(256);
   if (S * a.m <= kLdsFloats) {
     size_t lds = (size_t)S * a.m * sizeof(float);
-    hipLaunchKernelGGL((gemv_kernel<G, KIND, S, R, SPLITK, true>), grid, block, lds, st,
-                       a.w, a.row_bytes, a.n, x, a.m, y);
+    hipLaunchKernelGGL((gemv_kernel<G, KIND, S, R, SPLITK, true, PRE_NONE, POST_STORE, NPF>), grid,
+                       block, lds, st, a.w, a.row_bytes, a.n, x, a.m, y, nullptr, 0.0f, nullptr);
   } else {
-    hipLaunchKernelGGL((gemv_kernel<G, KIND, S, R, SPLITK, false>), grid, block, 0, st,
-                       a.w, a.row_bytes, a.n, x, a.m, y);
+    hipLaunchKernelGGL((gemv_kernel<G, KIND, S, R, SPLITK, false, PRE_NONE, POST_STORE, NPF>),
+                       grid, block, 0, st, a.w, a.row_bytes, a.n, x, a.m, y, nullptr, 0.0f,
+                       nullptr);
   }
   return hipGetLastError();
 }
@@ -185,7 +293,7 @@ hipError_t launch_fast(const LinearArgs &a, const float *x, float *y, int64_t ca
 template <int G, int KIND, int S>
 hipError_t launch_rows(const LinearArgs &a, const float *x, float *y, hipStream_t st) {
   if (a.m > 4096 && a.m % 64 == 0) return launch_fast<G, KIND, S, 4, 4>(a, x, y, 1024, st);
-  if (a.n >= 65536) return launch_fast<G, KIND, S, 2, 1>(a, x, y, 8192, st);
+  if (a.n >= 65536) return launch_fast<G, KIND, S, 2, 1, 1>(a, x, y, 8192, st);
   if (a.n >= 8192) return launch_fast<G, KIND, S, 4, 1>(a, x, y, 1024, st);
   return launch_fast<G, KIND, S, 1, 1>(a, x, y, 4096, st);
 }
@@ -225,7 +333,76 @@ hipError_t launch_g(const LinearArgs &a, hipStream_t st) {
   return hipSuccess;
 }
 
+template <int G, int KIND, int R, int SPLITK, int PRE, int POST, int NPF = npf_for<R, 1>()>
+hipError_t launch_fused_t(const FusedLinearArgs &f, int64_t cap, hipStream_t st) {
+  const LinearArgs &a = f.lin;
+  constexpr int RO = POST == POST_SWIGLU ? R / 2 : R;
+  const int64_t nout = POST == POST_SWIGLU ? a.n / 2 : a.n;
+  const int64_t rows_per_group = SPLITK > 1 ? RO : kWaves * RO;
+  const int64_t tiles = (nout + rows_per_group - 1) / rows_per_group;
+  dim3 grid(grid_for(tiles, cap)), block(256);
+  hipLaunchKernelGGL((gemv_kernel<G, KIND, 1, R, SPLITK, true, PRE, POST, NPF>), grid, block,
+                     (size_t)a.m * sizeof(float), st, a.w, a.row_bytes, a.n,
+                     reinterpret_cast<const float *>(a.x), a.m, a.y, f.wn, f.eps, f.res);
+  return hipGetLastError();
+}
+
+// Shape classes as launch_rows; the swiglu epilogue keeps whole rows per
+// wave (gate and up rows of one output in the same wave).
+template <int G, int KIND, int PRE, int POST>
+hipError_t launch_fused_rows(const FusedLinearArgs &f, hipStream_t st) {
+  const LinearArgs &a = f.lin;
+  if constexpr (POST == POST_SWIGLU) {
+    if (a.n >= 8192) return launch_fused_t<G, KIND, 4, 1, PRE, POST>(f, 1024, st);
+    return launch_fused_t<G, KIND, 2, 1, PRE, POST>(f, 4096, st);
+  } else {
+    if (a.m > 4096 && a.m % 64 == 0) return launch_fused_t<G, KIND, 4, 4, PRE, POST>(f, 1024, st);
+    if (a.n >= 65536) return launch_fused_t<G, KIND, 2, 1, PRE, POST, 1>(f, 8192, st);
+    if (a.n >= 8192) return launch_fused_t<G, KIND, 4, 1, PRE, POST>(f, 1024, st);
+    return launch_fused_t<G, KIND, 1, 1, PRE, POST>(f, 4096, st);
+  }
+}
+
+template <int G, int KIND, int PRE>
+hipError_t launch_fused_pre(const FusedLinearArgs &f, hipStream_t st) {
+  if (f.post == POST_STORE) return launch_fused_rows<G, KIND, PRE, POST_STORE>(f, st);
+  if (f.post == POST_RESIDUAL) return launch_fused_rows<G, KIND, PRE, POST_RESIDUAL>(f, st);
+  if (f.post == POST_SWIGLU) return launch_fused_rows<G, KIND, PRE, POST_SWIGLU>(f, st);
+  return hipErrorInvalidValue;
+}
+
+template <int G, int KIND>
+hipError_t launch_fused_g(const FusedLinearArgs &f, hipStream_t st) {
+  if (f.pre == PRE_NONE) return launch_fused_pre<G, KIND, PRE_NONE>(f, st);
+  if (f.pre == PRE_RMSNORM) return launch_fused_pre<G, KIND, PRE_RMSNORM>(f, st);
+  if (f.pre == PRE_SWIGLU) return launch_fused_pre<G, KIND, PRE_SWIGLU>(f, st);
+  return hipErrorInvalidValue;
+}
+
 }  // namespace
+
+bool gemv_fused_supported(const FusedLinearArgs &f) {
+  const LinearArgs &a = f.lin;
+  const int pre = f.pre, post = f.post;
+  const int sb = a.kind == SCALE_F16 ? 2 : 4;
+  if (pre == PRE_RMSNORM && reinterpret_cast<uintptr_t>(f.wn) % 8 != 0) return false;
+  return a.s == 1 && !a.x_is_bf16 && a.m <= kLdsFloats && a.m % 32 == 0 &&
+         (a.G == 32 || a.G == 64) && reinterpret_cast<uintptr_t>(a.w) % 16 == 0 &&
+         a.row_bytes % 16 == 0 && ((a.m / a.G) * sb) % 16 == 0 &&
+         reinterpret_cast<uintptr_t>(a.x) % 16 == 0 && pre >= PRE_NONE && pre <= PRE_SWIGLU &&
+         post >= POST_STORE && post <= POST_SWIGLU && (post != POST_SWIGLU || a.n % 2 == 0);
+}
+
+hipError_t launch_gemv_fused(const FusedLinearArgs &f, hipStream_t st) {
+  const LinearArgs &a = f.lin;
+  if (!gemv_fused_supported(f)) return hipErrorInvalidValue;
+  if (a.n == 0) return hipSuccess;
+  if (a.G == 64 && a.kind == SCALE_F16) return launch_fused_g<64, SCALE_F16>(f, st);
+  if (a.G == 64 && a.kind == SCALE_F32) return launch_fused_g<64, SCALE_F32>(f, st);
+  if (a.G == 32 && a.kind == SCALE_F16) return launch_fused_g<32, SCALE_F16>(f, st);
+  if (a.G == 32 && a.kind == SCALE_F32) return launch_fused_g<32, SCALE_F32>(f, st);
+  return hipErrorInvalidValue;
+}
 
 hipError_t launch_gemv(const LinearArgs &a, hipStream_t st) {
   if (a.s == 0 || a.n == 0) return hipSuccess;

@@ -36,6 +36,27 @@ struct LinearArgs {
 };
 // Decode path (s small, f32 x): VALU GEMV.
 hipError_t launch_gemv(const LinearArgs &a, hipStream_t st);
+// One-row GEMV with its neighbours folded in (decode step, s = 1).
+// Prologue (how x is read):
+//   PRE_RMSNORM: rmsnorm(x) with bf16 weights wn; staged as wn * x, the
+//                factor 1 / sqrt(mean(x^2) + eps) applied to each output;
+//   PRE_SWIGLU:  x holds [gate | up] (2m floats), read as silu(gate) * up.
+// Epilogue (what is stored):
+//   POST_RESIDUAL: y = res + W x (res may be y itself);
+//   POST_SWIGLU:   rows [0, n/2) are gate rows and [n/2, n) up rows; stores
+//                  y[j] = silu(g_j) * u_j for j < n/2.
+enum { PRE_NONE = 0, PRE_RMSNORM = 1, PRE_SWIGLU = 2 };
+enum { POST_STORE = 0, POST_RESIDUAL = 1, POST_SWIGLU = 2 };
+struct FusedLinearArgs {
+  LinearArgs lin;        // s = 1, f32 x, aligned rows
+  int pre, post;
+  const uint16_t *wn;    // PRE_RMSNORM: m bf16 norm weights
+  float eps;
+  const float *res;      // POST_RESIDUAL: residual [n]
+};
+// False when the shape cannot take the fused path (x staged in LDS).
+bool gemv_fused_supported(const FusedLinearArgs &f);
+hipError_t launch_gemv_fused(const FusedLinearArgs &a, hipStream_t st);
 // Prefill path: MFMA GEMM (bf16 x, or f32 x split into two bf16 terms).
 hipError_t launch_gemm(const LinearArgs &a, hipStream_t st);
 // Small batches (2 <= s <= 32, f32 x): MFMA over zero-padded 16-row tiles.

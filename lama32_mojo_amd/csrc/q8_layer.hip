@@ -59,16 +59,6 @@ __device__ __forceinline__ void rotate(float x0, float x1, float c, float sn, fl
 }
 
 // Sum over a 256-thread block (4 waves); every thread gets the total.
-__device__ __forceinline__ float block_sum256(float v, float *red) {
-  v = wave_sum(v);
-  const int wid = threadIdx.x >> 6;
-  if ((threadIdx.x & 63) == 0) red[wid] = v;
-  __syncthreads();
-  const float t = (red[0] + red[1]) + (red[2] + red[3]);
-  __syncthreads();
-  return t;
-}
-
 // ---- RMSNorm (k_rmsnorm_w): y = bf16(w) * x * 1/sqrt(mean(x^2) + eps) -------
 // One 256-thread block per row.  With res != null the row is h = x + res,
 // stored to h_out, and normalised (k_res_add followed by k_rmsnorm_w).

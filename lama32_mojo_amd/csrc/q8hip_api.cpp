@@ -522,6 +522,62 @@ int64_t attn_nsplit(int64_t maxlen) { return (maxlen + 63) / 64; }
 
 }  // namespace
 
+int q8_linear_fused(q8_ctx *ctx, q8_buf *w, uint64_t owt_u16, q8_buf *a, uint64_t ox_f32,
+                    uint64_t oy_f32, int64_t m, int64_t n, int G, int scale_dtype, int pre,
+                    uint64_t onorm_u16, float eps, int post, uint64_t ores_f32) {
+  if (int rc = check_ctx(ctx)) return rc;
+  if (int rc = check_linear(ctx, "q8_linear_fused", w, owt_u16, 1, m, n, G, scale_dtype))
+    return rc;
+  if (!a) return fail(ctx, Q8_ERR_ARG, "q8_linear_fused: null activation buffer");
+  if (pre != Q8_PRE_NONE && pre != Q8_PRE_RMSNORM && pre != Q8_PRE_SWIGLU)
+    return fail(ctx, Q8_ERR_ARG, "q8_linear_fused: pre=%d", pre);
+  if (post != Q8_POST_STORE && post != Q8_POST_RESIDUAL && post != Q8_POST_SWIGLU)
+    return fail(ctx, Q8_ERR_ARG, "q8_linear_fused: post=%d", post);
+  if (post == Q8_POST_SWIGLU && n % 2 != 0)
+    return fail(ctx, Q8_ERR_SHAPE, "q8_linear_fused: n=%lld must be even (gate and up rows)",
+                (long long)n);
+  const uint64_t nx = (uint64_t)(pre == Q8_PRE_SWIGLU ? 2 : 1) * (uint64_t)m;
+  const uint64_t ny = post == Q8_POST_SWIGLU ? (uint64_t)n / 2 : (uint64_t)n;
+  if (int rc = check_f32(ctx, a, ox_f32, nx, "q8_linear_fused", "x")) return rc;
+  if (int rc = check_f32(ctx, a, oy_f32, ny, "q8_linear_fused", "y")) return rc;
+  if (nx && ny && overlaps(ox_f32, ox_f32 + nx, oy_f32, oy_f32 + ny))
+    return fail(ctx, Q8_ERR_ARG, "q8_linear_fused: x and y overlap");
+  if (post == Q8_POST_RESIDUAL) {
+    if (int rc = check_f32(ctx, a, ores_f32, ny, "q8_linear_fused", "residual")) return rc;
+    if (bad_alias(oy_f32, ny, ores_f32, ny))
+      return fail(ctx, Q8_ERR_ARG, "q8_linear_fused: y partially overlaps the residual");
+  }
+  if (pre == Q8_PRE_RMSNORM && !fits(onorm_u16, (uint64_t)m, 2, w->size))
+    return fail(ctx, Q8_ERR_RANGE, "q8_linear_fused: norm weights exceed the weight buffer");
+  q8::FusedLinearArgs f;
+  q8::LinearArgs &la = f.lin;
+  la.w = bytes(w, owt_u16 * 2);
+  la.row_bytes = rowstride_u16(m, G, scale_dtype) * 2;
+  la.x = bytes(a, ox_f32 * 4);
+  la.x_is_bf16 = 0;
+  la.y = fptr(a, oy_f32);
+  la.s = 1;
+  la.m = m;
+  la.n = n;
+  la.G = G;
+  la.kind = scale_dtype;
+  f.pre = pre;
+  f.post = post;
+  f.wn = pre == Q8_PRE_RMSNORM ? reinterpret_cast<const uint16_t *>(bytes(w, onorm_u16 * 2))
+                               : nullptr;
+  f.eps = eps;
+  f.res = post == Q8_POST_RESIDUAL ? fptr(a, ores_f32) : nullptr;
+  if (!q8::gemv_fused_supported(f))
+    return fail(ctx, Q8_ERR_UNSUPPORTED, "q8_linear_fused: m=%lld (needs m <= 16384, m %% 32 == 0, "
+                "16-byte aligned rows and x, 8-byte aligned norm weights)", (long long)m);
+  if (ctx->host_only) return fail(ctx, Q8_ERR_NODEVICE, "q8_linear_fused: host-only context");
+  if (n == 0) return ok(ctx);
+  if (int rc = set_device(ctx)) return rc;
+  hipError_t e = q8::launch_gemv_fused(f, ctx->stream);
+  if (e != hipSuccess) return hip_fail(ctx, e, "q8_linear_fused launch");
+  return ok(ctx);
+}
+
 int q8_rmsnorm(q8_ctx *ctx, q8_buf *w, uint64_t owt_u16, q8_buf *a, uint64_t ox_f32,
                uint64_t oy_f32, int64_t rows, int64_t d, float eps) {
   if (int rc = check_ctx(ctx)) return rc;

@@ -155,8 +155,12 @@ class Q8Llama:
 
     def __init__(self, ctx: Context, cfg: Config, maxlen: int, G: int = 64, scale: str = "f16",
                  weights: Mapping[str, np.ndarray] | None = None, seed: int = 0,
-                 std: float = 0.02, act_floats: int | None = None, max_prefill: int = 1):
+                 std: float = 0.02, act_floats: int | None = None, max_prefill: int = 1,
+                 fuse: bool = True):
         self.ctx, self.cfg, self.maxlen = ctx, cfg, int(maxlen)
+        # one-row steps fold rmsnorm, swiglu and the residual adds into the
+        # GEMV launches
+        self.fuse = bool(fuse)
         self.G, self.scale = G, scale
         self.qk = Q8Kernels(ctx, G, scale)
         names = weight_names(cfg)
@@ -255,6 +259,9 @@ class Q8Llama:
         H, QD, KVD, I = cfg.hidden, cfg.q_dim(), cfg.kv_dim(), cfg.inter
         rsH = q8_rowstride(H, self.G, self.scale)
         pb = self.posbuf if device_pos else None
+        if (s == 1 and self.fuse and lo.k == lo.q + QD * rsH and lo.v == lo.k + KVD * rsH
+                and lo.up == lo.gate + I * rsH):
+            return self._layer_fused(L, ox, pos0, pb, oh)
         xn = a.alloc(s * H)
         q8hip.rmsnorm(ctx, w.buf, lo.in_norm, a.buf, ox, xn, s, H, cfg.eps)
         if s == 1 and lo.k == lo.q + QD * rsH and lo.v == lo.k + KVD * rsH:
@@ -296,6 +303,33 @@ class Q8Llama:
         q8hip.add(ctx, a.buf, om, oh, s * H)
         return oh
 
+    def _layer_fused(self, L: int, ox: int, pos0: int, pb, oh: int | None) -> int:
+        """One-row block in five launches: norm + q|k|v, attention (split +
+        merge), o + residual, norm + gate|up + swiglu, down + residual (in
+        place)."""
+        cfg, ctx, a, w = self.cfg, self.ctx, self.a, self.w
+        lo = self.lo[L]
+        H, QD, KVD, I = cfg.hidden, cfg.q_dim(), cfg.kv_dim(), cfg.inter
+        G, sc = self.G, self.scale
+        oq = a.alloc(QD + 2 * KVD)
+        q8hip.linear_fused(ctx, w.buf, lo.q, a.buf, ox, oq, H, QD + 2 * KVD, G, sc,
+                           pre=q8hip.PRE_RMSNORM, onorm_u16=lo.in_norm, eps=cfg.eps)
+        oao = a.alloc(QD)
+        q8hip.decode_attention(ctx, a.buf, oq, oq + QD, oq + QD + KVD, self.oinv, self.kv,
+                               self.okc[L], self.ovc[L], self.maxlen, oao, pos0, cfg.n_heads,
+                               cfg.n_kv, cfg.head_dim, pb, 0)
+        if oh is None:
+            oh = a.alloc(H)
+        q8hip.linear_fused(ctx, w.buf, lo.o, a.buf, oao, oh, QD, H, G, sc,
+                           post=q8hip.POST_RESIDUAL, ores_f32=ox)
+        og = a.alloc(I)
+        q8hip.linear_fused(ctx, w.buf, lo.gate, a.buf, oh, og, H, 2 * I, G, sc,
+                           pre=q8hip.PRE_RMSNORM, onorm_u16=lo.post_norm, eps=cfg.eps,
+                           post=q8hip.POST_SWIGLU)
+        q8hip.linear_fused(ctx, w.buf, lo.down, a.buf, og, oh, I, H, G, sc,
+                           post=q8hip.POST_RESIDUAL, ores_f32=oh)
+        return oh
+
     # ---- token loop ----------------------------------------------------------
     def embed(self, s: int) -> int:
         """Gather s embedding rows for the ids already in self.ids."""
@@ -307,10 +341,17 @@ class Q8Llama:
 
     def _head(self, oh: int, s: int) -> int:
         cfg = self.cfg
+        head = "model.embed_tokens.weight" if cfg.tied else "lm_head.weight"
+        if self.fuse:
+            olg = self.a.alloc(cfg.vocab)
+            q8hip.linear_fused(self.ctx, self.w.buf, self.w.o(head), self.a.buf,
+                               oh + (s - 1) * cfg.hidden, olg, cfg.hidden, cfg.vocab, self.G,
+                               self.scale, pre=q8hip.PRE_RMSNORM,
+                               onorm_u16=self.w.o("model.norm.weight"), eps=cfg.eps)
+            return olg
         onrm = self.a.alloc(cfg.hidden)
         q8hip.rmsnorm(self.ctx, self.w.buf, self.w.o("model.norm.weight"), self.a.buf,
                       oh + (s - 1) * cfg.hidden, onrm, 1, cfg.hidden, cfg.eps)
-        head = "model.embed_tokens.weight" if cfg.tied else "lm_head.weight"
         return self.linear(onrm, 1, cfg.hidden, self.w.o(head), cfg.vocab)
 
     def _run(self, s: int, pos0: int, device_pos: bool) -> int:

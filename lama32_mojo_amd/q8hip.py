@@ -69,6 +69,8 @@ SIGNATURES = {
     "q8_linear": (_I, [_P, _P, _U64, _P, _U64, _U64, _I64, _I64, _I64, _I, _I]),
     "q8_linear_bf16act": (_I, [_P, _P, _U64, _P, _U64, _P, _U64, _I64, _I64, _I64, _I, _I]),
     "q8_embed_gather": (_I, [_P, _P, _U64, _P, _U64, _P, _U64, _I64, _I64, _I64, _I, _I]),
+    "q8_linear_fused": (_I, [_P, _P, _U64, _P, _U64, _U64, _I64, _I64, _I, _I, _I, _U64,
+                            ctypes.c_float, _I, _U64]),
     "q8_rmsnorm": (_I, [_P, _P, _U64, _P, _U64, _U64, _I64, _I64, ctypes.c_float]),
     "q8_add_rmsnorm": (_I, [_P, _P, _U64, _P, _U64, _U64, _U64, _U64, _I64, _I64,
                            ctypes.c_float]),
@@ -253,6 +255,22 @@ def linear(ctx: Context, w: Buffer, owt_u16: int, a: Buffer, ox_f32: int, oy_f32
            s: int, m: int, n: int, G: int = 64, scale="f16") -> None:
     ctx.check(ctx._lib.q8_linear(ctx.h, w.h, int(owt_u16), a.h, int(ox_f32), int(oy_f32),
                                  int(s), int(m), int(n), int(G), scale_code(scale)))
+
+
+PRE_NONE, PRE_RMSNORM, PRE_SWIGLU = 0, 1, 2
+POST_STORE, POST_RESIDUAL, POST_SWIGLU = 0, 1, 2
+
+
+def linear_fused(ctx: Context, w: Buffer, owt_u16: int, a: Buffer, ox_f32: int, oy_f32: int,
+                 m: int, n: int, G: int = 64, scale="f16", pre: int = PRE_NONE,
+                 onorm_u16: int = 0, eps: float = 0.0, post: int = POST_STORE,
+                 ores_f32: int = 0) -> None:
+    """One-row linear with rmsnorm or swiglu folded into the x load and a
+    residual add or the swiglu of gate|up rows folded into the store:
+    q8_linear_fused."""
+    ctx.check(ctx._lib.q8_linear_fused(ctx.h, w.h, int(owt_u16), a.h, int(ox_f32), int(oy_f32),
+                                       int(m), int(n), int(G), scale_code(scale), int(pre),
+                                       int(onorm_u16), float(eps), int(post), int(ores_f32)))
 
 
 def linear_bf16act(ctx: Context, w: Buffer, owt_u16: int, x: Buffer, ox_bf16: int, y: Buffer,

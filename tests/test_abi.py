@@ -86,6 +86,51 @@ def test_linear_validation(hctx):
     assert code_of(L, hctx, w, 8, a, 0, 4096, 0, 2048, 16)[0] == Q8_ERR_NODEVICE
 
 
+def test_linear_fused_validation(hctx):
+    m, n = 2048, 64
+    rs = q8hip.rowstride_u16(m)
+    w = hctx.alloc(2 * (n * rs + m + 4))          # rows, then m bf16 norm weights
+    a = hctx.alloc(4 * 16384)
+    F = q8hip.linear_fused
+    P, Q = q8hip, q8hip
+    norm = n * rs
+    # valid calls reach the device step
+    assert code_of(F, hctx, w, 0, a, 0, 4096, m, n, pre=P.PRE_RMSNORM, onorm_u16=norm,
+                   eps=1e-5)[0] == Q8_ERR_NODEVICE
+    assert code_of(F, hctx, w, 0, a, 0, 4096, m, n, post=Q.POST_RESIDUAL,
+                   ores_f32=4096)[0] == Q8_ERR_NODEVICE
+    assert code_of(F, hctx, w, 0, a, 0, 4096, m // 2, n, pre=P.PRE_SWIGLU, post=Q.POST_RESIDUAL,
+                   ores_f32=8192)[0] == Q8_ERR_NODEVICE
+    assert code_of(F, hctx, w, 0, a, 0, 4096, m, n, post=Q.POST_SWIGLU)[0] == Q8_ERR_NODEVICE
+    # unknown prologue / epilogue; odd row count for the swiglu epilogue
+    assert code_of(F, hctx, w, 0, a, 0, 4096, m, n, pre=3)[0] == Q8_ERR_ARG
+    assert code_of(F, hctx, w, 0, a, 0, 4096, m, n, post=3)[0] == Q8_ERR_ARG
+    assert code_of(F, hctx, w, 0, a, 0, 4096, m, n - 1, post=Q.POST_SWIGLU)[0] == Q8_ERR_SHAPE
+    # x overlaps y (swiglu reads 2m floats; the swiglu epilogue stores n/2)
+    assert code_of(F, hctx, w, 0, a, 0, 2000, m, n)[0] == Q8_ERR_ARG
+    assert code_of(F, hctx, w, 0, a, 0, 2000, m // 2, n, pre=P.PRE_SWIGLU)[0] == Q8_ERR_ARG
+    assert code_of(F, hctx, w, 0, a, 0, 16384 - n // 2, m, n,
+                   post=Q.POST_SWIGLU)[0] == Q8_ERR_NODEVICE
+    assert code_of(F, hctx, w, 0, a, 0, 16384 - n // 2, m, n)[0] == Q8_ERR_RANGE
+    # residual partly overlapping y; past the arena
+    assert code_of(F, hctx, w, 0, a, 0, 4096, m, n, post=Q.POST_RESIDUAL,
+                   ores_f32=4100)[0] == Q8_ERR_ARG
+    assert code_of(F, hctx, w, 0, a, 0, 4096, m, n, post=Q.POST_RESIDUAL,
+                   ores_f32=16380)[0] == Q8_ERR_RANGE
+    # norm weights past the weight buffer, or not 8-byte aligned
+    assert code_of(F, hctx, w, 0, a, 0, 4096, m, n, pre=P.PRE_RMSNORM,
+                   onorm_u16=norm + 5)[0] == Q8_ERR_RANGE
+    assert code_of(F, hctx, w, 0, a, 0, 4096, m, n, pre=P.PRE_RMSNORM,
+                   onorm_u16=norm + 2)[0] == q8hip.Q8_ERR_UNSUPPORTED
+    # x past the arena (swiglu: 2m floats)
+    assert code_of(F, hctx, w, 0, a, 14000, 0, m, n, pre=P.PRE_SWIGLU)[0] == Q8_ERR_RANGE
+    # rows too long to stage x on chip
+    big = 32768
+    wb = hctx.alloc(2 * q8hip.rowstride_u16(big))
+    ab = hctx.alloc(4 * (big + 16))
+    assert code_of(F, hctx, wb, 0, ab, 0, big, big, 1)[0] == q8hip.Q8_ERR_UNSUPPORTED
+
+
 def test_linear_bf16act_validation(hctx):
     rs = q8hip.rowstride_u16(1024, 32, "f32")
     w = hctx.alloc(2 * 64 * rs)

@@ -242,11 +242,106 @@ def test_elementwise_and_argmax(ctx):
         b.free()
 
 
-def gpu_model(ctx, spec, tensors, maxlen, max_prefill=8):
+def gpu_model(ctx, spec, tensors, maxlen, max_prefill=8, fuse=True):
     cfg = gm.Config(spec.hidden, spec.layers, spec.n_heads, spec.n_kv, spec.head_dim, spec.inter,
                     spec.vocab, spec.eps, 500000.0, 32.0, 1.0, 4.0, 8192.0, tied=True, name="tiny")
     return gm.Q8Llama(ctx, cfg, maxlen, spec.G, spec.scale, weights=tensors,
-                      max_prefill=max_prefill)
+                      max_prefill=max_prefill, fuse=fuse)
+
+
+# (m, n) of each GEMV shape class: 1 row per wave, 4 rows per wave, K split
+# over the waves (m > 4096), vocabulary heads (n >= 65536, 2 rows per wave)
+FUSED_SHAPES = [(2048, 3072), (2048, 16384), (8192, 2048), (512, 65600)]
+
+
+FUSED_CASES = [(q8hip.PRE_RMSNORM, q8hip.POST_STORE), (q8hip.PRE_NONE, q8hip.POST_RESIDUAL),
+               (q8hip.PRE_SWIGLU, q8hip.POST_RESIDUAL), (q8hip.PRE_SWIGLU, q8hip.POST_STORE),
+               (q8hip.PRE_RMSNORM, q8hip.POST_RESIDUAL), (q8hip.PRE_NONE, q8hip.POST_SWIGLU),
+               (q8hip.PRE_RMSNORM, q8hip.POST_SWIGLU)]
+
+
+@pytest.mark.parametrize("G,scale", [(64, "f16"), (32, "f32")])
+@pytest.mark.parametrize("m,n", FUSED_SHAPES)
+def test_linear_fused_equals_separate_calls(ctx, G, scale, m, n):
+    """q8_linear_fused against q8_rmsnorm or q8_swiglu, then q8_linear, then
+    q8_add or q8_swiglu.  Bit-exact without the norm, while both sum each row
+    in the same order; max-rel-err <= 1e-5 with the norm (its factor
+    multiplies the output instead of each x) and for the swiglu epilogue at
+    m > 4096 (whole rows per wave there, K split over the waves in
+    q8_linear)."""
+    say("linear_fused", G, scale, m, n)
+    rng = np.random.default_rng(m + n)
+    rs = q8hip.rowstride_u16(m, G, scale)
+    wsrc = ctx.alloc(2 * n * m)
+    wsrc.upload(f32_to_bf16_bits((0.02 * rng.standard_normal((n, m))).astype(np.float32)))
+    w = ctx.alloc(2 * (n * rs + m))
+    q8hip.quantize_pack(ctx, wsrc, 0, q8hip.Q8_SRC_BF16, n, m, w, 0, G, scale)
+    wsrc.free()
+    onorm = n * rs
+    w.upload(f32_to_bf16_bits((1 + 0.1 * rng.standard_normal(m)).astype(np.float32)), 2 * onorm)
+    x2 = (2 * rng.standard_normal(2 * m)).astype(np.float32)    # x, or [gate | up]
+    res = rng.standard_normal(n).astype(np.float32)
+    ox, oxs, oy, oyf, ores = 0, 2 * m, 3 * m, 3 * m + n, 3 * m + 2 * n
+    a = arena(ctx, 3 * m + 3 * n)
+    put(a, ox, x2)
+    eps = 1e-5
+
+    def separate(pre, post):
+        if pre == q8hip.PRE_RMSNORM:
+            q8hip.rmsnorm(ctx, w, onorm, a, ox, oxs, 1, m, eps)
+        else:
+            put(a, oxs, x2[:m])
+            if pre == q8hip.PRE_SWIGLU:
+                q8hip.swiglu(ctx, a, oxs, ox + m, m)
+        q8hip.linear(ctx, w, 0, a, oxs, oy, 1, m, n, G, scale)
+        if post == q8hip.POST_RESIDUAL:
+            put(a, ores, res)
+            q8hip.add(ctx, a, ores, oy, n)
+        if post == q8hip.POST_SWIGLU:
+            q8hip.swiglu(ctx, a, oy, oy + n // 2, n // 2)
+            return get(a, oy, (n // 2,))
+        return get(a, oy, (n,))
+
+    for pre, post in FUSED_CASES:
+        want = separate(pre, post)
+        assert np.all(np.isfinite(want)) and np.std(want) > 0
+        put(a, ores, res)
+        q8hip.linear_fused(ctx, w, 0, a, ox, oyf, m, n, G, scale, pre, onorm, eps, post, ores)
+        got = get(a, oyf, want.shape)
+        if pre == q8hip.PRE_RMSNORM or (post == q8hip.POST_SWIGLU and m > 4096):
+            assert np.all(np.isfinite(got)) and max_rel_err(got, want) <= 1e-5, (pre, post)
+        else:
+            assert np.array_equal(got, want), (pre, post)
+        if post == q8hip.POST_RESIDUAL:           # residual in place
+            put(a, oyf, res)
+            q8hip.linear_fused(ctx, w, 0, a, ox, oyf, m, n, G, scale, pre, onorm, eps, post, oyf)
+            got2 = get(a, oyf, want.shape)
+            assert np.array_equal(got2, got), (pre, post, "in place")
+    for b in (a, w):
+        b.free()
+
+
+def test_fused_model_equals_unfused(ctx):
+    """One-row steps with the folded launches give the logits of the
+    separate rmsnorm / swiglu / add launches within max-rel-err 1e-5 (the
+    norm factor is applied after the GEMV) and the same greedy ids."""
+    say("fused model")
+    spec, t, inv = tiny_model(seed=7)
+    maxlen = 24
+    a = gpu_model(ctx, spec, t, maxlen, fuse=True)
+    b = gpu_model(ctx, spec, t, maxlen, fuse=False)
+    try:
+        la, lb = a.forward([5, 6, 7]), b.forward([5, 6, 7])
+        assert max_rel_err(la, lb) <= 1e-5
+        tok = int(np.argmax(lb))
+        for _ in range(5):
+            la, lb = a.forward([tok]), b.forward([tok])
+            assert np.all(np.isfinite(la)) and max_rel_err(la, lb) <= 1e-5
+            assert int(np.argmax(la)) == int(np.argmax(lb))
+            tok = int(np.argmax(lb))
+    finally:
+        a.close()
+        b.close()
 
 
 @pytest.mark.parametrize("G,scale", [(64, "f16"), (32, "f32")])
