@@ -161,9 +161,9 @@ int q8_embed_gather(q8_ctx *ctx, q8_buf *w, uint64_t oemb_u16, q8_buf *ids,
  *                     fused gate|up weights); y = silu(W_g x~) * (W_u x~), n/2
  *                     floats (as q8_linear + q8_swiglu)
  * x must not overlap y.  Without Q8_PRE_RMSNORM the results equal the
- * separate calls to the bit.  Needs m <= 16384, m % 32 == 0, 16-byte
- * aligned rows and x and 8-byte aligned norm weights (Q8_ERR_UNSUPPORTED
- * otherwise).
+ * separate calls to the bit.  Needs m % 32 == 0, 16-byte aligned rows and
+ * x, 8-byte aligned norm weights and, with a prologue, m <= 16384
+ * (Q8_ERR_UNSUPPORTED otherwise).
  * Replaces rmsnorm_op + mm_q8_op, mm_q8_op + swiglu_mul_op and mm_q8_op +
  * res_add_op / add_op of run_layer_q8 (src/llama_q8.mojo:144-230). */
 #define Q8_PRE_NONE 0

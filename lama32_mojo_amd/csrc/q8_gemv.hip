@@ -30,7 +30,11 @@ namespace q8 {
 namespace {
 
 constexpr int kWaves = 4;               // wavefronts per workgroup
-constexpr int kLdsFloats = 16384;       // x staged in LDS up to 64 KiB
+constexpr int kLdsFloats = 16384;       // fused prologues stage x in LDS up to 64 KiB
+// Plain x is staged only up to 32 KiB: a larger stage caps the workgroups
+// per CU (160 KiB of LDS) below what the grid needs for one round, and the
+// waves read x from L2 just as well.
+constexpr int kLdsStageFloats = 8192;
 
 template <int G, int KIND, int S, int R, int SPLITK, bool XLDS, int PRE = PRE_NONE,
           int POST = POST_STORE, int NPF = 1>
@@ -105,32 +109,45 @@ __global__ __launch_bounds__(256) void gemv_kernel(
   if constexpr (XLDS) {
     const int64_t tot = S * m;   // multiple of 4 (m % 32 == 0)
     float ss = 0.0f;
-    for (int64_t i = 4 * threadIdx.x; i < tot; i += 4 * blockDim.x) {
-      if constexpr (PRE == PRE_SWIGLU) {
-        // x holds [gate | up]: 2m floats
-        const f32x4 gv = *reinterpret_cast<const f32x4 *>(x + i);
-        const f32x4 uv = *reinterpret_cast<const f32x4 *>(x + m + i);
-        f32x4 o;
-        o.x = (gv.x / (1.0f + expf(-gv.x))) * uv.x;
-        o.y = (gv.y / (1.0f + expf(-gv.y))) * uv.y;
-        o.z = (gv.z / (1.0f + expf(-gv.z))) * uv.z;
-        o.w = (gv.w / (1.0f + expf(-gv.w))) * uv.w;
+    // batches of XB independent 16-byte loads per thread, then the LDS
+    // stores (a load-store-load chain would wait on L2 once per step)
+    constexpr int XB = 4;
+    for (int64_t i0 = 4 * threadIdx.x; i0 < tot; i0 += 4 * 256 * XB) {
+      f32x4 xv[XB], uv[XB];
+      uint2 wb[XB];
+#pragma unroll
+      for (int u = 0; u < XB; ++u) {
+        const int64_t i = i0 + 4 * 256 * u;
+        if (i < tot) {
+          xv[u] = *reinterpret_cast<const f32x4 *>(x + i);
+          if constexpr (PRE == PRE_SWIGLU) uv[u] = *reinterpret_cast<const f32x4 *>(x + m + i);
+          if constexpr (PRE == PRE_RMSNORM) wb[u] = *reinterpret_cast<const uint2 *>(wn + i);
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < XB; ++u) {
+        const int64_t i = i0 + 4 * 256 * u;
+        if (i >= tot) continue;
+        f32x4 o = xv[u];
+        if constexpr (PRE == PRE_SWIGLU) {
+          // x holds [gate | up]: 2m floats
+          const f32x4 gv = xv[u];
+          o.x = (gv.x / (1.0f + expf(-gv.x))) * uv[u].x;
+          o.y = (gv.y / (1.0f + expf(-gv.y))) * uv[u].y;
+          o.z = (gv.z / (1.0f + expf(-gv.z))) * uv[u].z;
+          o.w = (gv.w / (1.0f + expf(-gv.w))) * uv[u].w;
+        } else if constexpr (PRE == PRE_RMSNORM) {
+          const f32x4 v4 = xv[u];
+          ss = __builtin_fmaf(v4.x, v4.x, ss);
+          ss = __builtin_fmaf(v4.y, v4.y, ss);
+          ss = __builtin_fmaf(v4.z, v4.z, ss);
+          ss = __builtin_fmaf(v4.w, v4.w, ss);
+          o.x = bf16_bits_to_f32(wb[u].x & 0xffffu) * v4.x;
+          o.y = bf16_bits_to_f32(wb[u].x >> 16) * v4.y;
+          o.z = bf16_bits_to_f32(wb[u].y & 0xffffu) * v4.z;
+          o.w = bf16_bits_to_f32(wb[u].y >> 16) * v4.w;
+        }
         *reinterpret_cast<f32x4 *>(xs + i) = o;
-      } else if constexpr (PRE == PRE_RMSNORM) {
-        const f32x4 xv = *reinterpret_cast<const f32x4 *>(x + i);
-        const uint2 wb = *reinterpret_cast<const uint2 *>(wn + i);
-        ss = __builtin_fmaf(xv.x, xv.x, ss);
-        ss = __builtin_fmaf(xv.y, xv.y, ss);
-        ss = __builtin_fmaf(xv.z, xv.z, ss);
-        ss = __builtin_fmaf(xv.w, xv.w, ss);
-        f32x4 o;
-        o.x = bf16_bits_to_f32(wb.x & 0xffffu) * xv.x;
-        o.y = bf16_bits_to_f32(wb.x >> 16) * xv.y;
-        o.z = bf16_bits_to_f32(wb.y & 0xffffu) * xv.z;
-        o.w = bf16_bits_to_f32(wb.y >> 16) * xv.w;
-        *reinterpret_cast<f32x4 *>(xs + i) = o;
-      } else {
-        *reinterpret_cast<f32x4 *>(xs + i) = *reinterpret_cast<const f32x4 *>(x + i);
       }
     }
     if constexpr (PRE == PRE_RMSNORM) {
@@ -273,7 +290,7 @@ hipError_t launch_fast(const LinearArgs &a, const float *x, float *y, int64_t ca
   const int64_t rows_per_group = SPLITK > 1 ? R : kWaves * R;
   const int64_t tiles = (a.n + rows_per_group - 1) / rows_per_group;
   dim3 grid(grid_for(tiles, cap)), block(256);
-  if (S * a.m <= kLdsFloats) {
+  if (S * a.m <= kLdsStageFloats) {
     size_t lds = (size_t)S * a.m * sizeof(float);
     hipLaunchKernelGGL((gemv_kernel<G, KIND, S, R, SPLITK, true, PRE_NONE, POST_STORE, NPF>), grid,
                        block, lds, st, a.w, a.row_bytes, a.n, x, a.m, y, nullptr, 0.0f, nullptr);
@@ -341,9 +358,17 @@ hipError_t launch_fused_t(const FusedLinearArgs &f, int64_t cap, hipStream_t st)
   const int64_t rows_per_group = SPLITK > 1 ? RO : kWaves * RO;
   const int64_t tiles = (nout + rows_per_group - 1) / rows_per_group;
   dim3 grid(grid_for(tiles, cap)), block(256);
+  const float *x = reinterpret_cast<const float *>(a.x);
+  if constexpr (PRE == PRE_NONE) {
+    if (a.m > kLdsStageFloats) {
+      hipLaunchKernelGGL((gemv_kernel<G, KIND, 1, R, SPLITK, false, PRE, POST, NPF>), grid, block,
+                         0, st, a.w, a.row_bytes, a.n, x, a.m, a.y, f.wn, f.eps, f.res);
+      return hipGetLastError();
+    }
+  }
   hipLaunchKernelGGL((gemv_kernel<G, KIND, 1, R, SPLITK, true, PRE, POST, NPF>), grid, block,
-                     (size_t)a.m * sizeof(float), st, a.w, a.row_bytes, a.n,
-                     reinterpret_cast<const float *>(a.x), a.m, a.y, f.wn, f.eps, f.res);
+                     (size_t)a.m * sizeof(float), st, a.w, a.row_bytes, a.n, x, a.m, a.y, f.wn,
+                     f.eps, f.res);
   return hipGetLastError();
 }
 
@@ -386,7 +411,7 @@ bool gemv_fused_supported(const FusedLinearArgs &f) {
   const int pre = f.pre, post = f.post;
   const int sb = a.kind == SCALE_F16 ? 2 : 4;
   if (pre == PRE_RMSNORM && reinterpret_cast<uintptr_t>(f.wn) % 8 != 0) return false;
-  return a.s == 1 && !a.x_is_bf16 && a.m <= kLdsFloats && a.m % 32 == 0 &&
+  return a.s == 1 && !a.x_is_bf16 && (pre == PRE_NONE || a.m <= kLdsFloats) && a.m % 32 == 0 &&
          (a.G == 32 || a.G == 64) && reinterpret_cast<uintptr_t>(a.w) % 16 == 0 &&
          a.row_bytes % 16 == 0 && ((a.m / a.G) * sb) % 16 == 0 &&
          reinterpret_cast<uintptr_t>(a.x) % 16 == 0 && pre >= PRE_NONE && pre <= PRE_SWIGLU &&

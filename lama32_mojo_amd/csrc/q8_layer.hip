@@ -488,9 +488,10 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(
 
 // Merge of the partial records of attn_decode_kernel: block h (256 threads)
 // stages head h's records of all nsplit splits in LDS (independent loads,
-// issued before the position is known), then thread d < HD forms o[d] / l
-// over the active splits.  Does nothing when one block per KV head was
-// active (it wrote the output itself).
+// issued before the position is known); one wave forms each active split's
+// factor exp(m_x - M) and the total l = sum_x l_x exp(m_x - M); then thread
+// d < HD forms o[d] = sum_x f_x o_x[d] / l.  Does nothing when one block per
+// KV head was active (it wrote the output itself).
 template <int HD, int GRP>
 __global__ __launch_bounds__(256) void attn_merge_kernel(const float *__restrict__ part,
                                                          float *__restrict__ out, int nsplit,
@@ -499,12 +500,23 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(const float *__restrict
   constexpr int KC = decode_attn_chunk(HD), NW = 4;
   constexpr int PR = HD + 2;
   constexpr int WPH = NW / (GRP < NW ? GRP : NW);
+  static_assert(kDecodeAttnMaxSplit <= 64, "one wave forms the split factors");
   __shared__ float rs[kDecodeAttnMaxSplit * PR];
+  __shared__ float fac[kDecodeAttnMaxSplit];
+  __shared__ float lsum;
   const int h = blockIdx.x, g = h / GRP, hh = h % GRP;
   const float *recs = part + (int64_t)g * nsplit * (GRP * PR) + hh * PR;
-  for (int t = threadIdx.x; t < nsplit * PR; t += 256) {
-    const int x = t / PR, e = t % PR;
-    rs[t] = recs[x * GRP * PR + e];
+  // batches of 8 independent loads per thread, then the LDS stores
+  for (int t0 = threadIdx.x; t0 < nsplit * PR; t0 += 256 * 8) {
+    float r[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int t = t0 + 256 * u;
+      r[u] = t < nsplit * PR ? recs[(t / PR) * GRP * PR + t % PR] : 0.0f;
+    }
+#pragma unroll
+    for (int u = 0; u < 8; ++u)
+      if (t0 + 256 * u < nsplit * PR) rs[t0 + 256 * u] = r[u];
   }
   const int pos0 = posp ? *posp : pos0_host;
   const int nctx = pos0 < maxlen ? pos0 + 1 : maxlen;
@@ -513,16 +525,20 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(const float *__restrict
   const int active = (chunks + cpb - 1) / cpb;
   if (active <= 1) return;
   __syncthreads();
+  if (threadIdx.x < 64) {
+    const int x = threadIdx.x;
+    const float mx = x < active ? rs[x * PR + HD] : -INFINITY;
+    const float big = wave_max(mx);
+    const float f = x < active ? expf(mx - big) : 0.0f;
+    const float l = wave_sum(x < active ? rs[x * PR + HD + 1] * f : 0.0f);
+    fac[x] = f;
+    if (x == 0) lsum = l;
+  }
+  __syncthreads();
   for (int d = threadIdx.x; d < HD; d += 256) {
-    float mx = -INFINITY;
-    for (int x = 0; x < active; ++x) mx = fmaxf(mx, rs[x * PR + HD]);
-    float l = 0.0f, o = 0.0f;
-    for (int x = 0; x < active; ++x) {
-      const float f = expf(rs[x * PR + HD] - mx);
-      l = __builtin_fmaf(rs[x * PR + HD + 1], f, l);
-      o = __builtin_fmaf(rs[x * PR + d], f, o);
-    }
-    out[h * HD + d] = o / l;
+    float o = 0.0f;
+    for (int x = 0; x < active; ++x) o = __builtin_fmaf(rs[x * PR + d], fac[x], o);
+    out[h * HD + d] = o / lsum;
   }
 }
 

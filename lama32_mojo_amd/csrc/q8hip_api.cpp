@@ -568,8 +568,9 @@ int q8_linear_fused(q8_ctx *ctx, q8_buf *w, uint64_t owt_u16, q8_buf *a, uint64_
   f.eps = eps;
   f.res = post == Q8_POST_RESIDUAL ? fptr(a, ores_f32) : nullptr;
   if (!q8::gemv_fused_supported(f))
-    return fail(ctx, Q8_ERR_UNSUPPORTED, "q8_linear_fused: m=%lld (needs m <= 16384, m %% 32 == 0, "
-                "16-byte aligned rows and x, 8-byte aligned norm weights)", (long long)m);
+    return fail(ctx, Q8_ERR_UNSUPPORTED, "q8_linear_fused: m=%lld (needs m %% 32 == 0, 16-byte "
+                "aligned rows and x, 8-byte aligned norm weights and, with a prologue, "
+                "m <= 16384)", (long long)m);
   if (ctx->host_only) return fail(ctx, Q8_ERR_NODEVICE, "q8_linear_fused: host-only context");
   if (n == 0) return ok(ctx);
   if (int rc = set_device(ctx)) return rc;

@@ -112,6 +112,15 @@ def lib() -> ctypes.CDLL:
         if not os.path.exists(LIB_PATH):
             raise RuntimeError(
                 f"{LIB_PATH} not found: build it with `python -m lama32_mojo_amd.build`")
+        # torch ships its own libamdhip64.so.7 under the same SONAME; whichever
+        # copy loads first serves the whole process.  Load torch's first when
+        # torch is present, so the process has one HIP runtime in one order
+        # whether or not the caller touches torch later (torch cannot find the
+        # GPU when it comes second).
+        try:
+            import torch  # noqa: F401
+        except ImportError:
+            pass
         cdll = ctypes.CDLL(LIB_PATH)
         for name, (res, args) in SIGNATURES.items():
             fn = getattr(cdll, name)

@@ -124,11 +124,14 @@ def test_linear_fused_validation(hctx):
                    onorm_u16=norm + 2)[0] == q8hip.Q8_ERR_UNSUPPORTED
     # x past the arena (swiglu: 2m floats)
     assert code_of(F, hctx, w, 0, a, 14000, 0, m, n, pre=P.PRE_SWIGLU)[0] == Q8_ERR_RANGE
-    # rows too long to stage x on chip
+    # rows too long to stage a normalised x on chip (a plain x is read from L2)
     big = 32768
-    wb = hctx.alloc(2 * q8hip.rowstride_u16(big))
+    rsb = q8hip.rowstride_u16(big)
+    wb = hctx.alloc(2 * (rsb + big))
     ab = hctx.alloc(4 * (big + 16))
-    assert code_of(F, hctx, wb, 0, ab, 0, big, big, 1)[0] == q8hip.Q8_ERR_UNSUPPORTED
+    assert code_of(F, hctx, wb, 0, ab, 0, big, big, 1, pre=P.PRE_RMSNORM,
+                   onorm_u16=rsb)[0] == q8hip.Q8_ERR_UNSUPPORTED
+    assert code_of(F, hctx, wb, 0, ab, 0, big, big, 1)[0] == Q8_ERR_NODEVICE
 
 
 def test_linear_bf16act_validation(hctx):
