@@ -5,10 +5,12 @@ Default workload -- Llama-3.2-1B decode step, batch 1, at a KV context of
 1024 tokens: the whole token step of the reference's Q8 model
 (qwen3_mojo/src/qwen_q8.mojo:127-162 with run_layer_q8,
 src/llama_q8.mojo:144-230) on libq8hip -- embedding gather, 16 layers of
-[rmsnorm, fused q|k|v GEMV 2048->3072, RoPE + fp16 KV append, attention,
-o GEMV 2048->2048, add + rmsnorm, fused gate|up GEMV 2048->16384, swiglu,
-down GEMV 8192->2048, add], final rmsnorm, tied lm_head GEMV 2048->128256 and
-argmax.  Weights are random bf16 ~N(0, 0.02) per tensor, packed on the GPU by
+[rmsnorm + fused q|k|v GEMV 2048->3072, RoPE + fp16 KV append + attention
+(context splits, then their merge), o GEMV 2048->2048 + residual, rmsnorm +
+fused gate|up GEMV 2048->16384 + swiglu, down GEMV 8192->2048 + residual],
+final rmsnorm + tied lm_head GEMV 2048->128256, argmax: six launches per
+layer, the norms, swiglu and residual adds folded into the GEMVs.  Weights
+are random bf16 ~N(0, 0.02) per tensor, packed on the GPU by
 q8_quantize_pack into one weight arena (G=64, f16 scales: the reference
 layout); norms ~1; the 1024-token KV context is random fp16.
 
@@ -34,6 +36,9 @@ Other workloads (--workload):
   prefill  Llama-3.2-1B prefill linears, M = 512 bf16 activations, all 16
            layers x 7 unfused projections on the MFMA GEMM (TFLOP/s), group 32
   qwen8b   Qwen3-8B decode linears, --batch 1 / 4 / 16, group 32
+  e2e-8b   Llama-3.1-8B end to end: prefill of 2048 random ids (seed 3),
+           then 256 greedy decode steps (one HIP graph per token); value is
+           decode tok/s, config holds the prefill time
 """
 
 from __future__ import annotations
@@ -65,7 +70,8 @@ def parse():
     p.add_argument("--steps", type=int, default=50)
     p.add_argument("--warmup", type=int, default=5)
     p.add_argument("--workload", default="decode",
-                   choices=["decode", "decode-linears", "linear", "prefill", "qwen8b"])
+                   choices=["decode", "decode-linears", "linear", "prefill", "qwen8b",
+                            "e2e-8b"])
     p.add_argument("--layout", default=None, choices=["g64f16", "g32f32"],
                    help="packed layout (default: g64f16; g32f32 for --workload linear)")
     p.add_argument("--batch", type=int, default=1)
@@ -340,10 +346,11 @@ def run_decode_model(B: Bench, ctxlen: int = 1024):
         "data": "synthetic (random-init N(0,0.02) bf16 weights packed on GPU, norms ~1; "
                 "random fp16 KV context)",
         "config": {"workload": f"{cfg.name} decode step batch 1 at KV context {ctxlen}: "
-                               f"embedding gather, {cfg.layers} layers (rmsnorm, fused q|k|v "
-                               "GEMV, RoPE + fp16 KV append, attention, o GEMV, add+rmsnorm, "
-                               "fused gate|up GEMV, swiglu, down GEMV, add), final norm, "
-                               f"lm_head GEMV {n_h}x{m_h}, argmax; one HIP graph per token",
+                               f"embedding gather, {cfg.layers} layers (rmsnorm + fused "
+                               "q|k|v GEMV, RoPE + fp16 KV append + attention, merge, o GEMV "
+                               "+ residual, rmsnorm + fused gate|up GEMV + swiglu, down GEMV "
+                               f"+ residual), final norm + lm_head GEMV {n_h}x{m_h}, argmax; "
+                               "one HIP graph per token",
                    "layout": f"G={G} {scale} scales", "batch": 1, "tok_s": round(tok_s, 1),
                    "weight_bytes_per_token": weight_bytes, "kv_bytes_per_token": kv_bytes,
                    "pct_hbm_peak": round(100 * value / HBM_PEAK_GBS, 1),
@@ -354,6 +361,77 @@ def run_decode_model(B: Bench, ctxlen: int = 1024):
                      "kernel": f"lm_head GEMV {n_h}x{m_h}: {head_bytes} B/launch, "
                                f"{head_ms * 1e3:.2f} us avg over {kk} launches"},
         "cpu_baseline": cpu,
+    }
+
+
+def run_e2e_8b(B: Bench, prompt: int = 2048, gen: int = 256):
+    """Llama-3.1-8B: prefill `prompt` random ids, then `gen` greedy steps."""
+    from lama32_mojo_amd import model as gm
+
+    args, q8hip, ctx, torch = B.args, B.q8hip, B.ctx, B.torch
+    G, scale, sb = B.G, B.scale, B.sb
+    cfg = gm.LLAMA_31_8B
+    m = gm.Q8Llama(ctx, cfg, prompt + gen + 8, G, scale, seed=3, max_prefill=prompt)
+    ids = np.random.default_rng(3).integers(0, cfg.vocab, size=prompt).tolist()
+    m.forward_argmax(ids[:64])                 # warm-up: first launches, then forget
+    m.reset()
+    torch.cuda.synchronize()
+    e0, e1 = B.events()
+    e0.record(B.stream)
+    first = m.forward_argmax(ids)
+    e1.record(B.stream)
+    torch.cuda.synchronize()
+    prefill_ms = e0.elapsed_time(e1)
+    # decode: capture, then replays that read the previous id on the device
+    steps = gen - 1
+    warm = min(args.warmup, 8)
+    m.decode_steps(first, warm)
+    ms, wall = B.time_steps(lambda: m.graph.launch(), steps - warm, 0)
+    m.n_cached += steps - warm
+    assert int(m.posbuf.download((1,), np.int32)[0]) == prompt + steps
+    tok_s = 1000.0 / ms
+    H, L, QD, KVD, I = cfg.hidden, cfg.layers, cfg.q_dim(), cfg.kv_dim(), cfg.inter
+    lin_flops = 2.0 * prompt * L * H * (QD + 2 * KVD + I * 3) + 2.0 * prompt * L * QD * H
+    weight_bytes = 2 * (m.w.top - 32)
+
+    # roofline kernel: the untied lm_head GEMV 128256 x 4096 over two copies
+    n_h, m_h = cfg.vocab, cfg.hidden
+    w2, offs2 = B.pack_arena([(n_h, m_h), (n_h, m_h)], [5, 6])
+    xa = B.activations(32 + m_h + n_h, 1)
+    a = q8hip.Buffer.wrap(ctx, xa.data_ptr(), 4 * (32 + m_h + n_h))
+    heads = [(lambda o=o: q8hip.linear(ctx, w2, o, a, 32, 32 + m_h, 1, m_h, n_h, G, scale))
+             for o in offs2]
+    head_ms, _ = B.time_steps(lambda: [h() for h in heads], 10, 2)
+    head_ms /= 2
+    head_bytes = linear_bytes(1, m_h, n_h, G, sb)
+    achieved = head_bytes / (head_ms * 1e-3) / 1e9
+    w2.free()
+    m.close()
+    return {
+        "metric": f"decode tok/s batch 1 after a {prompt}-token prefill, {cfg.name} Q8",
+        "value": round(tok_s, 1),
+        "unit": "tok/s",
+        "ms_per_step": round(ms, 4),
+        "higher_is_better": True,
+        "dtype": "int8xf32",
+        "data": "synthetic (random-init N(0,0.02) bf16 weights packed on GPU, norms ~1; "
+                "random prompt ids, seed 3)",
+        "config": {"workload": f"{cfg.name} end to end: prefill {prompt} ids (7 Q8 GEMMs per "
+                               "layer on MFMA with f32 activations as two bf16 terms, RoPE + "
+                               "fp16 KV append, causal attention), then "
+                               f"{gen} greedy steps of the captured decode graph",
+                   "layout": f"G={G} {scale} scales", "batch": 1,
+                   "prefill_ms": round(prefill_ms, 2),
+                   "prefill_linear_tflops": round(lin_flops / (prefill_ms * 1e-3) / 1e12, 1),
+                   "decode_ms_per_token": round(ms, 4),
+                   "decode_weight_gbs": round(weight_bytes / (ms * 1e-3) / 1e9, 1),
+                   "e2e_ms": round(prefill_ms + gen * ms, 1), "wall_s": round(wall, 3)},
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+                     "traffic": None,
+                     "kernel": f"lm_head GEMV {n_h}x{m_h}: {head_bytes} B/launch, "
+                               f"{head_ms * 1e3:.2f} us avg over 10 launches"},
+        "cpu_baseline": None,
     }
 
 
@@ -497,7 +575,8 @@ def main():
     if args.layout is None:
         # the reference layout for the Llama-3.2-1B decode step; group 32
         # with f32 scales where the workload is defined with it
-        args.layout = "g64f16" if args.workload in ("decode", "decode-linears") else "g32f32"
+        args.layout = ("g64f16" if args.workload in ("decode", "decode-linears", "e2e-8b")
+                       else "g32f32")
     import torch
     from lama32_mojo_amd import q8hip
     ctx = q8hip.Context(0)
@@ -506,6 +585,8 @@ def main():
         res = run_decode_model(B)
     elif args.workload == "decode-linears":
         res = run_decode(B, LLAMA_1B)
+    elif args.workload == "e2e-8b":
+        res = run_e2e_8b(B)
     elif args.workload == "qwen8b":
         res = run_decode(B, QWEN3_8B)
     elif args.workload == "linear":
