@@ -271,6 +271,59 @@ int q8_graph_end(q8_ctx *ctx, void **graph);
 int q8_graph_launch(q8_ctx *ctx, void *graph);
 void q8_graph_destroy(void *graph);
 
+/* ---- packed checkpoint files (safetensors) -----------------------------------
+ * Host code; no context needed except for q8_st_upload.  Errors return a
+ * Q8_ERR_* code with the message in q8_st_error() (per thread). */
+typedef struct q8_st q8_st;
+typedef struct q8_stw q8_stw;
+
+/* Open a safetensors model: a file, or a directory holding either
+ * model.safetensors.index.json (shards in order of first appearance in its
+ * weight_map) or model.safetensors.  Every header is parsed and checked
+ * (offsets inside the file, bytes = shape x dtype size).
+ * Replaces SafeTensors.__init__ (src/safetensors.mojo:36-84). */
+int q8_st_open(const char *path, q8_st **out);
+void q8_st_close(q8_st *st);
+const char *q8_st_error(void);
+/* Number of tensors (-1 for a null handle); index of `name` or -1
+ * (SafeTensors.num_tensors / has / get, src/safetensors.mojo:86-95). */
+int64_t q8_st_count(const q8_st *st);
+int64_t q8_st_find(const q8_st *st, const char *name);
+/* Tensor i: name, dtype string ("F16", "BF16", ...), rank and shape, shard
+ * path, absolute byte offset in that shard and byte count (TensorInfo,
+ * src/safetensors.mojo:17-33).  Any output pointer may be null; the
+ * strings and shape live until q8_st_close. */
+int q8_st_info(const q8_st *st, int64_t i, const char **name, const char **dtype, int *ndim,
+               const int64_t **shape, const char **path, uint64_t *begin, uint64_t *nbytes);
+/* The first shard's __metadata__ entries, in file order. */
+int64_t q8_st_metadata_count(const q8_st *st);
+int q8_st_metadata(const q8_st *st, int64_t i, const char **key, const char **value);
+/* Bytes [byte_off, byte_off + nbytes) of tensor i into host memory. */
+int q8_st_read(const q8_st *st, int64_t i, uint64_t byte_off, void *dst, uint64_t nbytes);
+/* Bytes [src_off, src_off + nbytes) of tensor i to byte offset byte_off of
+ * a device buffer, through the context's pinned staging (file reads
+ * overlap the copies); returns when the bytes are on the device.
+ * Replaces the per-tensor read + memcpy of Weights.upload_all
+ * (src/resident.mojo:30-58). */
+int q8_st_upload(q8_ctx *ctx, const q8_st *st, int64_t i, uint64_t src_off, uint64_t nbytes,
+                 q8_buf *buf, uint64_t byte_off);
+
+/* Write a safetensors file laid out as the safetensors library's
+ * serializer lays it out (the writer behind quantize.py's save_file,
+ * qwen3_mojo/scripts/quantize.py:59-61): tensors sorted by dtype (U64, I64,
+ * F64, F32, U32, I32, BF16, F16, U16, I16, F8_E4M3, F8_E5M2, I8, U8, BOOL),
+ * then by name; compact JSON, "__metadata__" (given key/value pairs, in the
+ * given order) first; header padded with spaces to a multiple of 8.  shapes
+ * holds the tensors' dims back to back.  The header is written at open;
+ * q8_stw_put writes tensor i (caller's order) in any order; q8_stw_close
+ * fails if a tensor was never written. */
+int q8_stw_open(const char *path, int64_t count, const char *const *names,
+                const char *const *dtypes, const int *ndims, const int64_t *shapes,
+                int64_t nmeta, const char *const *meta_keys, const char *const *meta_values,
+                q8_stw **out);
+int q8_stw_put(q8_stw *w, int64_t i, const void *data, uint64_t nbytes);
+int q8_stw_close(q8_stw *w);
+
 #ifdef __cplusplus
 }
 #endif

@@ -31,6 +31,10 @@ struct q8_ctx {
   // The decode attention's partial records use it too: both run in stream
   // order on this context.
   float *gemm_ws = nullptr;
+  // Pinned staging for file -> device uploads (q8_st_upload): two halves,
+  // allocated on first use.
+  void *stage = nullptr;
+  hipEvent_t stage_ev[2] = {nullptr, nullptr};
 };
 
 namespace {
@@ -169,6 +173,9 @@ void q8_destroy(q8_ctx *ctx) {
       (void)hipStreamDestroy(ctx->own);
     }
     if (ctx->gemm_ws) (void)hipFree(ctx->gemm_ws);
+    if (ctx->stage) (void)hipHostFree(ctx->stage);
+    for (hipEvent_t &ev : ctx->stage_ev)
+      if (ev) (void)hipEventDestroy(ev);
   }
   delete ctx;
 }
@@ -261,6 +268,61 @@ int q8_buf_upload(q8_ctx *ctx, q8_buf *buf, uint64_t byte_off, const void *src, 
   hipError_t e = hipMemcpyAsync(bytes(buf, byte_off), src, nbytes, hipMemcpyHostToDevice, ctx->stream);
   if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
   if (e != hipSuccess) return hip_fail(ctx, e, "q8_buf_upload");
+  return ok(ctx);
+}
+
+namespace {
+constexpr uint64_t kStageHalf = (uint64_t)32 << 20;   // bytes per staging half
+}
+
+int q8_st_upload(q8_ctx *ctx, const q8_st *st, int64_t i, uint64_t src_off, uint64_t nbytes,
+                 q8_buf *buf, uint64_t byte_off) {
+  if (int rc = check_ctx(ctx)) return rc;
+  if (!st || !buf) return fail(ctx, Q8_ERR_ARG, "q8_st_upload: null argument");
+  uint64_t size = 0;
+  const char *name = nullptr;
+  if (q8_st_info(st, i, &name, nullptr, nullptr, nullptr, nullptr, nullptr, &size) != Q8_OK)
+    return fail(ctx, Q8_ERR_ARG, "q8_st_upload: %s", q8_st_error());
+  if (src_off > size || nbytes > size - src_off)
+    return fail(ctx, Q8_ERR_RANGE, "q8_st_upload: [%llu, +%llu) exceeds '%s' (%llu bytes)",
+                (unsigned long long)src_off, (unsigned long long)nbytes, name,
+                (unsigned long long)size);
+  if (!fits(byte_off, nbytes, 1, buf->size))
+    return fail(ctx, Q8_ERR_RANGE, "q8_st_upload: [%llu, +%llu) exceeds buffer of %llu bytes",
+                (unsigned long long)byte_off, (unsigned long long)nbytes,
+                (unsigned long long)buf->size);
+  if (ctx->host_only) return fail(ctx, Q8_ERR_NODEVICE, "q8_st_upload: host-only context");
+  if (nbytes == 0) return ok(ctx);
+  if (int rc = set_device(ctx)) return rc;
+  hipError_t e = hipSuccess;
+  if (!ctx->stage) {
+    e = hipHostMalloc(&ctx->stage, 2 * kStageHalf, hipHostMallocDefault);
+    if (e != hipSuccess) {
+      ctx->stage = nullptr;
+      return hip_fail(ctx, e, "q8_st_upload: pinned staging");
+    }
+    for (hipEvent_t &ev : ctx->stage_ev)
+      if (e == hipSuccess) e = hipEventCreateWithFlags(&ev, hipEventDisableTiming);
+    if (e != hipSuccess) return hip_fail(ctx, e, "q8_st_upload: events");
+  }
+  // read chunk k into half k % 2 while the copy of chunk k - 1 runs
+  uint64_t done = 0;
+  for (int k = 0; done < nbytes && e == hipSuccess; ++k) {
+    const int h = k & 1;
+    const uint64_t n = nbytes - done < kStageHalf ? nbytes - done : kStageHalf;
+    char *half = static_cast<char *>(ctx->stage) + h * kStageHalf;
+    if (k >= 2) e = hipEventSynchronize(ctx->stage_ev[h]);   // half h is free again
+    if (e != hipSuccess) break;
+    if (q8_st_read(st, i, src_off + done, half, n) != Q8_OK) {
+      (void)hipStreamSynchronize(ctx->stream);
+      return fail(ctx, Q8_ERR_ARG, "q8_st_upload: %s", q8_st_error());
+    }
+    e = hipMemcpyAsync(bytes(buf, byte_off + done), half, n, hipMemcpyHostToDevice, ctx->stream);
+    if (e == hipSuccess) e = hipEventRecord(ctx->stage_ev[h], ctx->stream);
+    done += n;
+  }
+  if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+  if (e != hipSuccess) return hip_fail(ctx, e, "q8_st_upload");
   return ok(ctx);
 }
 

@@ -165,10 +165,13 @@ class Q8Llama:
         self.qk = Q8Kernels(ctx, G, scale)
         names = weight_names(cfg)
         self.w = Weights(ctx, arena_elems(cfg, G, scale))
-        if weights is not None:
-            self.w.upload_all(weights, names)
-        else:
+        if weights is None:
             self._random_weights(names, seed, std)
+        elif hasattr(weights, "upload") and hasattr(weights, "infos"):
+            self._check_checkpoint(weights, names)
+            self.w.upload_file(weights, names)
+        else:
+            self.w.upload_all(weights, names)
         self.lo = []
         for L in range(cfg.layers):
             p = f"model.layers.{L}."
@@ -207,6 +210,26 @@ class Q8Llama:
         self.graph_logits = None
 
     # ---- weights -------------------------------------------------------------
+    def _check_checkpoint(self, st, names: Sequence[str]) -> None:
+        """A packed file (checkpoint.pack_checkpoint / quantize.py) must hold
+        this model's tensors in this layout: packed rows [n, rowstride(m)]
+        as 2-byte elements, norms as bf16 vectors."""
+        from .checkpoint import checkpoint_layout
+        G, sc = checkpoint_layout(st)
+        if (G, sc) != (self.G, self.scale):
+            raise ValueError(f"checkpoint layout G={G} {sc}, model expects G={self.G} "
+                             f"{self.scale}")
+        shapes = tensor_shapes(self.cfg)
+        for name in names:
+            if not st.has(name):
+                raise KeyError(f"{name} is not in the checkpoint")
+            sh = shapes[name]
+            want = ([sh[0], q8_rowstride(sh[1], self.G, self.scale)] if len(sh) == 2
+                    else list(sh))
+            info = st.get(name)
+            if info.shape != want:
+                raise ValueError(f"{name}: shape {info.shape} in the checkpoint, expected {want}")
+
     def _random_weights(self, names: Sequence[str], seed: int, std: float) -> None:
         import torch
 

@@ -70,6 +70,26 @@ class Weights:
         self.offs.update(offs)
         self.top = top
 
+    def upload_file(self, st, names: Sequence[str]) -> None:
+        """Tensors straight from a safetensors model (checkpoint.SafeTensors)
+        into the arena, in `names` order, each copied file -> device through
+        pinned staging (resident.mojo:30-58 reads each tensor's byte range
+        and copies it into the mapped arena)."""
+        top = self.top
+        for name in names:
+            if not st.has(name):
+                raise KeyError(f"{name} is not in the checkpoint")
+            info = st.get(name)
+            if info.dtype not in ("F16", "BF16", "U16", "I16"):
+                raise ValueError(f"{name}: dtype {info.dtype} is not 2 bytes per element")
+            count = info.nbytes() // 2
+            if top + count > self.cap:
+                raise RuntimeError("weight arena overflow at " + name)
+            st.upload(self.ctx, name, self.buf, 2 * top)
+            self.offs[name] = top
+            top += count
+        self.top = top
+
 
 class Acts:
     """f32 activation arena with bump allocation and a resettable mark."""

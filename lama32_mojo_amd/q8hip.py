@@ -72,6 +72,26 @@ SIGNATURES = {
     "q8_linear_fused": (_I, [_P, _P, _U64, _P, _U64, _U64, _I64, _I64, _I, _I, _I, _U64,
                             ctypes.c_float, _I, _U64]),
     "q8_rmsnorm": (_I, [_P, _P, _U64, _P, _U64, _U64, _I64, _I64, ctypes.c_float]),
+    "q8_st_open": (_I, [ctypes.c_char_p, ctypes.POINTER(_P)]),
+    "q8_st_close": (None, [_P]),
+    "q8_st_error": (ctypes.c_char_p, []),
+    "q8_st_count": (_I64, [_P]),
+    "q8_st_find": (_I64, [_P, ctypes.c_char_p]),
+    "q8_st_info": (_I, [_P, _I64, ctypes.POINTER(ctypes.c_char_p), ctypes.POINTER(ctypes.c_char_p),
+                        ctypes.POINTER(_I), ctypes.POINTER(ctypes.POINTER(_I64)),
+                        ctypes.POINTER(ctypes.c_char_p), ctypes.POINTER(_U64),
+                        ctypes.POINTER(_U64)]),
+    "q8_st_metadata_count": (_I64, [_P]),
+    "q8_st_metadata": (_I, [_P, _I64, ctypes.POINTER(ctypes.c_char_p),
+                            ctypes.POINTER(ctypes.c_char_p)]),
+    "q8_st_read": (_I, [_P, _I64, _U64, _P, _U64]),
+    "q8_st_upload": (_I, [_P, _P, _I64, _U64, _U64, _P, _U64]),
+    "q8_stw_open": (_I, [ctypes.c_char_p, _I64, ctypes.POINTER(ctypes.c_char_p),
+                         ctypes.POINTER(ctypes.c_char_p), ctypes.POINTER(_I),
+                         ctypes.POINTER(_I64), _I64, ctypes.POINTER(ctypes.c_char_p),
+                         ctypes.POINTER(ctypes.c_char_p), ctypes.POINTER(_P)]),
+    "q8_stw_put": (_I, [_P, _I64, _P, _U64]),
+    "q8_stw_close": (_I, [_P]),
     "q8_add_rmsnorm": (_I, [_P, _P, _U64, _P, _U64, _U64, _U64, _U64, _I64, _I64,
                            ctypes.c_float]),
     "q8_rope_kv": (_I, [_P, _P, _U64, _U64, _U64, _U64, _P, _U64, _U64, _I64, _I64, _I64, _P,
