@@ -39,6 +39,14 @@ Other workloads (--workload):
   e2e-8b   Llama-3.1-8B end to end: prefill of 2048 random ids (seed 3),
            then 256 greedy decode steps (one HIP graph per token); value is
            decode tok/s, config holds the prefill time
+  lmhead-pmc  the launches the HBM-traffic counter passes read: 3 copies of
+           1 GiB by torch's copy kernel (the calibration of known size), then
+           8 lm_head GEMVs 128256x2048 alternating over two tables
+
+`roofline.traffic` (default workload) is the lm_head GEMV's HBM bytes per
+launch measured by rocprofv3 FETCH_SIZE and WRITE_SIZE passes over
+--workload lmhead-pmc, each scaled by the copy kernel's known bytes / its
+counter reading; the figures are read from profiles/lm_head_gemv_pmc.md.
 """
 
 from __future__ import annotations
@@ -71,7 +79,7 @@ def parse():
     p.add_argument("--warmup", type=int, default=5)
     p.add_argument("--workload", default="decode",
                    choices=["decode", "decode-linears", "linear", "prefill", "qwen8b",
-                            "e2e-8b"])
+                            "e2e-8b", "lmhead-pmc"])
     p.add_argument("--layout", default=None, choices=["g64f16", "g32f32"],
                    help="packed layout (default: g64f16; g32f32 for --workload linear)")
     p.add_argument("--batch", type=int, default=1)
@@ -262,7 +270,7 @@ def run_decode(B: Bench, cfg):
                    "wall_s": round(wall, 3)},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
-                     "traffic": None,
+                     "traffic": measured_traffic(G, sb),
                      "kernel": f"lm_head GEMV {n_h}x{m_h}: {head_bytes} B/launch, "
                                f"{head_ms * 1e3:.2f} us avg over {kk} launches"},
         "cpu_baseline": cpu,
@@ -272,6 +280,21 @@ def run_decode(B: Bench, cfg):
 # ---------------------------------------------------------------------------
 # full decode step (Llama-3.2-1B model on the layer kernels, captured graph)
 # ---------------------------------------------------------------------------
+
+def measured_traffic(G: int, sb: int):
+    """The lm_head GEMV's HBM bytes per launch from the committed counter
+    passes (profiles/lm_head_gemv_pmc.md), for the layout they measured."""
+    if (G, sb) != (64, 2):
+        return None
+    try:
+        with open(os.path.join(ROOT, "profiles", "lm_head_gemv_pmc.md")) as f:
+            for line in f:
+                if line.strip().startswith("- traffic_bytes_per_launch:"):
+                    return int(line.split(":", 1)[1])
+    except OSError:
+        pass
+    return None
+
 
 def run_decode_model(B: Bench, ctxlen: int = 1024):
     from lama32_mojo_amd import model as gm
@@ -357,11 +380,39 @@ def run_decode_model(B: Bench, ctxlen: int = 1024):
                    "graph": True, "wall_s": round(wall, 3)},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
-                     "traffic": None,
+                     "traffic": measured_traffic(G, sb),
                      "kernel": f"lm_head GEMV {n_h}x{m_h}: {head_bytes} B/launch, "
                                f"{head_ms * 1e3:.2f} us avg over {kk} launches"},
         "cpu_baseline": cpu,
     }
+
+
+def run_lmhead_pmc(B: Bench):
+    """The launches the counter passes read (see the module docstring)."""
+    q8hip, ctx, torch = B.q8hip, B.ctx, B.torch
+    G, scale, sb = B.G, B.scale, B.sb
+    nbytes = 1 << 30
+    src = torch.empty(nbytes // 4, dtype=torch.float32, device="cuda").normal_()
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    del src, dst
+    n_h, m_h = LLAMA_1B["vocab"], LLAMA_1B["hidden"]
+    w2, offs2 = B.pack_arena([(n_h, m_h), (n_h, m_h)], [5, 6])
+    xa = B.activations(32 + m_h + n_h, 1)
+    a = q8hip.Buffer.wrap(ctx, xa.data_ptr(), 4 * (32 + m_h + n_h))
+    for i in range(8):
+        q8hip.linear(ctx, w2, offs2[i % 2], a, 32, 32 + m_h, 1, m_h, n_h, G, scale)
+    ctx.sync()
+    w2.free()
+    return {"metric": "counter-pass launches (no timing)", "value": 0, "unit": "none",
+            "ms_per_step": 0.0, "higher_is_better": True, "dtype": "int8xf32",
+            "data": "synthetic", "config": {"workload": "3 x 1 GiB copy, 8 x lm_head GEMV "
+                                                        f"{n_h}x{m_h}",
+                                            "copy_bytes": nbytes,
+                                            "lm_head_bytes": linear_bytes(1, m_h, n_h, G, sb)}}
 
 
 def run_e2e_8b(B: Bench, prompt: int = 2048, gen: int = 256):
@@ -575,7 +626,8 @@ def main():
     if args.layout is None:
         # the reference layout for the Llama-3.2-1B decode step; group 32
         # with f32 scales where the workload is defined with it
-        args.layout = ("g64f16" if args.workload in ("decode", "decode-linears", "e2e-8b")
+        args.layout = ("g64f16" if args.workload in ("decode", "decode-linears", "e2e-8b",
+                                                     "lmhead-pmc")
                        else "g32f32")
     import torch
     from lama32_mojo_amd import q8hip
@@ -585,6 +637,8 @@ def main():
         res = run_decode_model(B)
     elif args.workload == "decode-linears":
         res = run_decode(B, LLAMA_1B)
+    elif args.workload == "lmhead-pmc":
+        res = run_lmhead_pmc(B)
     elif args.workload == "e2e-8b":
         res = run_e2e_8b(B)
     elif args.workload == "qwen8b":
