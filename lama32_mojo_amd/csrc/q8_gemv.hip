@@ -280,9 +280,10 @@ int grid_for(int64_t tiles, int64_t cap) {
   return (int)(tiles < cap ? (tiles > 0 ? tiles : 1) : cap);
 }
 
-// NPF: K steps in flight per wave (registers against occupancy: one step for
-// the many-round vocabulary heads, two for 4-row waves, four for 1-row waves)
-template <int R, int S> constexpr int npf_for() { return R * S >= 8 ? 1 : R * S >= 4 ? 2 : 4; }
+// NPF: K steps in flight per wave (registers against occupancy: one step
+// for waves of 2 or more rows -- measured no slower than two on the decode
+// shapes, with more waves per SIMD -- and four for 1-row waves)
+template <int R, int S> constexpr int npf_for() { return R * S >= 4 ? 1 : 4; }
 
 template <int G, int KIND, int S, int R, int SPLITK, int NPF = npf_for<R, S>()>
 hipError_t launch_fast(const LinearArgs &a, const float *x, float *y, int64_t cap,
