@@ -222,22 +222,25 @@ int q8_attention(q8_ctx *ctx, q8_buf *a, uint64_t oq_f32, q8_buf *kv,
                  q8_buf *posbuf, uint64_t opos_i32, int nheads, int nkv,
                  int head_dim);
 
-/* Decode step of one new token (s = 1): RoPE of q at oq and k at ok, append
- * of the rotated k and of v at ov to cache row pos0 (as q8_rope_kv) and
- * causal attention of the token over rows 0 .. pos0 into out at oy (as
+/* Decode step of one new token (s = 1): with wn non-null, per-head RMSNorm
+ * of q and of k first (the head_dim bf16 weights at oqnorm / oknorm of wn,
+ * eps; k_rmsnorm2_w, src/llama_common.mojo:228-270, the same values as
+ * q8_rmsnorm over the head rows); RoPE of q at oq and k at ok, append of the
+ * rotated k and of v at ov to cache row pos0 (as q8_rope_kv) and causal
+ * attention of the token over rows 0 .. pos0 into out at oy (as
  * q8_attention), in two launches (context splits, then their merge).  q and
- * k in the arena are left unrotated.  The split records live in the
+ * k in the arena are left as they were.  The split records live in the
  * context's workspace, so calls on one context must not overlap (they do
  * not when issued on its stream).  head_dim 64 or 128, nheads / nkv in
  * {1, 2, 4, 8}; a cache block must stay under 2 GiB; position as in
  * q8_rope_kv.
- * Replaces the per-token attention of run_layer_q8 (src/llama_q8.mojo:144-230:
- * k_rope_qk_copy2, k_scores, k_softmax_rows, k_att_out). */
+ * Replaces the per-token attention of run_layer_q8 (src/llama_q8.mojo:171-205:
+ * k_rmsnorm2_w, k_rope_qk_copy2, k_scores, k_softmax_rows, k_att_out). */
 int q8_decode_attention(q8_ctx *ctx, q8_buf *a, uint64_t oq_f32, uint64_t ok_f32,
-                        uint64_t ov_f32, uint64_t oinv_f32, q8_buf *kv,
-                        uint64_t okc_f16, uint64_t ovc_f16, int64_t maxlen,
-                        uint64_t oy_f32, int64_t pos0, q8_buf *posbuf,
-                        uint64_t opos_i32, int nheads, int nkv, int head_dim);
+                        uint64_t ov_f32, uint64_t oinv_f32, q8_buf *kv, uint64_t okc_f16,
+                        uint64_t ovc_f16, int64_t maxlen, uint64_t oy_f32, int64_t pos0,
+                        q8_buf *posbuf, uint64_t opos_i32, int nheads, int nkv, int head_dim,
+                        q8_buf *wn, uint64_t oqnorm_u16, uint64_t oknorm_u16, float eps);
 
 /* g = silu(g) * u in place over n values (k_swiglu_mul,
  * src/llama_common.mojo:476-481). */

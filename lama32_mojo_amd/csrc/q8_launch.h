@@ -101,12 +101,15 @@ struct DecodeAttnArgs {
   __half *kc, *vc;         // cache blocks [maxlen, nkv*hd]
   float *out;              // [nheads*hd]
   float *part;             // scratch: nsplit * nheads * (hd + 2) floats
+  const uint16_t *qnorm = nullptr, *knorm = nullptr;   // per-head RMSNorm weights (hd bf16)
+  float eps = 0.0f;
   int nheads, nkv, head_dim, nsplit;
   const int *posp;         // device position (or null: pos0)
   int pos0, maxlen;
 };
-// RoPE of q and k, append of k and v at cache row pos0 and attention of the
-// one new token over rows 0 .. pos0: one launch of nsplit x nkv blocks over
+// Per-head RMSNorm of q and k (with qnorm / knorm), RoPE of q and k, append
+// of k and v at cache row pos0 and attention of the one new token over rows
+// 0 .. pos0: one launch of nsplit x nkv blocks over
 // context splits, then a merge launch.  Calls that share `part` must not
 // overlap.
 // Keys per chunk (one wave's unit of work) and the split count: one chunk

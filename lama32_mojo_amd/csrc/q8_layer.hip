@@ -269,7 +269,7 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(
     const float *__restrict__ q, const float *__restrict__ k, const float *__restrict__ v,
     const float *__restrict__ inv, __half *__restrict__ kc, __half *__restrict__ vc,
     float *__restrict__ part, float *__restrict__ out, int nkv, const int *posp, int pos0_host,
-    int maxlen) {
+    int maxlen, const uint16_t *__restrict__ qnw, const uint16_t *__restrict__ knw, float eps) {
   constexpr int KC = decode_attn_chunk(HD), NW = 4;
   constexpr int LPR = HD / 8;           // lanes per row (8 dims each)
   constexpr int RPI = 64 / LPR;         // rows per load instruction (row slots)
@@ -284,6 +284,7 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(
   __shared__ float ps[NW][HPW][64];
   __shared__ float wm[NW][HPW], wl[NW][HPW];
   __shared__ __align__(16) float wo[NW][HPW][RPI][HD];
+  __shared__ float hinv[GRP + 1];
   const int split = blockIdx.x, g = blockIdx.y, nsplit = gridDim.x;
   const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int hs = w % HS, kg = w / HS;
@@ -328,18 +329,42 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(
     return r < nctx ? raw : u32x4{0u, 0u, 0u, 0u};
   };
 
-  // prologue: rotate the group's query heads and the new k; round k, v
+  // prologue: per-head RMSNorm of q and the new k when norm weights are
+  // given (k_rmsnorm2_w: one wave per head, the row's two 64-element halves
+  // summed as block_sum256 sums them in q8_rmsnorm, so the normalised values
+  // are the same bits), then RoPE of the group's query heads and the new k;
+  // round k, v
+  if (qnw) {
+    for (int r = w; r < GRP + 1; r += NW) {
+      const float *src = r < GRP ? q + (g * GRP + r) * HD : k + g * HD;
+      const float a0 = src[lane];
+      float ss = wave_sum(a0 * a0);
+      if constexpr (HD == 128) {
+        const float a1 = src[64 + lane];
+        ss = ss + wave_sum(a1 * a1);
+      }
+      if (lane == 0) hinv[r] = 1.0f / sqrtf(ss / (float)HD + eps);
+    }
+    __syncthreads();
+  }
+  auto qval = [&](int hh, int d) -> float {
+    const float x = q[(g * GRP + hh) * HD + d];
+    return qnw ? bf16_bits_to_f32(qnw[d]) * x * hinv[hh] : x;
+  };
+  auto kval = [&](int d) -> float {
+    const float x = k[g * HD + d];
+    return knw ? bf16_bits_to_f32(knw[d]) * x * hinv[GRP] : x;
+  };
   for (int t = threadIdx.x; t < GRP * half; t += 256) {
     const int hh = t / half, d = t % half;
-    const int h = g * GRP + hh;
     float cs, sn;
     rope_cs((float)pos0 * inv[d], cs, sn);
-    rotate(q[h * HD + d], q[h * HD + half + d], cs, sn, qs[hh][d], qs[hh][half + d]);
+    rotate(qval(hh, d), qval(hh, half + d), cs, sn, qs[hh][d], qs[hh][half + d]);
   }
   for (int d = threadIdx.x; d < half; d += 256) {
     float cs, sn, r0, r1;
     rope_cs((float)pos0 * inv[d], cs, sn);
-    rotate(k[g * HD + d], k[g * HD + half + d], cs, sn, r0, r1);
+    rotate(kval(d), kval(half + d), cs, sn, r0, r1);
     const __half y0 = __float2half_rn(r0), y1 = __float2half_rn(r1);
     kn[d] = y0;
     kn[half + d] = y1;
@@ -677,7 +702,7 @@ template <int HD, int GRP>
 hipError_t launch_decode_attn_t(const DecodeAttnArgs &a, hipStream_t st) {
   hipLaunchKernelGGL((attn_decode_kernel<HD, GRP>), dim3((unsigned)a.nsplit, (unsigned)a.nkv),
                      dim3(256), 0, st, a.q, a.k, a.v, a.inv, a.kc, a.vc, a.part, a.out, a.nkv,
-                     a.posp, a.pos0, a.maxlen);
+                     a.posp, a.pos0, a.maxlen, a.qnorm, a.knorm, a.eps);
   hipLaunchKernelGGL((attn_merge_kernel<HD, GRP>), dim3((unsigned)a.nheads), dim3(256), 0, st,
                      a.part, a.out, a.nsplit, a.posp, a.pos0, a.maxlen);
   return hipGetLastError();

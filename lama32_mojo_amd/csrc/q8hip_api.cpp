@@ -787,8 +787,13 @@ int q8_attention(q8_ctx *ctx, q8_buf *a, uint64_t oq_f32, q8_buf *kv, uint64_t o
 int q8_decode_attention(q8_ctx *ctx, q8_buf *a, uint64_t oq_f32, uint64_t ok_f32,
                         uint64_t ov_f32, uint64_t oinv_f32, q8_buf *kv, uint64_t okc_f16,
                         uint64_t ovc_f16, int64_t maxlen, uint64_t oy_f32, int64_t pos0,
-                        q8_buf *posbuf, uint64_t opos_i32, int nheads, int nkv, int head_dim) {
+                        q8_buf *posbuf, uint64_t opos_i32, int nheads, int nkv, int head_dim,
+                        q8_buf *wn, uint64_t oqnorm_u16, uint64_t oknorm_u16, float eps) {
   if (int rc = check_ctx(ctx)) return rc;
+  if (wn && (!fits(oqnorm_u16, (uint64_t)(head_dim > 0 ? head_dim : 0), 2, wn->size) ||
+             !fits(oknorm_u16, (uint64_t)(head_dim > 0 ? head_dim : 0), 2, wn->size)))
+    return fail(ctx, Q8_ERR_RANGE, "q8_decode_attention: q/k norm weights exceed the weight "
+                "buffer");
   if (!a || !kv) return fail(ctx, Q8_ERR_ARG, "q8_decode_attention: null buffer");
   if (int rc = check_heads(ctx, nheads, nkv, head_dim, "q8_decode_attention")) return rc;
   const int grp = nheads / nkv;
@@ -833,6 +838,11 @@ int q8_decode_attention(q8_ctx *ctx, q8_buf *a, uint64_t oq_f32, uint64_t ok_f32
   da.vc = kvp + ovc_f16;
   da.out = fptr(a, oy_f32);
   da.part = ctx->gemm_ws;
+  if (wn) {
+    da.qnorm = reinterpret_cast<const uint16_t *>(bytes(wn, oqnorm_u16 * 2));
+    da.knorm = reinterpret_cast<const uint16_t *>(bytes(wn, oknorm_u16 * 2));
+    da.eps = eps;
+  }
   da.nheads = nheads;
   da.nkv = nkv;
   da.head_dim = head_dim;

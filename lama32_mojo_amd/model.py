@@ -3,9 +3,11 @@
 Host side of the reference's Q8 model: configuration, weight-arena layout,
 the layer runner and the token loop, driving only libq8hip.so entry points:
 
-  Config, make_config             src/llama_common.mojo:27-52, src/llama_gpu.mojo:29-31
+  Config, make_config             src/llama_common.mojo:27-52, src/llama_gpu.mojo:29-31,
+                                  qwen3_mojo/src/qwen_q8.mojo:30-32
+  rope_inv_freq                   src/llama_common.mojo:609-615 (plain, Qwen3)
   llama3_inv_freq                 src/llama_common.mojo:618-633
-  weight_names                    src/llama_gpu.mojo:33-47
+  weight_names                    src/llama_gpu.mojo:33-47, qwen3_mojo/src/qwen_q8.mojo:35-52
   LayerOffs                       src/llama_common.mojo:55-67
   Q8Llama.layer (run_layer_q8)    src/llama_q8.mojo:144-230
   Q8Llama.forward / forward_argmax  qwen3_mojo/src/qwen_q8.mojo:127-162
@@ -51,6 +53,8 @@ class Config:
     orig_ctx: float
     tied: bool = True          # lm_head = packed embed_tokens (Llama-3.2 / Qwen3 Q8 path)
     name: str = "llama"
+    qk_norm: bool = False      # per-head RMSNorm of q and k before RoPE (Qwen3)
+    rope: str = "llama3"       # "llama3" (wavelength scaling) or "plain" (Qwen3)
 
     def group(self) -> int:
         return self.n_heads // self.n_kv
@@ -71,6 +75,22 @@ LLAMA_32_1B = Config(2048, 16, 32, 8, 64, 8192, 128256, 1e-5, 500000.0, 32.0, 1.
 # Llama-3.1-8B (llama31_mojo/src/llama_gpu.mojo:26-41: untied lm_head)
 LLAMA_31_8B = Config(4096, 32, 32, 8, 128, 14336, 128256, 1e-5, 500000.0, 8.0, 1.0, 4.0, 8192.0,
                      tied=False, name="Llama-3.1-8B")
+# Qwen3-0.6B, the reference's Q8 model (qwen3_mojo/src/qwen_q8.mojo:24-32)
+QWEN3_06B = Config(1024, 28, 16, 8, 128, 3072, 151936, 1e-6, 1000000.0, 1.0, 1.0, 4.0, 8192.0,
+                   tied=True, name="Qwen3-0.6B", qk_norm=True, rope="plain")
+# Qwen3-8B (untied lm_head 4096 -> 151936)
+QWEN3_8B = Config(4096, 36, 32, 8, 128, 12288, 151936, 1e-6, 1000000.0, 1.0, 1.0, 4.0, 8192.0,
+                  tied=False, name="Qwen3-8B", qk_norm=True, rope="plain")
+
+
+def rope_inv_freq(cfg: Config) -> np.ndarray:
+    """RoPE inverse frequencies of the configuration: plain 1 / theta^(2d/hd)
+    (rope_inv_freq) or with llama3 wavelength scaling (llama3_inv_freq),
+    evaluated in float64 and stored as f32."""
+    if cfg.rope == "plain":
+        return np.array([1.0 / (cfg.theta ** (2.0 * d / cfg.head_dim)) for d in range(cfg.half())],
+                        dtype=np.float32)
+    return llama3_inv_freq(cfg)
 
 
 def llama3_inv_freq(cfg: Config) -> np.ndarray:
@@ -97,8 +117,10 @@ def weight_names(cfg: Config) -> list[str]:
     names = ["model.embed_tokens.weight", "model.norm.weight"]
     for L in range(cfg.layers):
         p = f"model.layers.{L}."
-        names += [p + "input_layernorm.weight", p + "post_attention_layernorm.weight",
-                  p + "self_attn.q_proj.weight", p + "self_attn.k_proj.weight",
+        names += [p + "input_layernorm.weight", p + "post_attention_layernorm.weight"]
+        if cfg.qk_norm:
+            names += [p + "self_attn.q_norm.weight", p + "self_attn.k_norm.weight"]
+        names += [p + "self_attn.q_proj.weight", p + "self_attn.k_proj.weight",
                   p + "self_attn.v_proj.weight", p + "self_attn.o_proj.weight",
                   p + "mlp.gate_proj.weight", p + "mlp.up_proj.weight",
                   p + "mlp.down_proj.weight"]
@@ -119,6 +141,9 @@ def tensor_shapes(cfg: Config) -> dict[str, tuple]:
             p + "self_attn.v_proj.weight": (KVD, H), p + "self_attn.o_proj.weight": (H, QD),
             p + "mlp.gate_proj.weight": (I, H), p + "mlp.up_proj.weight": (I, H),
             p + "mlp.down_proj.weight": (H, I)})
+        if cfg.qk_norm:
+            shapes[p + "self_attn.q_norm.weight"] = (cfg.head_dim,)
+            shapes[p + "self_attn.k_norm.weight"] = (cfg.head_dim,)
     if not cfg.tied:
         shapes["lm_head.weight"] = (cfg.vocab, H)
     return shapes
@@ -144,6 +169,8 @@ class LayerOffs:
     down: int
     in_norm: int
     post_norm: int
+    q_norm: int = -1           # per-head q / k RMSNorm weights (Qwen3), -1 if none
+    k_norm: int = -1
 
 
 class Q8Llama:
@@ -176,11 +203,13 @@ class Q8Llama:
         for L in range(cfg.layers):
             p = f"model.layers.{L}."
             o = self.w.o
+            qn = (o(p + "self_attn.q_norm.weight"), o(p + "self_attn.k_norm.weight")) \
+                if cfg.qk_norm else (-1, -1)
             self.lo.append(LayerOffs(o(p + "self_attn.q_proj.weight"), o(p + "self_attn.k_proj.weight"),
                                      o(p + "self_attn.v_proj.weight"), o(p + "self_attn.o_proj.weight"),
                                      o(p + "mlp.gate_proj.weight"), o(p + "mlp.up_proj.weight"),
                                      o(p + "mlp.down_proj.weight"), o(p + "input_layernorm.weight"),
-                                     o(p + "post_attention_layernorm.weight")))
+                                     o(p + "post_attention_layernorm.weight"), *qn))
         H, QD, KVD, I = cfg.hidden, cfg.q_dim(), cfg.kv_dim(), cfg.inter
         if act_floats is None:
             # two residual rows sets, one layer's temporaries (the arena is
@@ -189,15 +218,15 @@ class Q8Llama:
             s = max(1, int(max_prefill))
             att = q8hip.attention_scratch_floats(min(s, self.ATT_ROWS), cfg.n_heads, cfg.head_dim,
                                                  self.maxlen)
-            layer = s * (4 * H + 2 * QD + 2 * KVD + 2 * I) + att
+            layer = s * (4 * H + 3 * QD + 3 * KVD + 2 * I) + att    # incl. q/k norm outputs
             one = 2 * s * H + layer + H + cfg.vocab + 64
-            act_floats = PAD + cfg.half() + one + (2 * H + (4 * H + 2 * QD + 2 * KVD + 2 * I)
+            act_floats = PAD + cfg.half() + one + (2 * H + (4 * H + 3 * QD + 3 * KVD + 2 * I)
                                                    + q8hip.attention_scratch_floats(
                                                        1, cfg.n_heads, cfg.head_dim, self.maxlen)
                                                    + H + cfg.vocab + 64)
         self.a = Acts(ctx, act_floats)
         self.oinv = self.a.alloc(cfg.half())
-        self.a.write(self.oinv, llama3_inv_freq(cfg))
+        self.a.write(self.oinv, rope_inv_freq(cfg))
         kvd = cfg.kv_dim()
         self.kv = Buffer.alloc(ctx, 2 * cfg.layers * 2 * self.maxlen * kvd)
         self.okc = [(2 * L) * self.maxlen * kvd for L in range(cfg.layers)]
@@ -294,8 +323,16 @@ class Q8Llama:
             oq = self.linear(xn, s, H, lo.q, QD)
             okk = self.linear(xn, s, H, lo.k, KVD)
             ov = self.linear(xn, s, H, lo.v, KVD)
+        if cfg.qk_norm:                                   # k_rmsnorm2_w
+            oqn, okn = a.alloc(s * QD), a.alloc(s * KVD)
+            q8hip.rmsnorm(ctx, w.buf, lo.q_norm, a.buf, oq, oqn, s * cfg.n_heads, cfg.head_dim,
+                          cfg.eps)
+            q8hip.rmsnorm(ctx, w.buf, lo.k_norm, a.buf, okk, okn, s * cfg.n_kv, cfg.head_dim,
+                          cfg.eps)
+            oq, okk = oqn, okn
         oao = a.alloc(s * QD)
         if s == 1:
+            # (q and k are already normalised here when the model has q/k norms)
             q8hip.decode_attention(ctx, a.buf, oq, okk, ov, self.oinv, self.kv, self.okc[L],
                                    self.ovc[L], self.maxlen, oao, pos0, cfg.n_heads, cfg.n_kv,
                                    cfg.head_dim, pb, 0)
@@ -327,9 +364,9 @@ class Q8Llama:
         return oh
 
     def _layer_fused(self, L: int, ox: int, pos0: int, pb, oh: int | None) -> int:
-        """One-row block in five launches: norm + q|k|v, attention (split +
-        merge), o + residual, norm + gate|up + swiglu, down + residual (in
-        place)."""
+        """One-row block in six launches: norm + q|k|v, attention (q/k head
+        norms, RoPE, KV append, context splits) and its merge, o + residual,
+        norm + gate|up + swiglu, down + residual (in place)."""
         cfg, ctx, a, w = self.cfg, self.ctx, self.a, self.w
         lo = self.lo[L]
         H, QD, KVD, I = cfg.hidden, cfg.q_dim(), cfg.kv_dim(), cfg.inter
@@ -338,9 +375,11 @@ class Q8Llama:
         q8hip.linear_fused(ctx, w.buf, lo.q, a.buf, ox, oq, H, QD + 2 * KVD, G, sc,
                            pre=q8hip.PRE_RMSNORM, onorm_u16=lo.in_norm, eps=cfg.eps)
         oao = a.alloc(QD)
+        qk = dict(wn=w.buf, oqnorm_u16=lo.q_norm, oknorm_u16=lo.k_norm, eps=cfg.eps) \
+            if cfg.qk_norm else {}
         q8hip.decode_attention(ctx, a.buf, oq, oq + QD, oq + QD + KVD, self.oinv, self.kv,
                                self.okc[L], self.ovc[L], self.maxlen, oao, pos0, cfg.n_heads,
-                               cfg.n_kv, cfg.head_dim, pb, 0)
+                               cfg.n_kv, cfg.head_dim, pb, 0, **qk)
         if oh is None:
             oh = a.alloc(H)
         q8hip.linear_fused(ctx, w.buf, lo.o, a.buf, oao, oh, QD, H, G, sc,

@@ -100,7 +100,7 @@ SIGNATURES = {
     "q8_attention": (_I, [_P, _P, _U64, _P, _U64, _U64, _I64, _U64, _U64, _I64, _I64, _P, _U64,
                          _I, _I, _I]),
     "q8_decode_attention": (_I, [_P, _P, _U64, _U64, _U64, _U64, _P, _U64, _U64, _I64, _U64,
-                                _I64, _P, _U64, _I, _I, _I]),
+                                _I64, _P, _U64, _I, _I, _I, _P, _U64, _U64, ctypes.c_float]),
     "q8_swiglu": (_I, [_P, _P, _U64, _U64, _I64]),
     "q8_res_add": (_I, [_P, _P, _U64, _U64, _U64, _I64]),
     "q8_add": (_I, [_P, _P, _U64, _U64, _I64]),
@@ -360,11 +360,15 @@ def attention(ctx: Context, a: Buffer, oq: int, kv: Buffer, okc_f16: int, ovc_f1
 def decode_attention(ctx: Context, a: Buffer, oq: int, ok: int, ov: int, oinv: int, kv: Buffer,
                      okc_f16: int, ovc_f16: int, maxlen: int, oy: int, pos0: int, nheads: int,
                      nkv: int, head_dim: int, posbuf: Buffer | None = None,
-                     opos_i32: int = 0) -> None:
+                     opos_i32: int = 0, wn: Buffer | None = None, oqnorm_u16: int = 0,
+                     oknorm_u16: int = 0, eps: float = 0.0) -> None:
+    """One-token attention step; with wn, per-head RMSNorm of q and k first
+    (the q_norm / k_norm weights at oqnorm_u16 / oknorm_u16 of wn)."""
     ctx.check(ctx._lib.q8_decode_attention(ctx.h, a.h, int(oq), int(ok), int(ov), int(oinv), kv.h,
                                            int(okc_f16), int(ovc_f16), int(maxlen), int(oy),
                                            int(pos0), _h(posbuf), int(opos_i32), int(nheads),
-                                           int(nkv), int(head_dim)))
+                                           int(nkv), int(head_dim), _h(wn), int(oqnorm_u16),
+                                           int(oknorm_u16), float(eps)))
 
 
 def swiglu(ctx: Context, a: Buffer, og: int, ou: int, n: int) -> None:

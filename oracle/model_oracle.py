@@ -10,6 +10,8 @@ float64 numpy restatements of the reference's layer kernels and layer runner
 GPU reads:
 
   rmsnorm          k_rmsnorm_w              src/llama_common.mojo:197-225
+  head_rmsnorm     k_rmsnorm2_w             src/llama_common.mojo:228-270
+  rope_inv_freq    rope_inv_freq            src/llama_common.mojo:609-615
   llama3_inv_freq  llama3_inv_freq          src/llama_common.mojo:618-633
   rope             k_rope_qk_copy2          src/llama_common.mojo:299-342
   attention        k_scores, k_softmax_rows, k_att_out
@@ -38,6 +40,22 @@ def rmsnorm(x: np.ndarray, w_bits: np.ndarray, eps: float) -> np.ndarray:
     w = bf16_bits_to_f32(w_bits).astype(np.float64)
     inv = 1.0 / np.sqrt(np.mean(x * x, axis=-1, keepdims=True) + float(np.float32(eps)))
     return w * x * inv
+
+
+def head_rmsnorm(x: np.ndarray, w_bits: np.ndarray, nheads: int, head_dim: int,
+                 eps: float) -> np.ndarray:
+    """Per-head RMSNorm of rows [s, nheads * head_dim] with one head_dim
+    weight vector (k_rmsnorm2_w: every head row normalised on its own)."""
+    s = x.shape[0]
+    y = rmsnorm(np.asarray(x, dtype=np.float64).reshape(s * nheads, head_dim), w_bits, eps)
+    return y.reshape(s, nheads * head_dim)
+
+
+def rope_inv_freq(head_dim: int, theta: float) -> np.ndarray:
+    """Plain RoPE inverse frequencies 1 / theta^(2d / head_dim), float64
+    rounded to f32 (rope_inv_freq)."""
+    return np.array([1.0 / (theta ** (2.0 * d / head_dim)) for d in range(head_dim // 2)],
+                    dtype=np.float32)
 
 
 def llama3_inv_freq(head_dim: int, theta: float, factor: float, low_ff: float, high_ff: float,
@@ -119,6 +137,7 @@ class ModelSpec:
     G: int = 64
     scale: str = "f16"
     tied: bool = True
+    qk_norm: bool = False    # per-head q / k RMSNorm before RoPE (Qwen3)
 
 
 @dataclass
@@ -144,7 +163,8 @@ class OracleModel:
         return linear_f64_np(self.tensors[name], x, x.shape[1], sp.G, sp.scale)
 
     def layer(self, L: int, x: np.ndarray) -> np.ndarray:
-        """One pre-norm GQA block with KV append (run_layer_q8)."""
+        """One pre-norm GQA block with KV append (run_layer_q8,
+        src/llama_q8.mojo:144-230, including the q/k head norms of :171-182)."""
         sp = self.spec
         p = f"model.layers.{L}."
         s = x.shape[0]
@@ -152,6 +172,11 @@ class OracleModel:
         q = self.lin(p + "self_attn.q_proj.weight", xn)
         k = self.lin(p + "self_attn.k_proj.weight", xn)
         v = self.lin(p + "self_attn.v_proj.weight", xn)
+        if sp.qk_norm:
+            q = head_rmsnorm(q, self.tensors[p + "self_attn.q_norm.weight"], sp.n_heads,
+                             sp.head_dim, sp.eps)
+            k = head_rmsnorm(k, self.tensors[p + "self_attn.k_norm.weight"], sp.n_kv,
+                             sp.head_dim, sp.eps)
         q = rope(q, self.pos, self.inv, sp.n_heads, sp.head_dim)
         k = rope(k, self.pos, self.inv, sp.n_kv, sp.head_dim)
         self.kc[L][self.pos:self.pos + s] = f16_round(k)

@@ -25,7 +25,7 @@ from oracle import model_oracle as mo
 from oracle.q8_oracle import f32_to_bf16_bits, max_rel_err
 
 sys.path.insert(0, __file__.rsplit("/", 1)[0])
-from test_model_oracle import tiny_model  # noqa: E402
+from test_model_oracle import qwen_tiny, tiny_model  # noqa: E402
 
 pytestmark = pytest.mark.gpu
 
@@ -151,10 +151,10 @@ def test_attention(ctx, head_dim, nh, nkv, s, pos0):
 def test_decode_attention_equals_rope_then_attention(ctx, head_dim, nh, nkv, pos0):
     """The one-launch token step writes the same cache bits as q8_rope_kv and
     matches q8_rope_kv + q8_attention within 2e-6 (it sums the splits in
-    another order).  maxlen 1536 gives 6 context splits: pos0 <= 255 is
-    served by one block, larger pos0 by 2 .. 6 blocks merged by the last to
-    arrive; a second call must reproduce the first (its counters are back at
-    zero)."""
+    another order).  maxlen 1536 gives 24 (head_dim 64) or 32 (head_dim 128)
+    context splits of one chunk each: pos0 < 64 (32) is served by one block
+    per KV head, larger pos0 by up to 24 blocks whose records the merge
+    launch combines; a second call must reproduce the first."""
     say("decode attention", head_dim, nh, nkv, pos0)
     rng = np.random.default_rng(4)
     maxlen = 1536
@@ -243,8 +243,14 @@ def test_elementwise_and_argmax(ctx):
 
 
 def gpu_model(ctx, spec, tensors, maxlen, max_prefill=8, fuse=True):
-    cfg = gm.Config(spec.hidden, spec.layers, spec.n_heads, spec.n_kv, spec.head_dim, spec.inter,
-                    spec.vocab, spec.eps, 500000.0, 32.0, 1.0, 4.0, 8192.0, tied=True, name="tiny")
+    if spec.qk_norm:        # Qwen3-style: plain RoPE, theta 1e6 (as qwen_tiny's oracle)
+        cfg = gm.Config(spec.hidden, spec.layers, spec.n_heads, spec.n_kv, spec.head_dim,
+                        spec.inter, spec.vocab, spec.eps, 1000000.0, 1.0, 1.0, 4.0, 8192.0,
+                        tied=True, name="tiny-qwen", qk_norm=True, rope="plain")
+    else:
+        cfg = gm.Config(spec.hidden, spec.layers, spec.n_heads, spec.n_kv, spec.head_dim,
+                        spec.inter, spec.vocab, spec.eps, 500000.0, 32.0, 1.0, 4.0, 8192.0,
+                        tied=True, name="tiny")
     return gm.Q8Llama(ctx, cfg, maxlen, spec.G, spec.scale, weights=tensors,
                       max_prefill=max_prefill, fuse=fuse)
 
@@ -403,3 +409,88 @@ def test_graph_replay_equals_eager(ctx):
         a.close()
         b.close()
 
+
+
+@pytest.mark.parametrize("head_dim,nh,nkv", [(128, 16, 8), (64, 8, 2)])
+@pytest.mark.parametrize("pos0", [0, 100, 700])
+def test_decode_attention_qk_norm_equals_rmsnorm_rope_attention(ctx, head_dim, nh, nkv, pos0):
+    """With q/k norm weights the one-token step writes the cache bits of
+    q8_rmsnorm over the head rows + q8_rope_kv, and its output is within
+    2e-6 of q8_rmsnorm + q8_rope_kv + q8_attention (1e-5 of float64)."""
+    say("decode attention qk-norm", head_dim, nh, nkv, pos0)
+    rng = np.random.default_rng(8)
+    maxlen, eps = 1024, 1e-6
+    qd, kvd = nh * head_dim, nkv * head_dim
+    inv = mo.rope_inv_freq(head_dim, 1000000.0)
+    cache = rng.standard_normal((2, maxlen, kvd)).astype(np.float16)
+    q = (3 * rng.standard_normal(qd)).astype(np.float32)
+    k = (3 * rng.standard_normal(kvd)).astype(np.float32)
+    v = rng.standard_normal(kvd).astype(np.float32)
+    qnw = f32_to_bf16_bits((1 + 0.2 * rng.standard_normal(head_dim)).astype(np.float32))
+    knw = f32_to_bf16_bits((1 + 0.2 * rng.standard_normal(head_dim)).astype(np.float32))
+    w = ctx.alloc(2 * (64 + 2 * head_dim))
+    w.upload(qnw, 2 * 64)
+    w.upload(knw, 2 * (64 + head_dim))
+    oq, ok, ov, oinv, oy = 0, qd, qd + kvd, qd + 2 * kvd, qd + 2 * kvd + head_dim
+    oqn, okn = oy + qd, oy + 2 * qd
+    osc = okn + kvd
+    a = arena(ctx, osc + q8hip.attention_scratch_floats(1, nh, head_dim, maxlen))
+    kv1, kv2 = ctx.alloc(cache.nbytes), ctx.alloc(cache.nbytes)
+    kv1.upload(cache)
+    kv2.upload(cache)
+    for buf, x in [(oq, q), (ok, k), (ov, v), (oinv, inv)]:
+        put(a, buf, x)
+    q8hip.decode_attention(ctx, a, oq, ok, ov, oinv, kv1, 0, maxlen * kvd, maxlen, oy, pos0, nh,
+                           nkv, head_dim, wn=w, oqnorm_u16=64, oknorm_u16=64 + head_dim, eps=eps)
+    fused = get(a, oy, (qd,))
+    q8hip.rmsnorm(ctx, w, 64, a, oq, oqn, nh, head_dim, eps)
+    q8hip.rmsnorm(ctx, w, 64 + head_dim, a, ok, okn, nkv, head_dim, eps)
+    qn = get(a, oqn, (1, qd))
+    q8hip.rope_kv(ctx, a, oqn, okn, ov, oinv, kv2, 0, maxlen * kvd, maxlen, 1, pos0, nh, nkv,
+                  head_dim)
+    q8hip.attention(ctx, a, oqn, kv2, 0, maxlen * kvd, maxlen, oy, osc, 1, pos0, nh, nkv,
+                    head_dim)
+    sep = get(a, oy, (qd,))
+    c1 = kv1.download((2, maxlen, kvd), np.float16)
+    assert np.array_equal(c1, kv2.download((2, maxlen, kvd), np.float16))
+    assert np.all(np.isfinite(fused)) and max_rel_err(fused, sep) <= 2e-6
+    qr = mo.rope(mo.head_rmsnorm(q[None].astype(np.float64), qnw, nh, head_dim, eps), pos0, inv,
+                 nh, head_dim)
+    ref = mo.attention(qr, c1[0].astype(np.float64), c1[1].astype(np.float64), pos0, nh, nkv,
+                       head_dim)
+    assert max_rel_err(fused, ref[0]) <= 1e-5
+    assert max_rel_err(qn[0], mo.head_rmsnorm(q[None].astype(np.float64), qnw, nh, head_dim,
+                                               eps)[0]) <= 1e-6
+    for b in (a, w, kv1, kv2):
+        b.free()
+
+
+def test_qwen_style_model_forward_and_greedy_decode(ctx):
+    """Qwen3-style tiny model (q/k head norms, plain RoPE, head_dim 128):
+    logits within 1e-3 of the float64 model, the same greedy ids through
+    eager steps and graph replays, fused layers within 1e-5 of unfused."""
+    say("qwen-style model")
+    spec, t, inv = qwen_tiny(seed=6)
+    maxlen = 32
+    prompt = [7, 1, 8, 2, 8]
+    ref = mo.OracleModel(spec, t, inv, maxlen)
+    m = gpu_model(ctx, spec, t, maxlen)
+    u = gpu_model(ctx, spec, t, maxlen, fuse=False)
+    try:
+        lg, lr = m.forward(prompt), ref.forward(prompt)
+        assert max_rel_err(lg, lr) <= 1e-3, max_rel_err(lg, lr)
+        assert max_rel_err(u.forward(prompt), lg) <= 1e-5
+        nxt = int(np.argmax(lg))
+        assert nxt == int(np.argmax(lr))
+        ids_ref, cur = [], nxt
+        for _ in range(6):
+            cur = int(np.argmax(ref.forward([cur])))
+            ids_ref.append(cur)
+        got = [m.forward_argmax([nxt])]
+        lu = u.forward([nxt])
+        got += m.decode_steps(got[-1], 5)
+        assert got == ids_ref, (got, ids_ref)
+        assert int(np.argmax(lu)) == ids_ref[0]
+    finally:
+        m.close()
+        u.close()

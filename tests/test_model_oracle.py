@@ -108,10 +108,12 @@ def packed(n, m, seed, std, G, scale):
 
 
 def tiny_model(maxlen=16, G=64, scale="f16", layers=2, seed=0, hidden=512, n_heads=8, n_kv=2,
-               head_dim=64, inter=1024, vocab=97):
-    """A small Llama-style model (packed rows 16-byte aligned, head_dim 64)."""
+               head_dim=64, inter=1024, vocab=97, qk_norm=False):
+    """A small Llama-style model (packed rows 16-byte aligned, head_dim 64);
+    with qk_norm a Qwen3-style one (per-head q/k norms, plain RoPE)."""
     spec = mo.ModelSpec(hidden=hidden, layers=layers, n_heads=n_heads, n_kv=n_kv,
-                        head_dim=head_dim, inter=inter, vocab=vocab, eps=1e-5, G=G, scale=scale)
+                        head_dim=head_dim, inter=inter, vocab=vocab,
+                        eps=1e-6 if qk_norm else 1e-5, G=G, scale=scale, qk_norm=qk_norm)
     rng = np.random.default_rng(seed)
     H, QD, KVD, I = spec.hidden, spec.n_heads * spec.head_dim, spec.n_kv * spec.head_dim, spec.inter
     t = {"model.embed_tokens.weight": packed(spec.vocab, H, seed + 1, 0.5, G, scale),
@@ -127,8 +129,18 @@ def tiny_model(maxlen=16, G=64, scale="f16", layers=2, seed=0, hidden=512, n_hea
             t[p + name] = packed(n, m, seed + k, 1.5 / np.sqrt(m), G, scale)
         for name in ["input_layernorm.weight", "post_attention_layernorm.weight"]:
             t[p + name] = f32_to_bf16_bits((1 + 0.1 * rng.standard_normal(H)).astype(np.float32))
-    inv = mo.llama3_inv_freq(spec.head_dim, 500000.0, 32.0, 1.0, 4.0, 8192.0)
+        if qk_norm:
+            for name in ["self_attn.q_norm.weight", "self_attn.k_norm.weight"]:
+                t[p + name] = f32_to_bf16_bits(
+                    (1 + 0.1 * rng.standard_normal(head_dim)).astype(np.float32))
+    inv = (mo.rope_inv_freq(spec.head_dim, 1000000.0) if qk_norm else
+           mo.llama3_inv_freq(spec.head_dim, 500000.0, 32.0, 1.0, 4.0, 8192.0))
     return spec, t, inv
+
+
+def qwen_tiny(**kw):
+    """A small Qwen3-style model: head_dim 128, GQA 2, q/k head norms."""
+    return tiny_model(hidden=512, n_heads=4, n_kv=2, head_dim=128, qk_norm=True, **kw)
 
 
 def test_prefill_equals_token_by_token():
@@ -144,3 +156,63 @@ def test_prefill_equals_token_by_token():
     assert np.all(np.isfinite(la)) and np.std(la) > 0.1
     np.testing.assert_allclose(la, lb, rtol=1e-9, atol=1e-12, equal_nan=False)
     assert a.pos == b.pos == len(ids)
+
+
+def test_head_rmsnorm_is_rowwise_and_heads_are_independent():
+    rng = np.random.default_rng(3)
+    nh, hd, eps = 3, 8, 1e-6
+    x = rng.standard_normal((2, nh * hd))
+    w = f32_to_bf16_bits((1 + 0.1 * rng.standard_normal(hd)).astype(np.float32))
+    y = mo.head_rmsnorm(x, w, nh, hd, eps)
+    for i in range(2):
+        for h in range(nh):
+            np.testing.assert_allclose(y[i, h * hd:(h + 1) * hd],
+                                       mo.rmsnorm(x[i:i + 1, h * hd:(h + 1) * hd], w, eps)[0],
+                                       rtol=1e-12)
+    x2 = x.copy()
+    x2[:, hd:2 * hd] *= 7.0                 # scale head 1 only
+    y2 = mo.head_rmsnorm(x2, w, nh, hd, 0.0)
+    y0 = mo.head_rmsnorm(x, w, nh, hd, 0.0)
+    np.testing.assert_allclose(y2, y0, rtol=1e-12)
+
+
+def test_rope_inv_freq_geometric():
+    """Plain RoPE frequencies: 1 at d = 0, a constant ratio theta^(-2/hd)
+    between neighbours (to f32 rounding), theta^(-(hd-2)/hd) at the end."""
+    hd, theta = 128, 1000000.0
+    inv = mo.rope_inv_freq(hd, theta).astype(np.float64)
+    assert inv[0] == 1.0
+    np.testing.assert_allclose(inv[1:] / inv[:-1], np.exp(-2.0 * np.log(theta) / hd), rtol=3e-7)
+    np.testing.assert_allclose(inv[-1], np.exp(-(hd - 2) / hd * np.log(theta)), rtol=1e-7)
+
+
+def test_qk_norm_removes_the_scale_of_q_and_k_projections():
+    """With per-head q/k norms (eps = 0, which makes them scale-free),
+    W_q -> 4 W_q and W_k -> 4 W_k (powers of two: only the f16 group scales
+    change, exactly) leave the logits unchanged; without the norms they
+    change them."""
+    spec, t, inv = qwen_tiny(seed=4)
+    spec = mo.ModelSpec(**{**spec.__dict__, "eps": 0.0})
+    rs_h = t["model.layers.0.self_attn.q_proj.weight"].shape[1]
+    groups = spec.hidden // spec.G
+
+    def scaled(tensors):
+        out = dict(tensors)
+        for L in range(spec.layers):
+            for name in ["self_attn.q_proj.weight", "self_attn.k_proj.weight"]:
+                key = f"model.layers.{L}.{name}"
+                w = out[key].copy()
+                sc = w[:, :groups].view(np.float16).astype(np.float32) * 4.0
+                w[:, :groups] = sc.astype(np.float16).view(np.uint16)
+                out[key] = w
+        return out
+
+    assert rs_h == groups + spec.hidden // 2
+    ids = [3, 1, 4, 1, 5]
+    base = mo.OracleModel(spec, t, inv, 16).forward(ids)
+    big = mo.OracleModel(spec, scaled(t), inv, 16).forward(ids)
+    np.testing.assert_allclose(big, base, rtol=1e-9, atol=1e-9)
+    plain = mo.ModelSpec(**{**spec.__dict__, "qk_norm": False})
+    a = mo.OracleModel(plain, t, inv, 16).forward(ids)
+    b = mo.OracleModel(plain, scaled(t), inv, 16).forward(ids)
+    assert np.max(np.abs(a - b)) > 1e-3
