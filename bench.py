@@ -323,9 +323,7 @@ def run_decode_model(B: Bench, ctxlen: int = 1024, cfg=None, tok_metric: bool = 
     src.free()
     del kvt
     m.n_cached = ctxlen
-    m.capture_decode()
-    m.ids.upload(np.array([128000 % cfg.vocab], dtype=np.int32))
-    m.posbuf.upload(np.array([ctxlen], dtype=np.int32))
+    m.prime_decode(128000 % cfg.vocab)
     ms, wall = B.time_steps(lambda: m.graph.launch(), K, W)
     pos_end = int(m.posbuf.download((1,), np.int32)[0])
     assert pos_end == ctxlen + W + K, pos_end

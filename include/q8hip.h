@@ -177,6 +177,24 @@ int q8_linear_fused(q8_ctx *ctx, q8_buf *w, uint64_t owt_u16, q8_buf *a,
                     int scale_dtype, int pre, uint64_t onorm_u16, float eps,
                     int post, uint64_t ores_f32);
 
+/* The end of a token step in two launches: logits y (n floats at oy) = W
+ * rmsnorm(x) over the lm_head's n packed rows (norm weights at onorm of w;
+ * as q8_linear_fused with Q8_PRE_RMSNORM), their argmax (as q8_argmax: the
+ * lowest index of the largest value, 0 when y[0] is NaN) written to
+ * ids[oid], the position at posbuf[opos] advanced by pos_step (posbuf NULL:
+ * none) and, with gather != 0, the embedding row of that id -- from the n
+ * packed rows of m at oemb of w, as q8_embed_gather -- written to x_next
+ * (m floats at onext of a), ready for the next step.  The argmax partials
+ * live in the context's workspace.  Needs m <= 16384, m % 32 == 0 and the
+ * alignment of q8_linear_fused.
+ * Replaces the final rmsnorm_op + lm_head mm_q8_op + argmax_op + the next
+ * embed of the token loop (qwen3_mojo/src/qwen_q8.mojo:110-162). */
+int q8_head_argmax(q8_ctx *ctx, q8_buf *w, uint64_t owt_u16, uint64_t onorm_u16, float eps,
+                   q8_buf *a, uint64_t ox_f32, uint64_t oy_f32, int64_t m, int64_t n, int G,
+                   int scale_dtype, q8_buf *ids, uint64_t oid_i32, q8_buf *posbuf,
+                   uint64_t opos_i32, int64_t pos_step, int gather, uint64_t oemb_u16,
+                   uint64_t onext_f32);
+
 /* y = bf16(wn) * x / sqrt(mean(x^2) + eps) for `rows` rows of d, wn = d bf16
  * values at owt (k_rmsnorm_w / rmsnorm_op, src/llama_common.mojo:197-225,
  * 690-696). */

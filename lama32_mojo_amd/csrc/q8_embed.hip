@@ -44,7 +44,99 @@ hipError_t launch_g(const GatherArgs &a, hipStream_t st) {
   return hipGetLastError();
 }
 
+// The token step's last launch: the argmax over the GEMV's per-workgroup
+// partials (value desc, row asc; k_argmax's result: index 0 when logits[0]
+// is NaN or no value exceeds it), written to ids[0]; the device position
+// advanced; and, with emb, the embedding row of that id gathered into xnext
+// exactly as embed_gather_kernel gathers it.  One 1024-thread workgroup.
+template <int G, int KIND>
+__global__ __launch_bounds__(1024) void argmax_finish_kernel(
+    const float *__restrict__ part, int nblocks, const float *__restrict__ logits,
+    int32_t *__restrict__ ids, int *pos, int pos_step, const uint8_t *__restrict__ emb,
+    int64_t row_bytes, int64_t vocab, float *__restrict__ xnext, int64_t d) {
+  constexpr int SB = ScaleTraits<KIND>::bytes;
+  __shared__ float bv[16];
+  __shared__ int bi[16];
+  __shared__ int sid;
+  const int *pidx = reinterpret_cast<const int *>(part + nblocks);
+  float best = -INFINITY;
+  int bidx = INT32_MAX;
+  // the partials in batches of 8 independent loads per thread, then the
+  // compares (in index order within the thread)
+  for (int t0 = threadIdx.x; t0 < nblocks; t0 += 8 * 1024) {
+    float v[8];
+    int i[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int t = t0 + 1024 * u;
+      v[u] = t < nblocks ? part[t] : -INFINITY;
+      i[u] = t < nblocks ? pidx[t] : INT32_MAX;
+    }
+#pragma unroll
+    for (int u = 0; u < 8; ++u)
+      if (v[u] > best || (v[u] == best && i[u] < bidx)) {
+        best = v[u];
+        bidx = i[u];
+      }
+  }
+  for (int off = 32; off > 0; off >>= 1) {
+    const float ob = __shfl_xor(best, off, 64);
+    const int oi = __shfl_xor(bidx, off, 64);
+    if (ob > best || (ob == best && oi < bidx)) {
+      best = ob;
+      bidx = oi;
+    }
+  }
+  const int w = threadIdx.x >> 6;
+  if ((threadIdx.x & 63) == 0) {
+    bv[w] = best;
+    bi[w] = bidx;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    float b = bv[0];
+    int id = bi[0];
+    for (int t = 1; t < 16; ++t)
+      if (bv[t] > b || (bv[t] == b && bi[t] < id)) {
+        b = bv[t];
+        id = bi[t];
+      }
+    const float v0 = logits[0];
+    if (id == INT32_MAX || v0 != v0) id = 0;
+    ids[0] = id;
+    if (pos) pos[0] += pos_step;
+    sid = id;
+  }
+  if (!emb) return;
+  __syncthreads();
+  const int64_t id = sid;
+  const uint8_t *row = emb + id * row_bytes;
+  const int8_t *codes = reinterpret_cast<const int8_t *>(row + (d / G) * SB);
+  for (int64_t c = 4 * (int64_t)threadIdx.x; c < d; c += 4 * 1024) {
+    const float sc = load_scale<KIND>(row, c / G);
+#pragma unroll
+    for (int u = 0; u < 4; ++u) xnext[c + u] = (float)codes[c + u] * sc;
+  }
+}
+
+template <int G, int KIND>
+hipError_t launch_finish_g(const ArgmaxFinishArgs &a, hipStream_t st) {
+  hipLaunchKernelGGL((argmax_finish_kernel<G, KIND>), dim3(1), dim3(1024), 0, st, a.part,
+                     a.nblocks, a.logits, a.ids, a.pos, a.pos_step, a.emb, a.row_bytes, a.vocab,
+                     a.xnext, a.d);
+  return hipGetLastError();
+}
+
 }  // namespace
+
+hipError_t launch_argmax_finish(const ArgmaxFinishArgs &a, hipStream_t st) {
+  if (a.nblocks < 1 || a.nblocks > kArgmaxMaxBlocks) return hipErrorInvalidValue;
+  if (!a.emb || (a.G == 64 && a.kind == SCALE_F16)) return launch_finish_g<64, SCALE_F16>(a, st);
+  if (a.G == 64 && a.kind == SCALE_F32) return launch_finish_g<64, SCALE_F32>(a, st);
+  if (a.G == 32 && a.kind == SCALE_F16) return launch_finish_g<32, SCALE_F16>(a, st);
+  if (a.G == 32 && a.kind == SCALE_F32) return launch_finish_g<32, SCALE_F32>(a, st);
+  return hipErrorInvalidValue;
+}
 
 hipError_t launch_embed_gather(const GatherArgs &a, hipStream_t st) {
   if (a.s == 0) return hipSuccess;

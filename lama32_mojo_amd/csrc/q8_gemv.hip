@@ -41,13 +41,15 @@ template <int G, int KIND, int S, int R, int SPLITK, bool XLDS, int PRE = PRE_NO
 __global__ __launch_bounds__(256) void gemv_kernel(
     const uint8_t *__restrict__ w, int64_t row_bytes, int64_t n,
     const float *__restrict__ x, int64_t m, float *y, const uint16_t *__restrict__ wn,
-    float eps, const float *res) {
+    float eps, const float *res, float *__restrict__ amax) {
   extern __shared__ float xs[];
   __shared__ float part[SPLITK > 1 ? SPLITK : 1][R][S];
   __shared__ float red[4];
   static_assert(PRE == PRE_NONE || (XLDS && S == 1), "fused prologues stage one x row in LDS");
   static_assert(POST != POST_SWIGLU || (SPLITK == 1 && R % 2 == 0 && S == 1),
                 "the swiglu epilogue pairs gate and up rows within a wave");
+  static_assert(POST != POST_ARGMAX || (SPLITK == 1 && S == 1),
+                "the argmax epilogue keeps whole rows per wave");
   constexpr int SB = ScaleTraits<KIND>::bytes;
   const int lane = threadIdx.x & 63;
   const int wid = threadIdx.x >> 6;
@@ -174,6 +176,8 @@ __global__ __launch_bounds__(256) void gemv_kernel(
     }
   };
 
+  float best_v = -INFINITY;              // POST_ARGMAX: lane 0's best row so far
+  int best_i = INT32_MAX;
   bool first = true;
   for (; r0 < nout; r0 += stride_rows) {
     float acc[R][S];
@@ -220,6 +224,18 @@ __global__ __launch_bounds__(256) void gemv_kernel(
 #pragma unroll
           for (int b = 0; b < S; ++b)
             store(r0, r, b, v[r][b], POST == POST_SWIGLU ? v[(r + RO) % R][b] : 0.0f);
+        if constexpr (POST == POST_ARGMAX) {
+          // rows in increasing order, strict >: the lowest row among equal
+          // values; NaN never wins
+#pragma unroll
+          for (int r = 0; r < R; ++r) {
+            const float yv = inv * v[r][0];
+            if (r0 + r < n && yv > best_v) {
+              best_v = yv;
+              best_i = (int)(r0 + r);
+            }
+          }
+        }
       }
     } else {
 #pragma unroll
@@ -238,6 +254,26 @@ __global__ __launch_bounds__(256) void gemv_kernel(
         store(r0, r, b, v, 0.0f);
       }
       __syncthreads();
+    }
+  }
+  if constexpr (POST == POST_ARGMAX) {
+    __shared__ float bv[kWaves];
+    __shared__ int bi[kWaves];
+    if (lane == 0) {
+      bv[wid] = best_v;
+      bi[wid] = best_i;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      float b = bv[0];
+      int i = bi[0];
+      for (int u = 1; u < kWaves; ++u)
+        if (bv[u] > b || (bv[u] == b && bi[u] < i)) {
+          b = bv[u];
+          i = bi[u];
+        }
+      amax[blockIdx.x] = b;
+      reinterpret_cast<int *>(amax)[gridDim.x + blockIdx.x] = i;
     }
   }
 }
@@ -294,11 +330,12 @@ hipError_t launch_fast(const LinearArgs &a, const float *x, float *y, int64_t ca
   if (S * a.m <= kLdsStageFloats) {
     size_t lds = (size_t)S * a.m * sizeof(float);
     hipLaunchKernelGGL((gemv_kernel<G, KIND, S, R, SPLITK, true, PRE_NONE, POST_STORE, NPF>), grid,
-                       block, lds, st, a.w, a.row_bytes, a.n, x, a.m, y, nullptr, 0.0f, nullptr);
+                       block, lds, st, a.w, a.row_bytes, a.n, x, a.m, y, nullptr, 0.0f, nullptr,
+                       nullptr);
   } else {
     hipLaunchKernelGGL((gemv_kernel<G, KIND, S, R, SPLITK, false, PRE_NONE, POST_STORE, NPF>),
                        grid, block, 0, st, a.w, a.row_bytes, a.n, x, a.m, y, nullptr, 0.0f,
-                       nullptr);
+                       nullptr, nullptr);
   }
   return hipGetLastError();
 }
@@ -363,13 +400,14 @@ hipError_t launch_fused_t(const FusedLinearArgs &f, int64_t cap, hipStream_t st)
   if constexpr (PRE == PRE_NONE) {
     if (a.m > kLdsStageFloats) {
       hipLaunchKernelGGL((gemv_kernel<G, KIND, 1, R, SPLITK, false, PRE, POST, NPF>), grid, block,
-                         0, st, a.w, a.row_bytes, a.n, x, a.m, a.y, f.wn, f.eps, f.res);
+                         0, st, a.w, a.row_bytes, a.n, x, a.m, a.y, f.wn, f.eps, f.res, f.part);
       return hipGetLastError();
     }
   }
+  if (f.grid_out) *f.grid_out = (int)grid.x;
   hipLaunchKernelGGL((gemv_kernel<G, KIND, 1, R, SPLITK, true, PRE, POST, NPF>), grid, block,
                      (size_t)a.m * sizeof(float), st, a.w, a.row_bytes, a.n, x, a.m, a.y, f.wn,
-                     f.eps, f.res);
+                     f.eps, f.res, f.part);
   return hipGetLastError();
 }
 
@@ -381,6 +419,10 @@ hipError_t launch_fused_rows(const FusedLinearArgs &f, hipStream_t st) {
   if constexpr (POST == POST_SWIGLU) {
     if (a.n >= 8192) return launch_fused_t<G, KIND, 4, 1, PRE, POST>(f, 1024, st);
     return launch_fused_t<G, KIND, 2, 1, PRE, POST>(f, 4096, st);
+  } else if constexpr (POST == POST_ARGMAX) {
+    // whole rows per wave; the grid stays within kArgmaxMaxBlocks partials
+    if (a.n >= 65536) return launch_fused_t<G, KIND, 2, 1, PRE, POST, 1>(f, 8192, st);
+    return launch_fused_t<G, KIND, 1, 1, PRE, POST>(f, 4096, st);
   } else {
     if (a.m > 4096 && a.m % 64 == 0) return launch_fused_t<G, KIND, 4, 4, PRE, POST>(f, 1024, st);
     if (a.n >= 65536) return launch_fused_t<G, KIND, 2, 1, PRE, POST, 1>(f, 8192, st);
@@ -394,6 +436,7 @@ hipError_t launch_fused_pre(const FusedLinearArgs &f, hipStream_t st) {
   if (f.post == POST_STORE) return launch_fused_rows<G, KIND, PRE, POST_STORE>(f, st);
   if (f.post == POST_RESIDUAL) return launch_fused_rows<G, KIND, PRE, POST_RESIDUAL>(f, st);
   if (f.post == POST_SWIGLU) return launch_fused_rows<G, KIND, PRE, POST_SWIGLU>(f, st);
+  if (f.post == POST_ARGMAX) return launch_fused_rows<G, KIND, PRE, POST_ARGMAX>(f, st);
   return hipErrorInvalidValue;
 }
 
@@ -416,12 +459,13 @@ bool gemv_fused_supported(const FusedLinearArgs &f) {
          (a.G == 32 || a.G == 64) && reinterpret_cast<uintptr_t>(a.w) % 16 == 0 &&
          a.row_bytes % 16 == 0 && ((a.m / a.G) * sb) % 16 == 0 &&
          reinterpret_cast<uintptr_t>(a.x) % 16 == 0 && pre >= PRE_NONE && pre <= PRE_SWIGLU &&
-         post >= POST_STORE && post <= POST_SWIGLU && (post != POST_SWIGLU || a.n % 2 == 0);
+         post >= POST_STORE && post <= POST_ARGMAX && (post != POST_SWIGLU || a.n % 2 == 0) &&
+         (post != POST_ARGMAX || a.n <= INT32_MAX);
 }
 
 hipError_t launch_gemv_fused(const FusedLinearArgs &f, hipStream_t st) {
   const LinearArgs &a = f.lin;
-  if (!gemv_fused_supported(f)) return hipErrorInvalidValue;
+  if (!gemv_fused_supported(f) || (f.post == POST_ARGMAX && !f.part)) return hipErrorInvalidValue;
   if (a.n == 0) return hipSuccess;
   if (a.G == 64 && a.kind == SCALE_F16) return launch_fused_g<64, SCALE_F16>(f, st);
   if (a.G == 64 && a.kind == SCALE_F32) return launch_fused_g<64, SCALE_F32>(f, st);

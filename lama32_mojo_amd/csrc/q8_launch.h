@@ -46,14 +46,22 @@ hipError_t launch_gemv(const LinearArgs &a, hipStream_t st);
 //   POST_SWIGLU:   rows [0, n/2) are gate rows and [n/2, n) up rows; stores
 //                  y[j] = silu(g_j) * u_j for j < n/2.
 enum { PRE_NONE = 0, PRE_RMSNORM = 1, PRE_SWIGLU = 2 };
-enum { POST_STORE = 0, POST_RESIDUAL = 1, POST_SWIGLU = 2 };
+//   POST_ARGMAX:   y stored; each workgroup also writes its largest y and
+//                  its row (strict > in row order, so the lowest row among
+//                  equal values; NaN never wins) to part[blockIdx] and
+//                  ((int *)part)[grid + blockIdx]: the partials that
+//                  launch_argmax_finish reduces.
+enum { POST_STORE = 0, POST_RESIDUAL = 1, POST_SWIGLU = 2, POST_ARGMAX = 3 };
 struct FusedLinearArgs {
   LinearArgs lin;        // s = 1, f32 x, aligned rows
   int pre, post;
   const uint16_t *wn;    // PRE_RMSNORM: m bf16 norm weights
   float eps;
   const float *res;      // POST_RESIDUAL: residual [n]
+  float *part = nullptr; // POST_ARGMAX: 2 x kArgmaxMaxBlocks words
+  int *grid_out = nullptr;   // POST_ARGMAX: receives the workgroup count
 };
+constexpr int kArgmaxMaxBlocks = 8192;
 // False when the shape cannot take the fused path (x staged in LDS).
 bool gemv_fused_supported(const FusedLinearArgs &f);
 hipError_t launch_gemv_fused(const FusedLinearArgs &a, hipStream_t st);
@@ -128,6 +136,23 @@ hipError_t launch_swiglu(float *g, const float *u, int64_t n, hipStream_t st);
 hipError_t launch_res_add(const float *x, const float *o, float *y, int64_t n, hipStream_t st);
 hipError_t launch_add(const float *x, float *y, int64_t n, hipStream_t st);
 hipError_t launch_argmax(const float *v, int64_t n, int32_t *out, hipStream_t st);
+// Reduce the POST_ARGMAX partials of `nblocks` workgroups (the argmax of the
+// n logits, as launch_argmax: index 0 when logits[0] is NaN or nothing beats
+// it), write it to ids[0], add pos_step to *pos (pos may be null) and, with
+// emb non-null, gather that id's embedding row (d floats) into xnext.
+struct ArgmaxFinishArgs {
+  const float *part;
+  int nblocks;
+  const float *logits;
+  int32_t *ids;
+  int *pos;
+  int pos_step;
+  const uint8_t *emb;    // packed table (vocab rows) or null
+  int64_t row_bytes, vocab, d;
+  int G, kind;
+  float *xnext;
+};
+hipError_t launch_argmax_finish(const ArgmaxFinishArgs &a, hipStream_t st);
 hipError_t launch_pos_advance(int *pos, int s, hipStream_t st);
 
 }  // namespace q8

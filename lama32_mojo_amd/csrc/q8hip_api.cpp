@@ -641,6 +641,84 @@ int q8_linear_fused(q8_ctx *ctx, q8_buf *w, uint64_t owt_u16, q8_buf *a, uint64_
   return ok(ctx);
 }
 
+int q8_head_argmax(q8_ctx *ctx, q8_buf *w, uint64_t owt_u16, uint64_t onorm_u16, float eps,
+                   q8_buf *a, uint64_t ox_f32, uint64_t oy_f32, int64_t m, int64_t n, int G,
+                   int scale_dtype, q8_buf *ids, uint64_t oid_i32, q8_buf *posbuf,
+                   uint64_t opos_i32, int64_t pos_step, int gather, uint64_t oemb_u16,
+                   uint64_t onext_f32) {
+  if (int rc = check_ctx(ctx)) return rc;
+  if (int rc = check_linear(ctx, "q8_head_argmax", w, owt_u16, 1, m, n, G, scale_dtype))
+    return rc;
+  if (!a || !ids) return fail(ctx, Q8_ERR_ARG, "q8_head_argmax: null buffer");
+  if (n < 1 || n > INT32_MAX)
+    return fail(ctx, Q8_ERR_SHAPE, "q8_head_argmax: n=%lld", (long long)n);
+  if (int rc = check_f32(ctx, a, ox_f32, (uint64_t)m, "q8_head_argmax", "x")) return rc;
+  if (int rc = check_f32(ctx, a, oy_f32, (uint64_t)n, "q8_head_argmax", "logits")) return rc;
+  if (overlaps(ox_f32, ox_f32 + (uint64_t)m, oy_f32, oy_f32 + (uint64_t)n))
+    return fail(ctx, Q8_ERR_ARG, "q8_head_argmax: x and logits overlap");
+  if (!fits(onorm_u16, (uint64_t)m, 2, w->size))
+    return fail(ctx, Q8_ERR_RANGE, "q8_head_argmax: norm weights exceed the weight buffer");
+  if (!fits(oid_i32, 1, 4, ids->size))
+    return fail(ctx, Q8_ERR_RANGE, "q8_head_argmax: id slot exceeds its buffer");
+  if (posbuf && !fits(opos_i32, 1, 4, posbuf->size))
+    return fail(ctx, Q8_ERR_RANGE, "q8_head_argmax: position slot exceeds its buffer");
+  if (pos_step < INT32_MIN || pos_step > INT32_MAX)
+    return fail(ctx, Q8_ERR_ARG, "q8_head_argmax: pos_step=%lld", (long long)pos_step);
+  const uint64_t rs = (uint64_t)rowstride_u16(m, G, scale_dtype);
+  if (gather) {
+    // the next token's embedding: n packed rows of m at oemb (vocab = n)
+    if (!fits(oemb_u16, (uint64_t)n * rs, 2, w->size))
+      return fail(ctx, Q8_ERR_RANGE, "q8_head_argmax: embedding table exceeds the weight buffer");
+    if (int rc = check_f32(ctx, a, onext_f32, (uint64_t)m, "q8_head_argmax", "x_next")) return rc;
+    if (overlaps(onext_f32, onext_f32 + (uint64_t)m, oy_f32, oy_f32 + (uint64_t)n))
+      return fail(ctx, Q8_ERR_ARG, "q8_head_argmax: x_next overlaps the logits");
+  }
+  q8::FusedLinearArgs f;
+  q8::LinearArgs &la = f.lin;
+  la.w = bytes(w, owt_u16 * 2);
+  la.row_bytes = (int64_t)rs * 2;
+  la.x = bytes(a, ox_f32 * 4);
+  la.x_is_bf16 = 0;
+  la.y = fptr(a, oy_f32);
+  la.s = 1;
+  la.m = m;
+  la.n = n;
+  la.G = G;
+  la.kind = scale_dtype;
+  f.pre = q8::PRE_RMSNORM;
+  f.post = q8::POST_ARGMAX;
+  f.wn = reinterpret_cast<const uint16_t *>(bytes(w, onorm_u16 * 2));
+  f.eps = eps;
+  f.res = nullptr;
+  f.part = ctx->gemm_ws;   // 2 x 8192 words of partials, read by the second launch
+  int grid = 0;
+  f.grid_out = &grid;
+  if (!q8::gemv_fused_supported(f))
+    return fail(ctx, Q8_ERR_UNSUPPORTED, "q8_head_argmax: m=%lld (needs m <= 16384, m %% 32 == 0, "
+                "16-byte aligned rows and x, 8-byte aligned norm weights)", (long long)m);
+  if (ctx->host_only) return fail(ctx, Q8_ERR_NODEVICE, "q8_head_argmax: host-only context");
+  if (int rc = set_device(ctx)) return rc;
+  hipError_t e = q8::launch_gemv_fused(f, ctx->stream);
+  if (e != hipSuccess) return hip_fail(ctx, e, "q8_head_argmax launch");
+  q8::ArgmaxFinishArgs fa;
+  fa.part = ctx->gemm_ws;
+  fa.nblocks = grid;
+  fa.logits = la.y;
+  fa.ids = reinterpret_cast<int32_t *>(bytes(ids, oid_i32 * 4));
+  fa.pos = posbuf ? reinterpret_cast<int *>(bytes(posbuf, opos_i32 * 4)) : nullptr;
+  fa.pos_step = (int)pos_step;
+  fa.emb = gather ? bytes(w, oemb_u16 * 2) : nullptr;
+  fa.row_bytes = (int64_t)rs * 2;
+  fa.vocab = n;
+  fa.d = m;
+  fa.G = G;
+  fa.kind = scale_dtype;
+  fa.xnext = gather ? fptr(a, onext_f32) : nullptr;
+  e = q8::launch_argmax_finish(fa, ctx->stream);
+  if (e != hipSuccess) return hip_fail(ctx, e, "q8_head_argmax finish launch");
+  return ok(ctx);
+}
+
 int q8_rmsnorm(q8_ctx *ctx, q8_buf *w, uint64_t owt_u16, q8_buf *a, uint64_t ox_f32,
                uint64_t oy_f32, int64_t rows, int64_t d, float eps) {
   if (int rc = check_ctx(ctx)) return rc;

@@ -237,6 +237,7 @@ class Q8Llama:
         self.n_cached = 0
         self.graph = None
         self.graph_logits = None
+        self.graph_x = None
 
     # ---- weights -------------------------------------------------------------
     def _check_checkpoint(self, st, names: Sequence[str]) -> None:
@@ -416,15 +417,35 @@ class Q8Llama:
                       oh + (s - 1) * cfg.hidden, onrm, 1, cfg.hidden, cfg.eps)
         return self.linear(onrm, 1, cfg.hidden, self.w.o(head), cfg.vocab)
 
-    def _run(self, s: int, pos0: int, device_pos: bool) -> int:
-        cur = self.embed(s)
+    def _layers(self, cur: int, s: int, pos0: int, device_pos: bool) -> int:
+        """Every layer over the s rows at cur (ping-pong residual buffers);
+        returns the offset of the final residual rows."""
         nxt = self.a.alloc(s * self.cfg.hidden)
         for L in range(self.cfg.layers):
             mark = self.a.mark()
             self.layer(L, cur, s, pos0, device_pos, oh=nxt)
             self.a.reset(mark)
             cur, nxt = nxt, cur
-        return self._head(cur, s)
+        return cur
+
+    def _run(self, s: int, pos0: int, device_pos: bool) -> int:
+        return self._head(self._layers(self.embed(s), s, pos0, device_pos), s)
+
+    def _head_name(self) -> str:
+        return "model.embed_tokens.weight" if self.cfg.tied else "lm_head.weight"
+
+    def _head_argmax(self, oh: int, posbuf=None, onext: int | None = None) -> int:
+        """Final norm + lm_head + argmax -> ids[0] in two launches (position
+        step and the next embedding row with posbuf / onext); returns the
+        logits offset."""
+        cfg = self.cfg
+        olg = self.a.alloc(cfg.vocab)
+        q8hip.head_argmax(self.ctx, self.w.buf, self.w.o(self._head_name()),
+                          self.w.o("model.norm.weight"), cfg.eps, self.a.buf, oh, olg,
+                          cfg.hidden, cfg.vocab, self.G, self.scale, self.ids, 0, posbuf, 0, 1,
+                          self.w.o("model.embed_tokens.weight") if onext is not None else None,
+                          onext or 0)
+        return olg
 
     def _check_room(self, s: int) -> None:
         if self.n_cached + s > self.maxlen:
@@ -449,8 +470,12 @@ class Q8Llama:
         self._check_room(s)
         self.ids.upload(np.asarray(ids, dtype=np.int32))
         mark = self.a.mark()
-        olg = self._run(s, self.n_cached, False)
-        q8hip.argmax(self.ctx, self.a.buf, olg, self.cfg.vocab, self.ids, 0)
+        oh = self._layers(self.embed(s), s, self.n_cached, False)
+        if self.fuse:
+            self._head_argmax(oh + (s - 1) * self.cfg.hidden)
+        else:
+            olg = self._head(oh, s)
+            q8hip.argmax(self.ctx, self.a.buf, olg, self.cfg.vocab, self.ids, 0)
         nxt = int(self.ids.download((1,), np.int32)[0])
         self.a.reset(mark)
         self.n_cached += s
@@ -459,31 +484,49 @@ class Q8Llama:
 
     # ---- captured decode step -------------------------------------------------
     def capture_decode(self) -> None:
-        """Capture one decode step as a HIP graph: read ids[0] and the device
-        position, run every layer, write argmax -> ids[0], position += 1."""
+        """Capture one decode step as a HIP graph that reads the token's
+        embedding row and the device position and ends by writing the argmax
+        to ids[0], advancing the position and (fused) gathering the next
+        token's embedding row into the step's input: every launch of a
+        token in one graph, no host work between tokens."""
         if self.graph is not None:
             return
-        ctx = self.ctx
+        ctx, H = self.ctx, self.cfg.hidden
         mark = self.a.mark()
+        self.graph_x = self.a.alloc(H)          # the step's input row (persistent)
         self.ctx.graph_begin()
         try:
-            olg = self._run(1, 0, True)
-            q8hip.argmax(ctx, self.a.buf, olg, self.cfg.vocab, self.ids, 0)
-            q8hip.pos_advance(ctx, self.posbuf, 0, 1)
+            if self.fuse:
+                oh = self._layers(self.graph_x, 1, 0, True)
+                olg = self._head_argmax(oh, posbuf=self.posbuf, onext=self.graph_x)
+            else:
+                olg = self._run(1, 0, True)
+                q8hip.argmax(ctx, self.a.buf, olg, self.cfg.vocab, self.ids, 0)
+                q8hip.pos_advance(ctx, self.posbuf, 0, 1)
         finally:
             self.graph = self.ctx.graph_end()
         self.graph_logits = olg
         self.graph_mark = mark
         # the captured step owns its arena slice for the model's lifetime
 
+    def prime_decode(self, first_id: int) -> None:
+        """Set up replays of the captured step: the token id, the device
+        position (the cached length) and, for the fused step, the first
+        token's embedding row in the step's input."""
+        self.capture_decode()
+        self.ids.upload(np.array([first_id], dtype=np.int32))
+        self.posbuf.upload(np.array([self.n_cached], dtype=np.int32))
+        if self.fuse:
+            q8hip.embed_gather(self.ctx, self.w.buf, self.w.o("model.embed_tokens.weight"),
+                               self.ids, 0, self.a.buf, self.graph_x, 1, self.cfg.hidden,
+                               self.cfg.vocab, self.G, self.scale)
+
     def decode_steps(self, first_id: int, n: int) -> list[int]:
         """Greedy-decode n tokens starting from first_id at the current
         position by replaying the captured step; returns the n ids."""
         if self.n_cached + n > self.maxlen:
             raise RuntimeError("KV cache full")
-        self.capture_decode()
-        self.ids.upload(np.array([first_id], dtype=np.int32))
-        self.posbuf.upload(np.array([self.n_cached], dtype=np.int32))
+        self.prime_decode(first_id)
         out = []
         for _ in range(n):
             self.graph.launch()
@@ -495,9 +538,7 @@ class Q8Llama:
         """n replays of the captured step without host readback (timing)."""
         if self.n_cached + n > self.maxlen:
             raise RuntimeError("KV cache full")
-        self.capture_decode()
-        self.ids.upload(np.array([first_id], dtype=np.int32))
-        self.posbuf.upload(np.array([self.n_cached], dtype=np.int32))
+        self.prime_decode(first_id)
         for _ in range(n):
             self.graph.launch()
         self.n_cached += n

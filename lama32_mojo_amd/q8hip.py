@@ -71,6 +71,8 @@ SIGNATURES = {
     "q8_embed_gather": (_I, [_P, _P, _U64, _P, _U64, _P, _U64, _I64, _I64, _I64, _I, _I]),
     "q8_linear_fused": (_I, [_P, _P, _U64, _P, _U64, _U64, _I64, _I64, _I, _I, _I, _U64,
                             ctypes.c_float, _I, _U64]),
+    "q8_head_argmax": (_I, [_P, _P, _U64, _U64, ctypes.c_float, _P, _U64, _U64, _I64, _I64, _I,
+                           _I, _P, _U64, _P, _U64, _I64, _I, _U64, _U64]),
     "q8_rmsnorm": (_I, [_P, _P, _U64, _P, _U64, _U64, _I64, _I64, ctypes.c_float]),
     "q8_st_open": (_I, [ctypes.c_char_p, ctypes.POINTER(_P)]),
     "q8_st_close": (None, [_P]),
@@ -300,6 +302,21 @@ def linear_fused(ctx: Context, w: Buffer, owt_u16: int, a: Buffer, ox_f32: int, 
     ctx.check(ctx._lib.q8_linear_fused(ctx.h, w.h, int(owt_u16), a.h, int(ox_f32), int(oy_f32),
                                        int(m), int(n), int(G), scale_code(scale), int(pre),
                                        int(onorm_u16), float(eps), int(post), int(ores_f32)))
+
+
+def head_argmax(ctx: Context, w: Buffer, owt_u16: int, onorm_u16: int, eps: float, a: Buffer,
+                ox_f32: int, oy_f32: int, m: int, n: int, G: int, scale, ids: Buffer,
+                oid_i32: int = 0, posbuf: Buffer | None = None, opos_i32: int = 0,
+                pos_step: int = 1, oemb_u16: int | None = None, onext_f32: int = 0) -> None:
+    """rmsnorm + lm_head + argmax -> ids[oid] (+ position step, + the next
+    token's embedding row into onext_f32 when oemb_u16 is given):
+    q8_head_argmax."""
+    gather = oemb_u16 is not None
+    ctx.check(ctx._lib.q8_head_argmax(ctx.h, w.h, int(owt_u16), int(onorm_u16), float(eps), a.h,
+                                      int(ox_f32), int(oy_f32), int(m), int(n), int(G),
+                                      scale_code(scale), ids.h, int(oid_i32), _h(posbuf),
+                                      int(opos_i32), int(pos_step), int(gather),
+                                      int(oemb_u16) if gather else 0, int(onext_f32)))
 
 
 def linear_bf16act(ctx: Context, w: Buffer, owt_u16: int, x: Buffer, ox_bf16: int, y: Buffer,

@@ -134,6 +134,34 @@ def test_linear_fused_validation(hctx):
     assert code_of(F, hctx, wb, 0, ab, 0, big, big, 1)[0] == Q8_ERR_NODEVICE
 
 
+def test_head_argmax_validation(hctx):
+    m, n = 2048, 64
+    rs = q8hip.rowstride_u16(m)
+    w = hctx.alloc(2 * (2 * n * rs + m))
+    a = hctx.alloc(4 * 16384)
+    ids, pb = hctx.alloc(8), hctx.alloc(8)
+    H = q8hip.head_argmax
+    norm, emb = 2 * n * rs, n * rs
+    ok = dict(oemb_u16=emb, onext_f32=8192)
+    assert code_of(H, hctx, w, 0, norm, 1e-5, a, 0, 4096, m, n, 64, "f16", ids, 0, pb, 0, 1,
+                   **ok)[0] == Q8_ERR_NODEVICE
+    # logits overlap x; next row overlaps the logits
+    assert code_of(H, hctx, w, 0, norm, 1e-5, a, 0, 2000, m, n, 64, "f16", ids)[0] == Q8_ERR_ARG
+    assert code_of(H, hctx, w, 0, norm, 1e-5, a, 0, 4096, m, n, 64, "f16", ids, 0, pb, 0, 1,
+                   oemb_u16=emb, onext_f32=4100)[0] == Q8_ERR_ARG
+    # id / position slots, norm weights and embedding table out of range
+    assert code_of(H, hctx, w, 0, norm, 1e-5, a, 0, 4096, m, n, 64, "f16", ids, 2)[0] == Q8_ERR_RANGE
+    assert code_of(H, hctx, w, 0, norm, 1e-5, a, 0, 4096, m, n, 64, "f16", ids, 0, pb,
+                   2)[0] == Q8_ERR_RANGE
+    assert code_of(H, hctx, w, 0, norm + 1, 1e-5, a, 0, 4096, m, n, 64, "f16",
+                   ids)[0] == Q8_ERR_RANGE
+    assert code_of(H, hctx, w, 0, norm, 1e-5, a, 0, 4096, m, n, 64, "f16", ids,
+                   oemb_u16=emb + n * rs, onext_f32=8192)[0] == Q8_ERR_RANGE
+    # x or logits past the arena
+    assert code_of(H, hctx, w, 0, norm, 1e-5, a, 0, 16380, m, n, 64, "f16",
+                   ids)[0] == Q8_ERR_RANGE
+
+
 def test_linear_bf16act_validation(hctx):
     rs = q8hip.rowstride_u16(1024, 32, "f32")
     w = hctx.alloc(2 * 64 * rs)

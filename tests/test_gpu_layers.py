@@ -494,3 +494,73 @@ def test_qwen_style_model_forward_and_greedy_decode(ctx):
     finally:
         m.close()
         u.close()
+
+
+@pytest.mark.parametrize("G,scale", [(64, "f16"), (32, "f32")])
+@pytest.mark.parametrize("m,n", [(2048, 128256), (1024, 151936), (512, 5000)])
+def test_head_argmax_equals_linear_then_argmax(ctx, G, scale, m, n):
+    """q8_head_argmax: the logits of q8_linear_fused (rmsnorm prologue), the
+    argmax of q8_argmax on them (also with a tied maximum: the lower index
+    wins; and NaN logits give 0), the position step, and the next
+    embedding row exactly as q8_embed_gather gives it."""
+    say("head_argmax", G, scale, m, n)
+    rng = np.random.default_rng(n)
+    rs = q8hip.rowstride_u16(m, G, scale)
+    wsrc = ctx.alloc(2 * n * m)
+    wsrc.upload(f32_to_bf16_bits((0.05 * rng.standard_normal((n, m))).astype(np.float32)))
+    emb = n * rs                                     # a second table (the untied case)
+    onorm = 2 * n * rs
+    w = ctx.alloc(2 * (2 * n * rs + m))
+    q8hip.quantize_pack(ctx, wsrc, 0, q8hip.Q8_SRC_BF16, n, m, w, 0, G, scale)
+    q8hip.quantize_pack(ctx, wsrc, 0, q8hip.Q8_SRC_BF16, n, m, w, emb, G, scale)
+    wsrc.free()
+    w.upload(f32_to_bf16_bits((1 + 0.1 * rng.standard_normal(m)).astype(np.float32)), 2 * onorm)
+    ox, oy, oy2, onext, oref = 0, m, m + n, m + 2 * n, 2 * m + 2 * n
+    a = arena(ctx, 3 * m + 2 * n)
+    x = rng.standard_normal(m).astype(np.float32)
+    put(a, ox, x)
+    ids, pb = ctx.alloc(16), ctx.alloc(16)
+    pb.upload(np.array([41, 0, 0, 0], np.int32))
+    q8hip.head_argmax(ctx, w, 0, onorm, 1e-5, a, ox, oy, m, n, G, scale, ids, 0, pb, 0, 3, emb,
+                      onext)
+    got = int(ids.download((1,), np.int32)[0])
+    q8hip.linear_fused(ctx, w, 0, a, ox, oy2, m, n, G, scale, q8hip.PRE_RMSNORM, onorm, 1e-5)
+    lg = get(a, oy2, (n,))
+    assert np.array_equal(get(a, oy, (n,)), lg)
+    q8hip.argmax(ctx, a, oy2, n, ids, 1)
+    want = int(ids.download((2,), np.int32)[1])
+    assert got == want == int(np.argmax(lg))
+    assert int(pb.download((1,), np.int32)[0]) == 44
+    q8hip.embed_gather(ctx, w, emb, ids, 0, a, oref, 1, m, n, G, scale)
+    assert np.array_equal(get(a, onext, (m,)), get(a, oref, (m,)))
+    # a tie: copy the winning row to a lower index -> the lower index wins
+    if got > 0:
+        lo = got // 2
+        row = w.download((rs,), np.uint16, 2 * got * rs)
+        w.upload(row, 2 * lo * rs)
+        q8hip.head_argmax(ctx, w, 0, onorm, 1e-5, a, ox, oy, m, n, G, scale, ids, 0)
+        assert int(ids.download((1,), np.int32)[0]) == lo
+    # NaN logits (a NaN in x): index 0, as the reference's scan from v[0]
+    x[3] = np.nan
+    put(a, ox, x)
+    q8hip.head_argmax(ctx, w, 0, onorm, 1e-5, a, ox, oy, m, n, G, scale, ids, 0)
+    assert int(ids.download((1,), np.int32)[0]) == 0
+    for b in (a, w, ids, pb):
+        b.free()
+
+
+def test_fused_graph_decode_equals_unfused_graph(ctx):
+    """The captured fused step (lm_head + argmax + position + next embedding
+    in two launches) gives the greedy ids of the unfused captured step."""
+    say("fused graph")
+    spec, t, inv = tiny_model(seed=12)
+    a = gpu_model(ctx, spec, t, 32, fuse=True)
+    b = gpu_model(ctx, spec, t, 32, fuse=False)
+    try:
+        first = a.forward_argmax([9, 8, 7])
+        assert b.forward_argmax([9, 8, 7]) == first
+        assert a.decode_steps(first, 10) == b.decode_steps(first, 10)
+        assert int(a.posbuf.download((1,), np.int32)[0]) == 13
+    finally:
+        a.close()
+        b.close()
