@@ -223,7 +223,8 @@ int q8_rope_kv(q8_ctx *ctx, q8_buf *a, uint64_t oq_f32, uint64_t ok_f32,
                q8_buf *posbuf, uint64_t opos_i32, int nheads, int nkv,
                int head_dim);
 
-/* Floats of activation-arena scratch q8_attention needs. */
+/* Floats of activation-arena scratch q8_attention needs (0 from s = 16 on,
+ * where attention is one pass on the matrix cores). */
 uint64_t q8_attention_scratch_floats(int64_t s, int nheads, int head_dim,
                                      int64_t maxlen);
 
@@ -231,9 +232,11 @@ uint64_t q8_attention_scratch_floats(int64_t s, int nheads, int head_dim,
  * q at oq (query row i at position pos0 + i attends cache rows
  * 0 .. pos0 + i; head h reads KV head h / (nheads / nkv); scores scaled by
  * 1/sqrt(head_dim)) -- k_scores, k_softmax_rows and k_att_out
- * (src/llama_common.mojo:402-473) with their score buffer replaced by
- * q8_attention_scratch_floats() floats at oscratch.  head_dim 64 or 128,
- * nheads / nkv in {1, 2, 4, 8}.  Position as in q8_rope_kv. */
+ * (src/llama_common.mojo:402-473) with their score buffer replaced by an
+ * online softmax: for s >= 16 one MFMA pass per (16..128-row block, KV
+ * head), below that per-split partials in q8_attention_scratch_floats()
+ * floats at oscratch (oscratch is unused when that is 0).  head_dim 64 or
+ * 128, nheads / nkv in {1, 2, 4, 8}.  Position as in q8_rope_kv. */
 int q8_attention(q8_ctx *ctx, q8_buf *a, uint64_t oq_f32, q8_buf *kv,
                  uint64_t okc_f16, uint64_t ovc_f16, int64_t maxlen,
                  uint64_t oy_f32, uint64_t oscratch_f32, int64_t s, int64_t pos0,

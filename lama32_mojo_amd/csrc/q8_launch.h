@@ -93,13 +93,18 @@ hipError_t launch_rope_kv(float *q, float *k, const float *v, __half *kc, __half
 struct AttnArgs {
   const float *q;        // [s, nheads * head_dim], rotated
   const __half *kc, *vc; // [maxlen, nkv * head_dim]
-  float *part;           // scratch: s * nheads * nsplit * (head_dim + 2) floats
+  float *part;           // scratch (s < kPrefillMinRows only):
+                         //   s * nheads * nsplit * (head_dim + 2) floats
   float *out;            // [s, nheads * head_dim]
   int s, nheads, nkv, head_dim, nsplit;
   const int *posp;       // device position (or null: pos0)
   int pos0;
   int maxlen;            // cache rows; positions past it are clamped
 };
+// Row counts from which attention runs as one MFMA pass per (row block, KV
+// head) with no scratch; below it, as (KV head, 64-key split) partials
+// merged by a second kernel.
+constexpr int kPrefillMinRows = 16;
 // Causal GQA attention of s query rows at positions pos0 .. pos0+s-1 over
 // cache rows 0 .. pos0+i; nsplit = ceil(maxlen / 64).
 hipError_t launch_attention(const AttnArgs &a, hipStream_t st);

@@ -235,6 +235,238 @@ __global__ __launch_bounds__(64) void attn_combine_kernel(const float *__restric
     out[(int64_t)i * nheads * HD + h * HD + threadIdx.x + 64 * e] = o[e] * il;
 }
 
+// ---- multi-row causal attention on the matrix cores (prompt rows) -----------
+// One block of 4 waves serves one KV head and PB = 4 * (32 / GRP) consecutive
+// query rows; each wave owns 32 columns, a column being one (row, query head)
+// pair of the group.  Per tile of 64 keys the block stages K row-major and V
+// transposed in LDS, and each wave forms S^T = K Q^T and O^T += V^T P^T with
+// v_mfma_f32_32x32x16_f16 and an online softmax over its columns.
+// The f32 operands enter as binary16 hi + lo pairs: q scaled per column by a
+// power of two (largest |q| in [2^14, 2^15), so lo keeps its bits), p by
+// 2^14; K and V are binary16 already, so the products are exact and scores
+// and sums carry f32-level error.  Scores are kept in the log2 domain
+// (scaled by log2(e) / sqrt(head_dim)), so the softmax uses exp2.
+// Lane layout of the 32x32x16 MFMA (lane l, h = l / 32): A element i is
+// A[l % 32][8h + i], B element i is B[8h + i][l % 32], and accumulator
+// element v is D[8(v / 4) + 4h + v % 4][l % 32].  The keys of a P^T column
+// held by a lane follow the accumulator layout, so V^T stores each 16-key
+// chunk permuted (key 8a + 4h + b at 8h + 4a + b) to make one lane's eight
+// keys of an MFMA step contiguous.
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+
+constexpr int kPrefillBK = 64;   // keys per staged tile
+
+__device__ __forceinline__ void split_f16(float a, _Float16 &hi, _Float16 &lo) {
+  hi = (_Float16)a;
+  lo = (_Float16)(a - (float)hi);
+}
+
+template <int HD, int GRP>
+__global__ __launch_bounds__(256) void attn_prefill_kernel(const float *__restrict__ q,
+                                                           const __half *__restrict__ kc,
+                                                           const __half *__restrict__ vc,
+                                                           float *__restrict__ out, int s,
+                                                           int nheads, int nkv, const int *posp,
+                                                           int pos0_host, int maxlen) {
+  constexpr int BK = kPrefillBK;
+  constexpr int KS = HD / 16;                    // 16-dim steps of a score tile
+  constexpr int DT = HD / 32;                    // 32-dim tiles of the output
+  constexpr int PW = 32 / GRP;                   // query rows per wave
+  constexpr int PB = 4 * PW;                     // query rows per block
+  constexpr int KST = HD + 8;                    // K row stride in LDS (halves)
+  constexpr int VST = BK + 8;                    // V^T row stride in LDS (halves)
+  constexpr int KCH = BK * (HD / 8) / 256;       // 16-byte K chunks per thread
+  constexpr int VCH = (BK / 2) * (HD / 8) / 256; // V key pairs x 8 dims per thread
+  static_assert(KCH >= 1 && VCH >= 1, "tile too small for 256 threads");
+  __shared__ __attribute__((aligned(16))) _Float16 ks[BK * KST];
+  __shared__ __attribute__((aligned(16))) _Float16 vt[HD * VST];
+
+  const int g = blockIdx.y;
+  const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int col = lane & 31, hf = lane >> 5;
+  const int pos0 = posp ? *posp : pos0_host;
+  const int qdim = nheads * HD, kvdim = nkv * HD;
+  const int row0 = blockIdx.x * PB;
+  const int nkeys = min(pos0 + min(row0 + PB, s), maxlen);   // keys any row of the block sees
+  const int ntiles = nkeys > 0 ? (nkeys + BK - 1) / BK : 0;
+  const int wend = min(pos0 + min(row0 + w * PW + PW, s), maxlen);   // ... any row of the wave
+  const int i = row0 + w * PW + col / GRP;       // this lane's column: row i, head
+  const int head = g * GRP + col % GRP;
+  const int irow = min(i, s - 1);
+  const int kend = min(pos0 + irow + 1, maxlen); // keys 0 .. kend-1 are visible to it
+
+  // q of the column: dims 16ks + 8h + 0..7, scaled by 2^e, split hi + lo
+  half8 qh[KS], ql[KS];
+  float cs;
+  {
+    const float *qr = q + (int64_t)irow * qdim + head * HD + 8 * hf;
+    f32x4 qv[KS][2];
+    float mx = 0.0f;
+#pragma unroll
+    for (int k = 0; k < KS; ++k) {
+      qv[k][0] = *reinterpret_cast<const f32x4 *>(qr + 16 * k);
+      qv[k][1] = *reinterpret_cast<const f32x4 *>(qr + 16 * k + 4);
+#pragma unroll
+      for (int c = 0; c < 4; ++c) mx = fmaxf(mx, fmaxf(fabsf(qv[k][0][c]), fabsf(qv[k][1][c])));
+    }
+    mx = fmaxf(mx, __shfl_xor(mx, 32));
+    const int ex = (int)((__builtin_bit_cast(uint32_t, mx) >> 23) & 255u) - 127;
+    const int e = min(max(14 - ex, -126), 126);
+    const float qsc = __builtin_ldexpf(1.0f, e);
+    cs = __builtin_ldexpf(1.44269504088896341f / sqrtf((float)HD), -e);
+#pragma unroll
+    for (int k = 0; k < KS; ++k)
+#pragma unroll
+      for (int c = 0; c < 8; ++c) {
+        _Float16 hi, lo;
+        split_f16(qv[k][c >> 2][c & 3] * qsc, hi, lo);
+        qh[k][c] = hi;
+        ql[k][c] = lo;
+      }
+  }
+
+  // staging: registers hold the next tile while the current one is used
+  u32x4 kreg[KCH], vreg[VCH][2];
+  auto load_tile = [&](int kt) {
+    const int k0 = kt * BK;
+    const int nk = min(BK, nkeys - k0);
+    // keys k0 .. k0+nk-1 of this KV head; chunks of keys past them read as zero
+    const uint32_t nbytes = (uint32_t)(((int64_t)(nk - 1) * kvdim + HD) * 2);
+    const rsrc_t rk = make_rsrc(kc + (int64_t)k0 * kvdim + g * HD, nbytes);
+    const rsrc_t rv = make_rsrc(vc + (int64_t)k0 * kvdim + g * HD, nbytes);
+#pragma unroll
+    for (int u = 0; u < KCH; ++u) {
+      const int c = threadIdx.x + 256 * u;
+      const int key = c / (HD / 8), dg = c % (HD / 8);
+      kreg[u] = bload16(rk, (uint32_t)((key * kvdim + dg * 8) * 2));
+    }
+#pragma unroll
+    for (int u = 0; u < VCH; ++u) {
+      const int c = threadIdx.x + 256 * u;
+      const int kp = c % (BK / 2), dg = c / (BK / 2);
+      const uint32_t off = (uint32_t)((2 * kp * kvdim + dg * 8) * 2);
+      vreg[u][0] = bload16(rv, off);
+      vreg[u][1] = bload16(rv, off + (uint32_t)(kvdim * 2));
+    }
+  };
+  auto store_tile = [&]() {
+#pragma unroll
+    for (int u = 0; u < KCH; ++u) {
+      const int c = threadIdx.x + 256 * u;
+      const int key = c / (HD / 8), dg = c % (HD / 8);
+      *reinterpret_cast<u32x4 *>(&ks[key * KST + dg * 8]) = kreg[u];
+    }
+#pragma unroll
+    for (int u = 0; u < VCH; ++u) {
+      const int c = threadIdx.x + 256 * u;
+      const int kp = c % (BK / 2), dg = c / (BK / 2);
+      const int key = 2 * kp, r = key & 15;
+      const int at = (key & ~15) + 8 * ((r >> 2) & 1) + 4 * (r >> 3) + (r & 3);
+#pragma unroll
+      for (int d2 = 0; d2 < 4; ++d2) {
+        // dims 8dg + 2d2 and +1: (key, key + 1) pairs as one 32-bit word each
+        const uint32_t a = vreg[u][0][d2], b = vreg[u][1][d2];
+        *reinterpret_cast<uint32_t *>(&vt[(dg * 8 + 2 * d2) * VST + at]) =
+            __builtin_amdgcn_perm(b, a, 0x05040100u);
+        *reinterpret_cast<uint32_t *>(&vt[(dg * 8 + 2 * d2 + 1) * VST + at]) =
+            __builtin_amdgcn_perm(b, a, 0x07060302u);
+      }
+    }
+  };
+
+  f32x16 o[DT];
+#pragma unroll
+  for (int t = 0; t < DT; ++t)
+#pragma unroll
+    for (int v = 0; v < 16; ++v) o[t][v] = 0.0f;
+  float m = -INFINITY, l = 0.0f;
+  if (ntiles > 0) load_tile(0);
+  for (int kt = 0; kt < ntiles; ++kt) {
+    __syncthreads();                             // every wave is done with the last tile
+    store_tile();
+    __syncthreads();
+    if (kt + 1 < ntiles) load_tile(kt + 1);
+    const int k0 = kt * BK;
+    if (k0 >= wend) continue;                    // past every row of this wave
+    f32x16 sc[2];
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+#pragma unroll
+      for (int v = 0; v < 16; ++v) sc[t][v] = 0.0f;
+#pragma unroll
+      for (int k = 0; k < KS; ++k) {
+        const half8 a = *reinterpret_cast<const half8 *>(&ks[(32 * t + col) * KST + 16 * k + 8 * hf]);
+        sc[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, qh[k], sc[t], 0, 0, 0);
+        sc[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, ql[k], sc[t], 0, 0, 0);
+      }
+    }
+    // online softmax of the column over this tile (the other 32 keys of the
+    // tile live in lane l ^ 32)
+    float tmax = -INFINITY;
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const int key = k0 + 32 * t + 8 * (v >> 2) + 4 * hf + (v & 3);
+        const float x = key < kend ? sc[t][v] * cs : -INFINITY;
+        sc[t][v] = x;
+        tmax = fmaxf(tmax, x);
+      }
+    tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
+    const float mn = fmaxf(m, tmax);             // finite: key 0 is visible to every column
+    const float alpha = exp2f(m - mn);
+    m = mn;
+    float ps = 0.0f;
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const float p = exp2f(sc[t][v] - mn);
+        sc[t][v] = p;
+        ps += p;
+      }
+    l = __builtin_fmaf(l, alpha, ps);
+#pragma unroll
+    for (int t = 0; t < DT; ++t)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) o[t][v] *= alpha;
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        half8 bh, bl;
+#pragma unroll
+        for (int c = 0; c < 8; ++c) {
+          _Float16 hi, lo;
+          split_f16(sc[t][8 * j + c] * 16384.0f, hi, lo);
+          bh[c] = hi;
+          bl[c] = lo;
+        }
+#pragma unroll
+        for (int d = 0; d < DT; ++d) {
+          const half8 a =
+              *reinterpret_cast<const half8 *>(&vt[(32 * d + col) * VST + 32 * t + 16 * j + 8 * hf]);
+          o[d] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, bh, o[d], 0, 0, 0);
+          o[d] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, bl, o[d], 0, 0, 0);
+        }
+      }
+  }
+  l += __shfl_xor(l, 32);
+  if (i < s) {
+    const float il = 1.0f / (l * 16384.0f);
+    float *orow = out + (int64_t)i * qdim + head * HD + 4 * hf;
+#pragma unroll
+    for (int d = 0; d < DT; ++d)
+#pragma unroll
+      for (int vb = 0; vb < 4; ++vb) {
+        f32x4 r;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) r[c] = o[d][4 * vb + c] * il;
+        *reinterpret_cast<f32x4 *>(orow + 32 * d + 8 * vb) = r;
+      }
+  }
+}
+
 // ---- decode attention: RoPE + KV append + attention of one new token --------
 // Sum over aligned groups of N consecutive lanes (N = 8 or 16), in every lane.
 template <int N>
@@ -660,13 +892,23 @@ hipError_t launch_attn_t(const AttnArgs &a, hipStream_t st) {
   return hipGetLastError();
 }
 
+template <int HD, int GRP>
+hipError_t launch_prefill_t(const AttnArgs &a, hipStream_t st) {
+  constexpr int PB = 4 * (32 / GRP);
+  hipLaunchKernelGGL((attn_prefill_kernel<HD, GRP>), dim3((unsigned)((a.s + PB - 1) / PB), (unsigned)a.nkv),
+                     dim3(256), 0, st, a.q, a.kc, a.vc, a.out, a.s, a.nheads, a.nkv, a.posp,
+                     a.pos0, a.maxlen);
+  return hipGetLastError();
+}
+
 template <int HD>
 hipError_t launch_attn_hd(const AttnArgs &a, hipStream_t st) {
+  const bool mfma = a.s >= kPrefillMinRows;
   switch (a.nheads / a.nkv) {
-    case 1: return launch_attn_t<HD, 1>(a, st);
-    case 2: return launch_attn_t<HD, 2>(a, st);
-    case 4: return launch_attn_t<HD, 4>(a, st);
-    case 8: return launch_attn_t<HD, 8>(a, st);
+    case 1: return mfma ? launch_prefill_t<HD, 1>(a, st) : launch_attn_t<HD, 1>(a, st);
+    case 2: return mfma ? launch_prefill_t<HD, 2>(a, st) : launch_attn_t<HD, 2>(a, st);
+    case 4: return mfma ? launch_prefill_t<HD, 4>(a, st) : launch_attn_t<HD, 4>(a, st);
+    case 8: return mfma ? launch_prefill_t<HD, 8>(a, st) : launch_attn_t<HD, 8>(a, st);
     default: return hipErrorInvalidValue;
   }
 }

@@ -808,7 +808,7 @@ int q8_rope_kv(q8_ctx *ctx, q8_buf *a, uint64_t oq_f32, uint64_t ok_f32, uint64_
 }
 
 uint64_t q8_attention_scratch_floats(int64_t s, int nheads, int head_dim, int64_t maxlen) {
-  if (s < 0 || nheads <= 0 || head_dim <= 0 || maxlen <= 0) return 0;
+  if (s < 0 || nheads <= 0 || head_dim <= 0 || maxlen <= 0 || s >= q8::kPrefillMinRows) return 0;
   return (uint64_t)s * nheads * attn_nsplit(maxlen) * (uint64_t)(head_dim + 2);
 }
 

@@ -216,7 +216,8 @@ class Q8Llama:
             # reset after every layer), the head, and room for one captured
             # decode step besides a forward pass
             s = max(1, int(max_prefill))
-            att = q8hip.attention_scratch_floats(min(s, self.ATT_ROWS), cfg.n_heads, cfg.head_dim,
+            # (attention scratch grows with the rows up to 15 and is 0 from 16)
+            att = q8hip.attention_scratch_floats(min(s, 15), cfg.n_heads, cfg.head_dim,
                                                  self.maxlen)
             layer = s * (4 * H + 3 * QD + 3 * KVD + 2 * I) + att    # incl. q/k norm outputs
             one = 2 * s * H + layer + H + cfg.vocab + 64
@@ -296,8 +297,6 @@ class Q8Llama:
         self.w.buf.upload(host, 2 * off_u16)
 
     # ---- layer runner (run_layer_q8) ---------------------------------------
-    ATT_ROWS = 256      # query rows per attention call (bounds the scratch)
-
     def linear(self, ox: int, s: int, m: int, owt: int, n: int) -> int:
         oy = self.a.alloc(s * n)
         q8hip.linear(self.ctx, self.w.buf, owt, self.a.buf, ox, oy, s, m, n, self.G, self.scale)
@@ -340,14 +339,10 @@ class Q8Llama:
         else:
             q8hip.rope_kv(ctx, a.buf, oq, okk, ov, self.oinv, self.kv, self.okc[L], self.ovc[L],
                           self.maxlen, s, pos0, cfg.n_heads, cfg.n_kv, cfg.head_dim, pb, 0)
-            rows = min(s, self.ATT_ROWS)
-            osc = a.alloc(q8hip.attention_scratch_floats(rows, cfg.n_heads, cfg.head_dim,
+            osc = a.alloc(q8hip.attention_scratch_floats(s, cfg.n_heads, cfg.head_dim,
                                                          self.maxlen))
-            for r0 in range(0, s, rows):
-                r = min(rows, s - r0)
-                q8hip.attention(ctx, a.buf, oq + r0 * QD, self.kv, self.okc[L], self.ovc[L],
-                                self.maxlen, oao + r0 * QD, osc, r, pos0 + r0, cfg.n_heads,
-                                cfg.n_kv, cfg.head_dim, pb, 0)
+            q8hip.attention(ctx, a.buf, oq, self.kv, self.okc[L], self.ovc[L], self.maxlen, oao,
+                            osc, s, pos0, cfg.n_heads, cfg.n_kv, cfg.head_dim, pb, 0)
         oo = self.linear(oao, s, QD, lo.o, H)
         if oh is None:
             oh = a.alloc(s * H)

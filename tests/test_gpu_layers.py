@@ -116,8 +116,11 @@ def test_rope_kv_append(ctx, head_dim):
         b.free()
 
 
-@pytest.mark.parametrize("head_dim,nh,nkv", [(64, 32, 8), (128, 32, 8), (64, 8, 8), (128, 16, 2)])
-@pytest.mark.parametrize("s,pos0", [(1, 0), (1, 63), (1, 64), (1, 1023), (5, 100), (3, 1021)])
+@pytest.mark.parametrize("head_dim,nh,nkv", [(64, 32, 8), (128, 32, 8), (64, 8, 8), (128, 16, 2),
+                                              (64, 16, 8)])
+@pytest.mark.parametrize("s,pos0", [(1, 0), (1, 63), (1, 64), (1, 1023), (5, 100), (3, 1021),
+                                     (15, 9), (16, 0), (37, 5), (200, 700), (130, 894),
+                                     (300, 0)])
 def test_attention(ctx, head_dim, nh, nkv, s, pos0):
     say("attention", head_dim, nh, nkv, s, pos0)
     rng = np.random.default_rng(2)
@@ -143,6 +146,37 @@ def test_attention(ctx, head_dim, nh, nkv, s, pos0):
                     posbuf=pb, opos_i32=0)
     assert np.array_equal(get(a, oy, (s, qd)), y)
     for b in (a, kv, pb):
+        b.free()
+
+
+@pytest.mark.parametrize("head_dim,nh,nkv", [(128, 32, 8), (64, 8, 8)])
+def test_attention_prompt_rows_any_q_scale(ctx, head_dim, nh, nkv):
+    """The multi-row (s >= 16) path splits q into binary16 hi + lo after a
+    per-column power-of-two scaling: rows of q from 1e-30 to 30 in size
+    (a sharply peaked softmax at the top; beyond that f32 scores themselves
+    drift from float64) and an all-zero row (uniform weights) stay within
+    max-rel-err 1e-5 of float64, row by row."""
+    say("attention q scales", head_dim, nh, nkv)
+    rng = np.random.default_rng(5)
+    maxlen, s, pos0 = 512, 48, 40
+    qd, kvd = nh * head_dim, nkv * head_dim
+    kc = (rng.standard_normal((maxlen, kvd)) * 0.7).astype(np.float16)
+    vc = rng.standard_normal((maxlen, kvd)).astype(np.float16)
+    q = rng.standard_normal((s, qd))
+    scales = np.array([1e-30, 1e-7, 1e-3, 0.05, 1.0, 7.0, 30.0, 0.0])
+    q = (q * scales[np.arange(s) % len(scales)][:, None]).astype(np.float32)
+    kv = ctx.alloc(2 * 2 * maxlen * kvd)
+    kv.upload(np.concatenate([kc.reshape(-1), vc.reshape(-1)]))
+    assert q8hip.attention_scratch_floats(s, nh, head_dim, maxlen) == 0
+    a = arena(ctx, 2 * s * qd)
+    put(a, 0, q)
+    q8hip.attention(ctx, a, 0, kv, 0, maxlen * kvd, maxlen, s * qd, 0, s, pos0, nh, nkv, head_dim)
+    y = get(a, s * qd, (s, qd))
+    ref = mo.attention(q.astype(np.float64), kc.astype(np.float64), vc.astype(np.float64), pos0,
+                       nh, nkv, head_dim)
+    for i in range(s):
+        assert max_rel_err(y[i], ref[i]) <= 1e-5, (i, scales[i % len(scales)])
+    for b in (a, kv):
         b.free()
 
 
