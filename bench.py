@@ -478,7 +478,7 @@ def run_e2e_8b(B: Bench, prompt: int = 2048, gen: int = 256):
         "data": "synthetic (random-init N(0,0.02) bf16 weights packed on GPU, norms ~1; "
                 "random prompt ids, seed 3)",
         "config": {"workload": f"{cfg.name} end to end: prefill {prompt} ids (7 Q8 GEMMs per "
-                               "layer on MFMA with f32 activations as two bf16 terms, RoPE + "
+                               "layer as f16-MFMA dequant-GEMMs, RoPE + "
                                "fp16 KV append, causal attention), then "
                                f"{gen} greedy steps of the captured decode graph",
                    "layout": f"G={G} {scale} scales", "batch": 1,
@@ -583,7 +583,7 @@ def run_prefill(B: Bench, cfg=LLAMA_1B, M=512):
     return {
         "metric": "Q8 prefill GEMM TFLOP/s (% of dense bf16 MFMA peak), Llama-3.2-1B M=512",
         "value": round(tflops, 2), "unit": "TFLOP/s", "ms_per_step": round(ms, 4),
-        "higher_is_better": True, "dtype": "bf16xint8->f32", "data": "synthetic",
+        "higher_is_better": True, "dtype": "f16(q*s) x f16(x) -> f32", "data": "synthetic",
         "config": {"workload": f"{cfg['name']} prefill linears, M={M} bf16 activations, "
                                f"{cfg['layers']} layers x 7 projections ({len(shapes)} GEMMs)",
                    "layout": f"G={G} {scale} scales", "flops_per_step": flops,

@@ -114,16 +114,21 @@ int q8_quantize_pack(q8_ctx *ctx, q8_buf *src, uint64_t src_off, int src_dtype,
  * at f32 offset oy of the activation arena `a`, and W's packed rows at u16
  * offset owt of the weight arena `w` -- the k_mm_q8 / mm_q8_op contract
  * (src/llama_q8.mojo:54-93,124-141).  y must not overlap x.  The caller
- * allocates y (Acts.alloc), as mm_q8_op does. */
+ * allocates y (Acts.alloc), as mm_q8_op does.  Rows s < 32 run f32-exact
+ * products (GEMV, or MFMA on two bf16 terms of x); s >= 32 runs the
+ * dequant-GEMM on f16 MFMA (binary16 x rows after a power-of-two scaling,
+ * binary16 q * s), whose max-rel-err stays near 2e-4. */
 int q8_linear(q8_ctx *ctx, q8_buf *w, uint64_t owt_u16, q8_buf *a,
               uint64_t ox_f32, uint64_t oy_f32, int64_t s, int64_t m, int64_t n,
               int G, int scale_dtype);
 
 /* Prefill variant with bf16 activations: x bf16 [s, m] at element offset ox
- * of buffer x, y f32 [s, n] at f32 offset oy of buffer y.  Runs on bf16 MFMA
- * with exact int8 codes and a per-group f32 rescale.  No reference
- * counterpart (the reference is W8A32 only); it is the M = 512 bf16-
- * activation prefill case. */
+ * of buffer x, y f32 [s, n] at f32 offset oy of buffer y.  Runs as the
+ * dequant-GEMM on f16 MFMA: each x row scaled by a power of two into
+ * binary16 (exact for bf16 values), weights q * s rounded once to binary16
+ * (twice with f32 scales), f32 accumulation; max-rel-err stays near 2e-4.
+ * No reference counterpart (the reference is W8A32 only); it is the
+ * M = 512 bf16-activation prefill case. */
 int q8_linear_bf16act(q8_ctx *ctx, q8_buf *w, uint64_t owt_u16, q8_buf *x,
                       uint64_t ox_bf16, q8_buf *y, uint64_t oy_f32, int64_t s,
                       int64_t m, int64_t n, int G, int scale_dtype);

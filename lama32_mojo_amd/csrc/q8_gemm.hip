@@ -1,332 +1,377 @@
-// q8_gemm.hip -- prefill-path Q8 GEMM on gfx950 bf16 MFMA.
+// q8_gemm.hip -- prefill-path Q8 GEMM on gfx950 f16 MFMA, weights
+// dequantized in registers.
 //
-// y[i, j] = sum_g scale[j, g] * sum_{k in g} x[i, k] * q[j, k]
-// (k_mm_q8's arithmetic, src/llama_q8.mojo:73-84: unscaled dot per group,
-// one scale multiply per group) computed as a tiled GEMM on
-// v_mfma_f32_32x32x16_bf16:
-//   * |q| <= 127 is exact in bf16 and a bf16 x bf16 product is exact in the
-//     f32 accumulator, so each group's partial dot is exact up to f32
-//     accumulation; every group's partial starts from 0 in its own MFMA
-//     accumulator and is folded into the result with one v_fma per output;
-//   * f32 activations (the W8A32 path with many rows) are split into
-//     hi = bf16(x) and lo = bf16(x - hi) and run as two MFMAs; the residual
-//     error is below 2^-17 |x|.
+// y[i, j] = sum_k x[i, k] * (q[j, k] * scale[j, k / G])
+// (k_mm_q8's product, src/llama_q8.mojo:73-84) as a dequant-GEMM on
+// v_mfma_f32_32x32x16_f16, in two launches:
+//   1. act16_kernel: each activation row is scaled by a power of two 2^-e_i
+//      so that its largest |x| lies in [2^14, 2^15), rounded to binary16
+//      (exact for bf16 input: binary16 has three more mantissa bits and the
+//      scaled row sits inside its normal range), and written with 2^e_i;
+//   2. gemm_kernel: each lane turns its column's int8 codes into binary16
+//      weights q * s in registers and feeds them to the MFMA as the B
+//      operand; the activations come through LDS as the A operand; the f32
+//      accumulators need no per-group rescale, and each output is multiplied
+//      once by its row's 2^e_i.
+// Rounding: the binary16 weight carries one rounding of q * s (two with f32
+// scales, which are rounded to binary16 first), i.e. a relative error below
+// 2^-11; products and sums are f32.
 //
-// Cost model.  The per-group fold is one non-packed f32 FMA per output and
-// group, i.e. MACs / G FMAs: at G = 32 the VALU needs as many cycles for the
-// fold as the MFMA pipe needs for the products (16 FMA lanes vs 512 MACs per
-// clock and SIMD).  Everything else on the VALU is kept small: the codes of a
-// weight fragment are converted once and reused by all row tiles of a wave,
-// and all addressing is 32-bit buffer offsets whose range check also zero-fills
-// the ragged edges (no clamps in the loop).
+// Cost model (per SIMD: 512 MFMA MACs or 16 VALU lanes per clock).  A weight
+// costs 1.75 VALU operations (one xor per 4 codes, then per 2 codes a v_perm
+// that builds binary16 1024 + (q + 128), a packed subtract of 1152 and a
+// packed multiply by the scale) and is used by BM rows; the activations
+// cost no VALU work in the loop.  At BM = 128 the VALU needs ~0.44 clocks
+// per MFMA clock.
 //
-// Work decomposition (one 512-thread workgroup per BM x 128 output tile):
-//   * the 8 waves form 4 column slices of 32 outputs x 2 K-parities; wave
-//     (p, h) accumulates columns p*32.. over the 64-code K slots of parity h,
-//     so each SIMD runs two independent instruction streams whose MFMA and
-//     VALU work co-issue; the two parities meet in LDS at the end;
-//   * a wave's weight codes never touch LDS: lane l owns output column
-//     l % 32 and loads its 32 codes of a slot straight from memory into
-//     registers (two dwordx4), converted to bf16 in registers.  The MFMA K
-//     order inside a slot is permuted so each lane's codes come in two
-//     16-byte chunks and no k-step straddles a quantization group; the
-//     activation fragments read from LDS use the same permutation;
-//   * activations are staged through double-buffered LDS, 128 k per step,
-//     loaded one step ahead; the weight codes run in a register ring PB
-//     slots ahead, with the loop unrolled so ring slots are compile-time
-//     registers (a runtime slot index would force the loads to complete
-//     immediately).
+// Work decomposition (one workgroup of 8 waves per BM x BN output tile,
+// BN = 128 * TN): the waves form 4 column groups of 32 * TN outputs x 2
+// K-parities; wave (p, h) owns TN column tiles of 32 and all BM rows and
+// takes the second 64-code slot of each 128-code iteration when h = 1; the
+// two parities meet in LDS at the end.  Per iteration the workgroup stages
+// three tiles through registers into double-buffered LDS, each loaded with
+// whole 128-byte lines: activations (BM x 128 binary16), codes (BN rows x
+// 128 bytes, 16-byte chunks XOR-swizzled by row) and, every other
+// iteration, the scales of the next two.  A lane then reads its column's
+// codes and scales from LDS and dequantizes them in registers as the MFMA
+// B operand; the MFMA K order inside a slot is permuted so each lane's
+// codes come in two 16-byte chunks and no k-step straddles a quantization
+// group (the A fragments read from LDS use the same permutation).
 #include "q8_device.h"
 #include "q8_launch.h"
 
 namespace q8 {
 namespace {
 
-constexpr int NT = 512;        // 8 waves
-constexpr int BN = 128;        // 4 column slices of 32
-constexpr int KT = 128;        // k per iteration = 2 slots of 64 codes
-constexpr int LDA = KT + 8;    // bf16 per LDS row (16-byte pad)
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 
-// Raw scale bits of 4 consecutive 64-code slots (one load period), and the
-// scales of slot j of a period.  A slot holds 64 / G scales, so a period is
-// 8 (G=64, f16), 16 (G=64 f32 or G=32 f16) or 32 (G=32, f32) bytes, loaded
-// with naturally aligned loads: the scale section of a row is 16-byte
-// aligned (checked by the host) and periods start at multiples of 4 slots.
-template <int G, int KIND> struct ScalePeriod {
-  static constexpr int slot_bytes = (64 / G) * ScaleTraits<KIND>::bytes;
-  static constexpr int bytes = 4 * slot_bytes;
-  static constexpr int words = bytes / 4;
-  uint32_t wd[words];
-  __device__ __forceinline__ void load(rsrc_t r, uint32_t off) {
-    if constexpr (bytes == 8) {
-      const u32x2 v = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, 0));
-      wd[0] = v.x; wd[1] = v.y;
-    } else {
+constexpr int KT = 128;        // k per iteration = two 64-code slots
+constexpr int kWaves = 8;      // waves per workgroup: 8 (two K parities) or 4
+constexpr int LDA = KT + 8;    // halves per LDS row (16-byte pad)
+
+// ---- 1. activation rows to binary16 ----------------------------------------
+template <bool XF32>
+__global__ __launch_bounds__(256) void act16_kernel(const void *__restrict__ xv, int64_t m,
+                                                    uint16_t *__restrict__ x16,
+                                                    float *__restrict__ rf) {
+  __shared__ float red[4];
+  const int64_t r = blockIdx.x;
+  const int tid = threadIdx.x;
+  // 8 consecutive values per step (m is a multiple of 8)
+  auto load8 = [&](int64_t k, float (&v)[8]) {
+    if constexpr (XF32) {
+      const f32x4 *p = reinterpret_cast<const f32x4 *>(static_cast<const float *>(xv) + r * m + k);
+      const f32x4 a = p[0], b = p[1];
 #pragma unroll
-      for (int i = 0; i < words / 4; ++i) {
-        const u32x4 v = bload16(r, off + 16 * i);
-        wd[4 * i] = v.x; wd[4 * i + 1] = v.y; wd[4 * i + 2] = v.z; wd[4 * i + 3] = v.w;
+      for (int c = 0; c < 4; ++c) {
+        v[c] = a[c];
+        v[4 + c] = b[c];
+      }
+    } else {
+      const u32x4 d = *reinterpret_cast<const u32x4 *>(static_cast<const uint16_t *>(xv) + r * m + k);
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        v[2 * c] = __builtin_bit_cast(float, d[c] << 16);
+        v[2 * c + 1] = __builtin_bit_cast(float, d[c] & 0xffff0000u);
       }
     }
+  };
+  float mx = 0.0f;
+  for (int64_t k = 8 * tid; k < m; k += 8 * 256) {
+    float v[8];
+    load8(k, v);
+#pragma unroll
+    for (int c = 0; c < 8; ++c) mx = fmaxf(mx, fabsf(v[c]));
   }
-  // scale gi (0 .. 64/G - 1) of slot j (0..3) of the period
-  __device__ __forceinline__ float get(int j, int gi) const {
-    if constexpr (G == 64 && KIND == SCALE_F16)
-      return f16_bits_to_f32((uint16_t)(wd[j / 2] >> (16 * (j % 2))));
-    else if constexpr (G == 64)
-      return __builtin_bit_cast(float, wd[j]);
-    else if constexpr (KIND == SCALE_F16)
-      return f16_bits_to_f32((uint16_t)(wd[j] >> (16 * gi)));
-    else
-      return __builtin_bit_cast(float, wd[2 * j + gi]);
+  mx = wave_max(mx);
+  if ((tid & 63) == 0) red[tid >> 6] = mx;
+  __syncthreads();
+  mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  // largest |x| * 2^-e in [2^14, 2^15); rows of zeros, inf or NaN keep e = 0
+  int e = 0;
+  if (mx > 0.0f && mx <= 3.4028235e38f) {
+    e = (int)((__builtin_bit_cast(uint32_t, mx) >> 23) & 255u) - 127 - 14;
+    if (mx < 1.17549435e-38f) e = -126;       // subnormal maximum: as far as 2^126 goes
+    e = e < -126 ? -126 : e;
   }
-};
+  for (int64_t k = 8 * tid; k < m; k += 8 * 256) {
+    float v[8];
+    load8(k, v);
+    u32x4 o;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const f16x2 hv = {(_Float16)__builtin_ldexpf(v[2 * c], -e),
+                        (_Float16)__builtin_ldexpf(v[2 * c + 1], -e)};
+      o[c] = __builtin_bit_cast(uint32_t, hv);
+    }
+    *reinterpret_cast<u32x4 *>(x16 + r * m + k) = o;
+  }
+  if (tid == 0) rf[r] = __builtin_ldexpf(1.0f, e);
+}
 
-template <int G, int KIND, bool XF32, int BM, int PB>
-__global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(2, 2)))
-void gemm_kernel(const uint8_t *__restrict__ w, int64_t row_bytes, const void *__restrict__ xv,
-                 float *__restrict__ y, int64_t s, int64_t m, int64_t n, int nit,
-                 float *__restrict__ ws) {
+// ---- 2. the GEMM --------------------------------------------------------------
+// Eight codes (two dwords, k order) times one binary16 scale pair.
+__device__ __forceinline__ f16x8 dequant8(uint32_t d0, uint32_t d1, f16x2 s2) {
+  const f16x2 off = {(_Float16)1152.0f, (_Float16)1152.0f};
+  const uint32_t x0 = d0 ^ 0x80808080u, x1 = d1 ^ 0x80808080u;   // q + 128 per byte
+  // binary16 0x64hh = 1024 + hh exactly; minus 1152 gives q exactly
+  const f16x2 a = (__builtin_bit_cast(f16x2, __builtin_amdgcn_perm(0x64646464u, x0, 0x04010400u)) - off) * s2;
+  const f16x2 b = (__builtin_bit_cast(f16x2, __builtin_amdgcn_perm(0x64646464u, x0, 0x04030402u)) - off) * s2;
+  const f16x2 c = (__builtin_bit_cast(f16x2, __builtin_amdgcn_perm(0x64646464u, x1, 0x04010400u)) - off) * s2;
+  const f16x2 d = (__builtin_bit_cast(f16x2, __builtin_amdgcn_perm(0x64646464u, x1, 0x04030402u)) - off) * s2;
+  return f16x8{a.x, a.y, b.x, b.y, c.x, c.y, d.x, d.y};
+}
+
+template <int G, int KIND, int BM, int TN, int NW>
+__global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(NW / 4, NW / 4)))
+void gemm_kernel(const uint8_t *__restrict__ w, int64_t row_bytes,
+                   const uint16_t *__restrict__ x16, const float *__restrict__ rf,
+                   float *__restrict__ y, int64_t s, int64_t m, int64_t n, int nit,
+                   float *__restrict__ ws) {
   // blockIdx.z selects a K range of nit iterations (split-K): with
   // gridDim.z == 1 y is written directly, otherwise split z writes its
   // partial sums to ws[z] and splitk_reduce_kernel adds them up.
+  constexpr int NT = 64 * NW;                 // threads
+  constexpr int NP = NW / 4;                  // K parities among the waves (1 or 2)
   constexpr int SB = ScaleTraits<KIND>::bytes;
   constexpr int TM = BM / 32;                 // 32-row MFMA tiles per wave
-  constexpr int XB = XF32 ? 4 : 2;            // bytes per activation
-  constexpr int AU = BM * KT / 8 / NT;        // 8-activation chunks per thread
-  constexpr int NLDS = XF32 ? 2 : 1;
-  typedef ScalePeriod<G, KIND> SP;
-  static_assert(PB == 4, "scale loads cover periods of 4 slots");
-  __shared__ __attribute__((aligned(16))) uint16_t As[2][NLDS][BM * LDA];
+  constexpr int BN = 128 * TN;
+  constexpr int AU = BM * KT / 8 / NT;        // 8-half A chunks per thread
+  constexpr int NG = 64 / G;                  // groups per 64-code slot
+  constexpr int SPB = 2 * (KT / G) * SB;      // scale bytes of a row per 2 iterations
+  constexpr int SDW = BN * SPB / 4;           // ... as dwords per block
+  constexpr int SU = (SDW + NT - 1) / NT;     // ... per thread
+  constexpr int CU = BN * KT / 16 / NT;       // 16-byte code chunks per thread
+  __shared__ __attribute__((aligned(16))) uint16_t As[2][BM * LDA];
+  __shared__ __attribute__((aligned(16))) uint8_t Bs[2][BN * KT];    // codes, swizzled rows
+  __shared__ __attribute__((aligned(16))) uint8_t Ss[2][BN * SPB];   // scales of 2 iterations
+  __shared__ float rfs[BM];
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int p = wid & 3, h = wid >> 2;
+  const int p = wid & 3, h0 = wid >> 2;
   const int lr = lane & 31, lh = lane >> 5;
   const int64_t n0 = (int64_t)blockIdx.x * BN, m0 = (int64_t)blockIdx.y * BM;
-  // This split covers codes [kbase, kbase + nit * KT).  Wave parity h takes
-  // K half h of it, starting at khalf; iteration it of the wave covers the
-  // 64-code slot at khalf + 64 it (and the LDS tile of an iteration holds
-  // half 0's 64 columns, then half 1's).
+  // This split covers codes [kbase, kbase + nit * KT); iteration it covers
+  // the 128 codes from kbase + KT it: with 8 waves parity h0 takes the
+  // 64-code slot at 64 h0, with 4 waves each wave takes both slots.
   const int64_t kbase = (int64_t)blockIdx.z * nit * KT;
-  const int64_t khalf = kbase + (int64_t)h * nit * 64;
-  const int64_t mh = m - khalf;                       // codes of the row from khalf on
 
-  // Weights: this block's (at most) 128 packed rows.  Lane offsets are
-  // relative to the block's first row; a row past n lies past the resource.
+  // Weights: this block's (at most) BN packed rows; a row past n lies past
+  // the resource (its loads read zeros).
   const int64_t nrows = n - n0 < BN ? n - n0 : BN;
   const rsrc_t wr = make_rsrc(w + n0 * row_bytes, (uint32_t)(nrows * row_bytes));
-  const uint32_t wrow = (uint32_t)((p * 32 + lr) * row_bytes);
-  // Codes of one 64-code slot held by a lane, as two 16-code chunks.  The
-  // MFMA K order inside a slot is chosen so each k-step of 16 stays inside
-  // one quantization group: k-step t of lane half lh reads codes
-  //   G=64: [32 lh + 8 t, +8)                       (chunks at 32 lh, 32 lh + 16)
-  //   G=32: [32 (t / 2) + 16 lh + 8 (t % 2), +8)     (chunks at 16 lh, 32 + 16 lh)
-  // so t = 0..1 covers the slot's first group of 32 and t = 2..3 its second.
+  // Code tiles: BN rows x 128 codes per iteration, 8 threads per 128-byte
+  // row (coalesced), staged through registers.  The 16-byte chunk c of row
+  // r sits at LDS chunk c ^ ((r >> 1) & 7): the 16 rows one ds_read_b128
+  // pass reads then fall on 16 different bank groups.
+  auto load_codes = [&](u32x4 *dst, int it) {
+#pragma unroll
+    for (int u = 0; u < CU; ++u) {
+      const int c = tid + NT * u, r = c >> 3;
+      dst[u] = bload16(wr, (uint32_t)(r * row_bytes + (m / G) * SB + kbase + KT * it + 16 * (c & 7)));
+    }
+  };
+  auto store_codes = [&](const u32x4 *src, int buf) {
+#pragma unroll
+    for (int u = 0; u < CU; ++u) {
+      const int c = tid + NT * u, r = c >> 3;
+      *reinterpret_cast<u32x4 *>(&Bs[buf][r * KT + 16 * ((c & 7) ^ ((r >> 1) & 7))]) = src[u];
+    }
+  };
+  // Scale tiles: BN rows x SPB bytes per period of 2 iterations, as dwords
+  // (thread t takes dwords t, t + NT, ... of the [BN][SPB / 4] tile).
+  auto load_scales = [&](uint32_t *dst, int per) {
+#pragma unroll
+    for (int u = 0; u < SU; ++u) {
+      const int i = tid + NT * u;
+      if (i < SDW)
+        dst[u] = __builtin_amdgcn_raw_buffer_load_b32(
+            wr, (uint32_t)((i / (SPB / 4)) * row_bytes + (kbase + 2 * KT * per) / G * SB +
+                           4 * (i % (SPB / 4))), 0, 0);
+    }
+  };
+  auto store_scales = [&](const uint32_t *src, int buf) {
+#pragma unroll
+    for (int u = 0; u < SU; ++u) {
+      const int i = tid + NT * u;
+      if (i < SDW) *reinterpret_cast<uint32_t *>(&Ss[buf][4 * i]) = src[u];
+    }
+  };
+  // This lane's column within the block for tile t
+  auto bcol = [&](int t) { return p * 32 * TN + 32 * t + lr; };
+  // k-step ks of lane half lh reads codes (offsets within the slot)
+  //   G=64: [32 lh + 8 ks, +8)                      (chunks at 32 lh, 32 lh + 16)
+  //   G=32: [32 (ks / 2) + 16 lh + 8 (ks % 2), +8)   (chunks at 16 lh, 32 + 16 lh)
+  // so for G = 32 k-steps 0..1 are the slot's first group and 2..3 its second.
   const int chunk0 = G == 64 ? 32 * lh : 16 * lh;
   const int chunk1 = G == 64 ? 32 * lh + 16 : 32 + 16 * lh;
-  const uint32_t vcodes = wrow + (uint32_t)((m / G) * SB + khalf);
-  const uint32_t vscale = wrow + (uint32_t)(khalf / G * SB);
-  // Codes past the row end read the next row (finite codes that meet zero
-  // activations) or lie past the resource; scales past the last group are
-  // replaced by 0 below.
-  auto load_b = [&](u32x4 (&q)[2], int it) {
-    q[0] = bload16(wr, vcodes + it * 64 + chunk0);
-    q[1] = bload16(wr, vcodes + it * 64 + chunk1);
-  };
 
-  // Activations: this block's (at most) BM rows.  Chunk u of a thread is
-  // row c / 16, LDS columns 8 (c % 16) .. +8 (c = tid + NT u); LDS columns
-  // [0, 64) come from K half 0 and [64, 128) from K half 1.  A row past s
-  // lies past the resource, a column past m is sent past it explicitly.
+  // Activations (binary16 rows from act16_kernel): this block's (at most)
+  // BM rows, 128 k per iteration; chunk u of a thread is row c / 16, k
+  // 8 (c % 16) .. +8 (c = tid + NT u).  A row past s lies past the
+  // resource, a column past m is sent past it explicitly.
   const int64_t arows = s - m0 < BM ? s - m0 : BM;
-  const rsrc_t xr = make_rsrc(reinterpret_cast<const uint8_t *>(xv) + m0 * m * XB,
-                              (uint32_t)(arows * m * XB));
+  const rsrc_t xr = make_rsrc(x16 + m0 * m, (uint32_t)(arows * m * 2));
   const int64_t mk = m - kbase;
   uint32_t vx[AU];
-  int akc[AU], akk[AU];
+  int akc[AU];
 #pragma unroll
   for (int u = 0; u < AU; ++u) {
     const int c = tid + NT * u;
     akc[u] = (c % (KT / 8)) * 8;
-    akk[u] = akc[u] < 64 ? akc[u] : nit * 64 + akc[u] - 64;   // code offset within the split
-    vx[u] = (uint32_t)(((c / (KT / 8)) * m + kbase + akk[u]) * XB);
+    vx[u] = (uint32_t)(((c / (KT / 8)) * m + kbase + akc[u]) * 2);
   }
   auto load_a = [&](u32x4 *dst, int it) {
 #pragma unroll
     for (int u = 0; u < AU; ++u) {
-      const uint32_t off = it * 64 + akk[u] < mk ? vx[u] + it * 64 * XB : kOutOfRange;
-      if constexpr (!XF32) {
-        dst[u] = bload16(xr, off);
-      } else {
-        dst[2 * u] = bload16(xr, off);
-        dst[2 * u + 1] = bload16(xr, off + 16);
-      }
+      const uint32_t off = KT * it + akc[u] < mk ? vx[u] + KT * it * 2 : kOutOfRange;
+      dst[u] = bload16(xr, off);
     }
   };
   auto store_a = [&](const u32x4 *src, int buf) {
 #pragma unroll
     for (int u = 0; u < AU; ++u) {
       const int row = (tid + NT * u) / (KT / 8);
-      if constexpr (!XF32) {
-        *reinterpret_cast<u32x4 *>(&As[buf][0][row * LDA + akc[u]]) = src[u];
-      } else {
-        const uint32_t d[8] = {src[2 * u].x, src[2 * u].y, src[2 * u].z, src[2 * u].w,
-                               src[2 * u + 1].x, src[2 * u + 1].y, src[2 * u + 1].z,
-                               src[2 * u + 1].w};
-        uint32_t hi[4], lo[4];
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const float f0 = __builtin_bit_cast(float, d[2 * e]);
-          const float f1 = __builtin_bit_cast(float, d[2 * e + 1]);
-          const uint32_t h0 = bf16_rne(f0), h1 = bf16_rne(f1);
-          const uint32_t l0 = bf16_rne(f0 - __builtin_bit_cast(float, h0 << 16));
-          const uint32_t l1 = bf16_rne(f1 - __builtin_bit_cast(float, h1 << 16));
-          hi[e] = h0 | (h1 << 16);
-          lo[e] = l0 | (l1 << 16);
-        }
-        *reinterpret_cast<u32x4 *>(&As[buf][0][row * LDA + akc[u]]) = u32x4{hi[0], hi[1], hi[2], hi[3]};
-        *reinterpret_cast<u32x4 *>(&As[buf][NLDS - 1][row * LDA + akc[u]]) =
-            u32x4{lo[0], lo[1], lo[2], lo[3]};
-      }
+      *reinterpret_cast<u32x4 *>(&As[buf][row * LDA + akc[u]]) = src[u];
     }
   };
+  // activation column of k-step ks (same permutation as the codes)
+  auto acol = [&](int h, int ks) {
+    return 64 * h + (G == 64 ? 32 * lh + 8 * ks : 32 * (ks >> 1) + 16 * lh + 8 * (ks & 1));
+  };
 
-  f32x16 acc[TM];
+  if (tid < BM) rfs[tid] = tid < arows ? rf[m0 + tid] : 0.0f;
+
+  f32x16 acc[TM][TN];
 #pragma unroll
   for (int i = 0; i < TM; ++i)
 #pragma unroll
-    for (int v = 0; v < 16; ++v) acc[i][v] = 0.0f;
-
-  // units of work per slot: TH row tiles x one group of NG = 64 / G; a
-  // group is KS = G / 16 k-steps
-  constexpr int TH = TM < 2 ? TM : 2;
-  constexpr int NG = 64 / G, KS = G / 16;
-  constexpr int FPER = 16 / KS;               // fold FMAs after each MFMA
-  f32x16 pq[TH];                              // partials of the unit awaiting its fold
+    for (int t = 0; t < TN; ++t)
 #pragma unroll
-  for (int i = 0; i < TH; ++i)
-#pragma unroll
-    for (int v = 0; v < 16; ++v) pq[i][v] = 0.0f;
-  float psc = 0.0f;
+      for (int v = 0; v < 16; ++v) acc[i][t][v] = 0.0f;
 
-  u32x4 qb[PB][2];
-  SP sp;                                      // scales of the current period
-  u32x4 ra[XF32 ? 2 * AU : AU];
-
-#pragma unroll
-  for (int q = 0; q < PB; ++q) load_b(qb[q], q);
-  sp.load(wr, vscale);
+  u32x4 ra[AU], rc[CU];
+  uint32_t rs[SU];
+  load_scales(rs, 0);
+  load_codes(rc, 0);
   load_a(ra, 0);
+  store_scales(rs, 0);
+  store_codes(rc, 0);
   store_a(ra, 0);
+  if (nit > 2) load_scales(rs, 1);
+  load_codes(rc, 1);
   load_a(ra, 1);
   __syncthreads();
 
-  for (int i0 = 0; i0 < nit; i0 += PB) {
-    // this period's scales, and the next period's in flight
-    SP spc = sp;
-    sp.load(wr, vscale + (i0 + PB) * SP::slot_bytes);
+  const f16x2 zero2 = {(_Float16)0.0f, (_Float16)0.0f};
+  for (int it = 0; it < nit; ++it) {
+    const uint8_t *bt = Bs[it & 1];
+    const uint8_t *st = Ss[(it >> 1) & 1];
+    const uint16_t *at = As[it & 1];
 #pragma unroll
-    for (int j = 0; j < PB; ++j) {
-      const int it = i0 + j;
-      const int buf = it & 1;
-      bf16x8_t bf[4];
-      bf[0] = codes_to_bf16(qb[j][0].x, qb[j][0].y);
-      bf[1] = codes_to_bf16(qb[j][0].z, qb[j][0].w);
-      bf[2] = codes_to_bf16(qb[j][1].x, qb[j][1].y);
-      bf[3] = codes_to_bf16(qb[j][1].z, qb[j][1].w);
-      // a slot (or its second G=32 group) past the row end meets zero
-      // activations; its scales (whatever bytes were read) are forced to 0
-      const float sc0 = it * 64 < mh ? spc.get(j, 0) : 0.0f;
-      const float sc1 = (G == 32 && it * 64 + 32 < mh) ? spc.get(j, 1) : 0.0f;
-      load_b(qb[j], it + PB);
-
-      // activation column of k-step t (same permutation as the codes)
-      auto acol = [&](int t) {
-        return 64 * h + (G == 64 ? 32 * lh + 8 * t : 32 * (t >> 1) + 16 * lh + 8 * (t & 1));
-      };
-      // Work of a slot comes in units (TH row tiles x one quantization
-      // group): the unit's MFMAs fill fresh partials tq, and the f32 fold of
-      // the previous unit's partials pq (acc += scale * pq) is interleaved
-      // between them, so the fold never waits on an MFMA that has just been
-      // issued and the MFMA pipe never waits on the fold.  The last unit of
-      // a slot is folded during the first unit of the next slot.
+    for (int hh = 0; hh < 2 / NP; ++hh) {
+      const int h = h0 + hh;
+      // the slot's codes and scales for each column tile; a slot (or its
+      // second G=32 group) past the row end meets zero activations and its
+      // scales (whatever bytes were read) are forced to 0
+      const int64_t k0 = kbase + KT * it + 64 * h;
+      u32x4 cq[TN][2];
+      f16x2 s2[TN][NG];
 #pragma unroll
-      for (int u = 0; u < (TM / TH) * NG; ++u) {
-        const int ib = (u / NG) * TH, g = u % NG;
-        const int pib = u == 0 ? TM - TH : ((u - 1) / NG) * TH;   // rows of pq
-        f32x16 tq[TH];
+      for (int t = 0; t < TN; ++t) {
+        const int r = bcol(t);
+        const int sw = (r >> 1) & 7;
+        cq[t][0] = *reinterpret_cast<const u32x4 *>(bt + r * KT + 16 * ((4 * h + (chunk0 >> 4)) ^ sw));
+        cq[t][1] = *reinterpret_cast<const u32x4 *>(bt + r * KT + 16 * ((4 * h + (chunk1 >> 4)) ^ sw));
+        const uint8_t *sp = st + r * SPB + (2 * (it & 1) + h) * NG * SB;
 #pragma unroll
-        for (int ks = 0; ks < KS; ++ks) {
-          const int t = g * KS + ks;
-          bf16x8_t af[TH], al[TH];
+        for (int g = 0; g < NG; ++g) {
+          _Float16 hs;
+          if constexpr (KIND == SCALE_F16)
+            hs = *reinterpret_cast<const _Float16 *>(sp + 2 * g);
+          else
+            hs = (_Float16)*reinterpret_cast<const float *>(sp + 4 * g);
+          s2[t][g] = k0 + g * G < m ? f16x2{hs, hs} : zero2;
+        }
+      }
+      // A fragments of k-step ks + 1 are read while k-step ks runs
+      f16x8 af[2][TM];
 #pragma unroll
-          for (int ii = 0; ii < TH; ++ii) {
-            const int ao = ((ib + ii) * 32 + lr) * LDA + acol(t);
-            af[ii] = *reinterpret_cast<const bf16x8_t *>(&As[buf][0][ao]);
-            if constexpr (XF32) al[ii] = *reinterpret_cast<const bf16x8_t *>(&As[buf][NLDS - 1][ao]);
-          }
+      for (int ii = 0; ii < TM; ++ii)
+        af[0][ii] = *reinterpret_cast<const f16x8 *>(&at[(ii * 32 + lr) * LDA + acol(h, 0)]);
 #pragma unroll
-          for (int ii = 0; ii < TH; ++ii) {
-            if (ks == 0) {
-              const f32x16 z = {};
-              tq[ii] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[ii], bf[t], z, 0, 0, 0);
-            } else {
-              tq[ii] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[ii], bf[t], tq[ii], 0, 0, 0);
-            }
-            if constexpr (XF32)
-              tq[ii] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(al[ii], bf[t], tq[ii], 0, 0, 0);
-            const int e0 = (ks * TH + ii) * FPER;
+      for (int ks = 0; ks < 4; ++ks) {
+        if (ks < 3) {
 #pragma unroll
-            for (int e = e0; e < e0 + FPER; ++e)
-              acc[pib + e / 16][e % 16] = __builtin_fmaf(psc, pq[e / 16][e % 16], acc[pib + e / 16][e % 16]);
-          }
+          for (int ii = 0; ii < TM; ++ii)
+            af[(ks + 1) & 1][ii] =
+                *reinterpret_cast<const f16x8 *>(&at[(ii * 32 + lr) * LDA + acol(h, ks + 1)]);
+        }
+        const int g = G == 64 ? 0 : ks >> 1;
+        f16x8 bq[TN];
+#pragma unroll
+        for (int t = 0; t < TN; ++t) {
+          const u32x4 &c = cq[t][ks >> 1];
+          bq[t] = (ks & 1) ? dequant8(c.z, c.w, s2[t][g]) : dequant8(c.x, c.y, s2[t][g]);
         }
 #pragma unroll
-        for (int ii = 0; ii < TH; ++ii) pq[ii] = tq[ii];
-        psc = g == 0 ? sc0 : sc1;
+        for (int ii = 0; ii < TM; ++ii)
+#pragma unroll
+          for (int t = 0; t < TN; ++t)
+            acc[ii][t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[ks & 1][ii], bq[t], acc[ii][t], 0, 0, 0);
       }
-      store_a(ra, buf ^ 1);
-      __syncthreads();
+    }
+    // stage the tiles of iteration it + 1 (period (it + 1) / 2 starts
+    // there when it is odd), then load those of it + 2
+    if (it + 1 < nit) {
+      store_codes(rc, (it + 1) & 1);
+      store_a(ra, (it + 1) & 1);
+      if (it & 1) store_scales(rs, ((it + 1) >> 1) & 1);
+    }
+    __syncthreads();
+    if (it + 2 < nit) {
+      load_codes(rc, it + 2);
       load_a(ra, it + 2);
     }
+    if ((it & 1) && it + 3 < nit) load_scales(rs, (it + 3) >> 1);
   }
 
-  // fold of the last unit
-#pragma unroll
-  for (int ii = 0; ii < TH; ++ii)
-#pragma unroll
-    for (int v = 0; v < 16; ++v)
-      acc[TM - TH + ii][v] = __builtin_fmaf(psc, pq[ii][v], acc[TM - TH + ii][v]);
-
-  // The two K parities of each column slice meet in LDS (reusing As).
-  float *red = reinterpret_cast<float *>(&As[0][0][0]);   // 4 * TM * 16 * 64 floats
+  // With two K parities, each column tile's parities meet in LDS (reusing
+  // As), one column tile at a time; each output is scaled by its row's 2^e.
+  float *red = reinterpret_cast<float *>(&As[0][0]);   // 4 * TM * 16 * 64 floats
   static_assert(4 * TM * 16 * 64 * 4 <= (int)sizeof(As), "reduction buffer too small");
-  __syncthreads();
-  if (h == 1) {
+  const int rows_left = (int)(s - m0 - lh * 4);
 #pragma unroll
-    for (int i = 0; i < TM; ++i)
+  for (int t = 0; t < TN; ++t) {
+    if constexpr (NP == 2) {
+      __syncthreads();
+      if (h0 == 1) {
 #pragma unroll
-      for (int v = 0; v < 16; ++v) red[((p * TM + i) * 16 + v) * 64 + lane] = acc[i][v];
-  }
-  __syncthreads();
-  const int64_t col = n0 + p * 32 + lr;
-  if (h == 0 && col < n) {
-    // D layout of v_mfma_f32_32x32x16: lane -> column lane % 32,
-    // element v -> row 8 (v / 4) + 4 (lane / 32) + v % 4.
-    float *out = (gridDim.z == 1 ? y : ws + (int64_t)blockIdx.z * s * n) + (m0 + lh * 4) * n + col;
-    const int rows_left = (int)(s - m0 - lh * 4);
+        for (int i = 0; i < TM; ++i)
 #pragma unroll
-    for (int i = 0; i < TM; ++i)
-#pragma unroll
-      for (int v = 0; v < 16; ++v) {
-        const int r = i * 32 + (v >> 2) * 8 + (v & 3);
-        if (r < rows_left)
-          out[(int64_t)r * n] = acc[i][v] + red[((p * TM + i) * 16 + v) * 64 + lane];
+          for (int v = 0; v < 16; ++v) red[((p * TM + i) * 16 + v) * 64 + lane] = acc[i][t][v];
       }
+      __syncthreads();
+    }
+    const int64_t col = n0 + bcol(t);
+    if (h0 == 0 && col < n) {
+      // D layout of v_mfma_f32_32x32x16: lane -> column lane % 32,
+      // element v -> row 8 (v / 4) + 4 (lane / 32) + v % 4.
+      float *out = (gridDim.z == 1 ? y : ws + (int64_t)blockIdx.z * s * n) + (m0 + lh * 4) * n + col;
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+          const int r = i * 32 + (v >> 2) * 8 + (v & 3);
+          float o = acc[i][t][v];
+          if constexpr (NP == 2) o += red[((p * TM + i) * 16 + v) * 64 + lane];
+          if (r < rows_left) out[(int64_t)r * n] = o * rfs[r + lh * 4];
+        }
+    }
   }
 }
-
 
 // y[i] = sum over splits z (in order) of ws[z][i]; four outputs per thread.
 __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float *__restrict__ ws,
@@ -347,58 +392,60 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float *__restr
   }
 }
 
-template <int G, int KIND, bool XF32, int BM>
-hipError_t launch_bm(const LinearArgs &a, hipStream_t st) {
-  constexpr int PB = 4;
+template <int G, int KIND, int BM, int TN, int NW>
+hipError_t launch_t(const LinearArgs &a, const uint16_t *x16, const float *rf, hipStream_t st) {
+  constexpr int BN = 128 * TN;
   const int64_t nit_all = (a.m + KT - 1) / KT;
   const int64_t gx = (a.n + BN - 1) / BN, gy = (a.s + BM - 1) / BM;
   // Split K when the output tiles alone leave CUs idle (256 CUs, one 8-wave
-  // workgroup each); every split keeps at least 2 ring periods of iterations.
+  // workgroup each); every split keeps at least 4 iterations.
   int64_t splits = 1;
   if (a.ws) {
-    while (gx * gy * splits * 2 <= 256 && (nit_all + 2 * splits - 1) / (2 * splits) >= 2 * PB &&
+    while (gx * gy * splits * 2 <= 256 && (nit_all + 2 * splits - 1) / (2 * splits) >= 4 &&
            2 * splits * a.s * a.n <= a.ws_floats)
       splits *= 2;
   }
   int64_t nit = (nit_all + splits - 1) / splits;
-  nit = (nit + PB - 1) / PB * PB;
-  dim3 grid((unsigned)gx, (unsigned)gy, (unsigned)splits), block(NT);
-  hipLaunchKernelGGL((gemm_kernel<G, KIND, XF32, BM, PB>), grid, block, 0, st, a.w, a.row_bytes,
-                     a.x, a.y, a.s, a.m, a.n, (int)nit, a.ws);
-  if (splits > 1) {
-    const int64_t count = a.s * a.n;
-    const int64_t threads = (count + 3) / 4;
-    hipLaunchKernelGGL(splitk_reduce_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0,
-                       st, a.ws, a.y, count, (int)splits);
-  }
+  nit = (nit + 1) / 2 * 2;                    // whole scale periods of 2 iterations
+  dim3 grid((unsigned)gx, (unsigned)gy, (unsigned)splits), block(64 * NW);
+  hipLaunchKernelGGL((gemm_kernel<G, KIND, BM, TN, NW>), grid, block, 0, st, a.w, a.row_bytes, x16,
+                     rf, a.y, a.s, a.m, a.n, (int)nit, a.ws);
+  if (splits > 1) return launch_splitk_reduce(a.ws, a.y, a.s * a.n, (int)splits, st);
   return hipGetLastError();
 }
 
-template <int G, int KIND, bool XF32>
-hipError_t launch_x(const LinearArgs &a, hipStream_t st) {
-  // bf16 activations: 128-row tiles once the rows fill them (each converted
-  // weight fragment then feeds four row tiles); f32 activations carry a hi
-  // and a lo LDS copy and run 64-row tiles.
-  if constexpr (!XF32) {
-    if (a.s > 64) return launch_bm<G, KIND, XF32, 128>(a, st);
-  }
-  return launch_bm<G, KIND, XF32, 64>(a, st);
-}
-
 template <int G, int KIND>
-hipError_t launch_g(const LinearArgs &a, hipStream_t st) {
-  if (a.x_is_bf16) return launch_x<G, KIND, false>(a, st);
-  return launch_x<G, KIND, true>(a, st);
+hipError_t launch_g(const LinearArgs &a, const uint16_t *x16, const float *rf, hipStream_t st) {
+  // 128-row tiles once the rows fill them; two column tiles per wave when
+  // the 256-column tiles still give every CU a workgroup.
+  if (a.s > 64) {
+    const int64_t tiles256 = (a.n + 255) / 256 * ((a.s + 127) / 128);
+    if (tiles256 >= 256) return launch_t<G, KIND, 128, 2, kWaves>(a, x16, rf, st);
+    return launch_t<G, KIND, 128, 1, kWaves>(a, x16, rf, st);
+  }
+  return launch_t<G, KIND, 64, 1, kWaves>(a, x16, rf, st);
 }
 
 }  // namespace
 
-hipError_t launch_gemm(const LinearArgs &a, hipStream_t st) {
+hipError_t launch_splitk_reduce(const float *ws, float *y, int64_t count, int splits,
+                                hipStream_t st) {
+  const int64_t threads = (count + 3) / 4;
+  hipLaunchKernelGGL(splitk_reduce_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0,
+                     st, ws, y, count, splits);
+  return hipGetLastError();
+}
+
+hipError_t launch_gemm(const LinearArgs &a, uint16_t *x16, float *rf, hipStream_t st) {
   if (a.s == 0 || a.n == 0) return hipSuccess;
-  if (a.G == 64 && a.kind == SCALE_F16) return launch_g<64, SCALE_F16>(a, st);
-  if (a.G == 64 && a.kind == SCALE_F32) return launch_g<64, SCALE_F32>(a, st);
-  if (a.G == 32 && a.kind == SCALE_F16) return launch_g<32, SCALE_F16>(a, st);
-  if (a.G == 32 && a.kind == SCALE_F32) return launch_g<32, SCALE_F32>(a, st);
+  if (a.x_is_bf16)
+    hipLaunchKernelGGL((act16_kernel<false>), dim3((unsigned)a.s), dim3(256), 0, st, a.x, a.m, x16, rf);
+  else
+    hipLaunchKernelGGL((act16_kernel<true>), dim3((unsigned)a.s), dim3(256), 0, st, a.x, a.m, x16, rf);
+  if (a.G == 64 && a.kind == SCALE_F16) return launch_g<64, SCALE_F16>(a, x16, rf, st);
+  if (a.G == 64 && a.kind == SCALE_F32) return launch_g<64, SCALE_F32>(a, x16, rf, st);
+  if (a.G == 32 && a.kind == SCALE_F16) return launch_g<32, SCALE_F16>(a, x16, rf, st);
+  if (a.G == 32 && a.kind == SCALE_F32) return launch_g<32, SCALE_F32>(a, x16, rf, st);
   return hipErrorInvalidValue;
 }
 

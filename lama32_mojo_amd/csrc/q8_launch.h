@@ -65,8 +65,13 @@ constexpr int kArgmaxMaxBlocks = 8192;
 // False when the shape cannot take the fused path (x staged in LDS).
 bool gemv_fused_supported(const FusedLinearArgs &f);
 hipError_t launch_gemv_fused(const FusedLinearArgs &a, hipStream_t st);
-// Prefill path: MFMA GEMM (bf16 x, or f32 x split into two bf16 terms).
-hipError_t launch_gemm(const LinearArgs &a, hipStream_t st);
+// Prefill path, dequant-GEMM on f16 MFMA: x (bf16 or f32) is first written
+// as binary16 rows scaled by a power of two to x16 [s, m] with the factors
+// in rf [s]; then the weights are dequantized to binary16 in registers.
+hipError_t launch_gemm(const LinearArgs &a, uint16_t *x16, float *rf, hipStream_t st);
+// y[i] = sum over z < splits of ws[z * count + i] (split-K partial sums).
+hipError_t launch_splitk_reduce(const float *ws, float *y, int64_t count, int splits,
+                                hipStream_t st);
 // Small batches (2 <= s <= 32, f32 x): MFMA over zero-padded 16-row tiles.
 hipError_t launch_skinny(const LinearArgs &a, hipStream_t st);
 

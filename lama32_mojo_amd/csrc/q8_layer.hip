@@ -26,18 +26,6 @@
 namespace q8 {
 namespace {
 
-__device__ __forceinline__ float wave_max(float v) {
-  v = fmaxf(v, dpp_mov<0xb1>(v));
-  v = fmaxf(v, dpp_mov<0x4e>(v));
-  v = fmaxf(v, dpp_mov<0x141>(v));
-  v = fmaxf(v, dpp_mov<0x140>(v));
-  const float a = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 0));
-  const float b = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 16));
-  const float c = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 32));
-  const float d = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 48));
-  return fmaxf(fmaxf(a, b), fmaxf(c, d));
-}
-
 // cos and sin of a RoPE angle through one sincosf call, so every kernel that
 // rotates gets bit-identical values (separate cosf / sinf calls may be
 // lowered differently from one kernel to the next).
@@ -58,7 +46,6 @@ __device__ __forceinline__ void rotate(float x0, float x1, float c, float sn, fl
   y1 = b;
 }
 
-// Sum over a 256-thread block (4 waves); every thread gets the total.
 // ---- RMSNorm (k_rmsnorm_w): y = bf16(w) * x * 1/sqrt(mean(x^2) + eps) -------
 // One 256-thread block per row.  With res != null the row is h = x + res,
 // stored to h_out, and normalised (k_res_add followed by k_rmsnorm_w).

@@ -31,6 +31,9 @@ struct q8_ctx {
   // The decode attention's partial records use it too: both run in stream
   // order on this context.
   float *gemm_ws = nullptr;
+  // Binary16 copy of the activation rows of a prefill GEMM and their
+  // power-of-two factors (launch_gemm); longer inputs run in row chunks.
+  void *act16 = nullptr;
   // Pinned staging for file -> device uploads (q8_st_upload): two halves,
   // allocated on first use.
   void *stage = nullptr;
@@ -39,6 +42,7 @@ struct q8_ctx {
 
 namespace {
 constexpr int64_t kGemmWsFloats = (int64_t)4 << 20;
+constexpr int64_t kAct16Bytes = (int64_t)64 << 20;
 }
 
 struct q8_buf {
@@ -153,7 +157,9 @@ int q8_create(int device_ordinal, q8_ctx **out) {
     ctx->stream = ctx->own;
     // Split-K workspace of the prefill GEMM, allocated up front so that
     // calls captured into HIP graphs can use it too.
-    if (hipMalloc(&ctx->gemm_ws, kGemmWsFloats * sizeof(float)) != hipSuccess) {
+    if (hipMalloc(&ctx->gemm_ws, kGemmWsFloats * sizeof(float)) != hipSuccess ||
+        hipMalloc(&ctx->act16, kAct16Bytes) != hipSuccess) {
+      if (ctx->gemm_ws) (void)hipFree(ctx->gemm_ws);
       (void)hipStreamDestroy(ctx->own);
       delete ctx;
       return fail(nullptr, Q8_ERR_NOMEM, "q8_create: cannot allocate the GEMM workspace");
@@ -173,6 +179,7 @@ void q8_destroy(q8_ctx *ctx) {
       (void)hipStreamDestroy(ctx->own);
     }
     if (ctx->gemm_ws) (void)hipFree(ctx->gemm_ws);
+    if (ctx->act16) (void)hipFree(ctx->act16);
     if (ctx->stage) (void)hipHostFree(ctx->stage);
     for (hipEvent_t &ev : ctx->stage_ev)
       if (ev) (void)hipEventDestroy(ev);
@@ -407,8 +414,8 @@ bool gemm_aligned(const q8::LinearArgs &a) {
 }
 
 // Activation rows at which the W8A32 path switches from the VALU GEMV to the
-// small-batch MFMA kernel, and from that to the MFMA GEMM (f32 x split into
-// two bf16 terms in both).
+// small-batch MFMA kernel (f32 x split into two bf16 terms), and from that
+// to the dequant-GEMM on f16 MFMA.
 constexpr int64_t kSkinnyMinRows = 2;
 constexpr int64_t kGemmMinRows = 32;
 
@@ -416,6 +423,28 @@ constexpr int64_t kGemmMinRows = 32;
 void attach_gemm_workspace(q8_ctx *ctx, q8::LinearArgs &la) {
   la.ws = ctx->gemm_ws;
   la.ws_floats = kGemmWsFloats;
+}
+
+// Prefill GEMM on f16 MFMA through the context's binary16 activation
+// buffer, in chunks of as many rows as it holds (stream order keeps the
+// chunks from overlapping).
+hipError_t run_gemm(q8_ctx *ctx, q8::LinearArgs la) {
+  attach_gemm_workspace(ctx, la);
+  const int64_t rows = kAct16Bytes / (la.m * 2 + 4);
+  uint16_t *x16 = static_cast<uint16_t *>(ctx->act16);
+  float *rf = reinterpret_cast<float *>(static_cast<uint8_t *>(ctx->act16) + rows * la.m * 2);
+  const int64_t xb = la.x_is_bf16 ? 2 : 4;
+  const uint8_t *x0 = static_cast<const uint8_t *>(la.x);
+  float *y0 = la.y;
+  const int64_t s = la.s;
+  for (int64_t r0 = 0; r0 < s; r0 += rows) {
+    la.s = s - r0 < rows ? s - r0 : rows;
+    la.x = x0 + r0 * la.m * xb;
+    la.y = y0 + r0 * la.n;
+    hipError_t e = q8::launch_gemm(la, x16, rf, ctx->stream);
+    if (e != hipSuccess) return e;
+  }
+  return hipSuccess;
 }
 
 }  // namespace
@@ -450,8 +479,7 @@ int q8_linear(q8_ctx *ctx, q8_buf *w, uint64_t owt_u16, q8_buf *a, uint64_t ox_f
   la.kind = scale_dtype;
   hipError_t e;
   if (s >= kGemmMinRows && gemm_aligned(la)) {
-    attach_gemm_workspace(ctx, la);
-    e = q8::launch_gemm(la, ctx->stream);
+    e = run_gemm(ctx, la);
   } else if (s >= kSkinnyMinRows && gemm_aligned(la)) {
     e = q8::launch_skinny(la, ctx->stream);
   } else {
@@ -493,8 +521,7 @@ int q8_linear_bf16act(q8_ctx *ctx, q8_buf *w, uint64_t owt_u16, q8_buf *x, uint6
   la.kind = scale_dtype;
   hipError_t e;
   if (gemm_aligned(la)) {
-    attach_gemm_workspace(ctx, la);
-    e = q8::launch_gemm(la, ctx->stream);
+    e = run_gemm(ctx, la);
   } else {
     e = q8::launch_gemv(la, ctx->stream);
   }
