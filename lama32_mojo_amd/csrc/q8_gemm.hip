@@ -139,13 +139,13 @@ void gemm_kernel(const uint8_t *__restrict__ w, int64_t row_bytes,
   constexpr int BN = 128 * TN;
   constexpr int AU = BM * KT / 8 / NT;        // 8-half A chunks per thread
   constexpr int NG = 64 / G;                  // groups per 64-code slot
-  constexpr int SPB = 2 * (KT / G) * SB;      // scale bytes of a row per 2 iterations
+  constexpr int SPB = (KT / G) * SB;          // scale bytes of a row per iteration
   constexpr int SDW = BN * SPB / 4;           // ... as dwords per block
   constexpr int SU = (SDW + NT - 1) / NT;     // ... per thread
   constexpr int CU = BN * KT / 16 / NT;       // 16-byte code chunks per thread
   __shared__ __attribute__((aligned(16))) uint16_t As[2][BM * LDA];
   __shared__ __attribute__((aligned(16))) uint8_t Bs[2][BN * KT];    // codes, swizzled rows
-  __shared__ __attribute__((aligned(16))) uint8_t Ss[2][BN * SPB];   // scales of 2 iterations
+  __shared__ __attribute__((aligned(16))) uint8_t Ss[2][BN * SPB];   // scales
   __shared__ float rfs[BM];
 
   const int tid = threadIdx.x, lane = tid & 63;
@@ -180,16 +180,16 @@ void gemm_kernel(const uint8_t *__restrict__ w, int64_t row_bytes,
       *reinterpret_cast<u32x4 *>(&Bs[buf][r * KT + 16 * ((c & 7) ^ ((r >> 1) & 7))]) = src[u];
     }
   };
-  // Scale tiles: BN rows x SPB bytes per period of 2 iterations, as dwords
-  // (thread t takes dwords t, t + NT, ... of the [BN][SPB / 4] tile).
-  auto load_scales = [&](uint32_t *dst, int per) {
+  // Scale tiles: BN rows x SPB bytes per iteration, as dwords (thread t
+  // takes dwords t, t + NT, ... of the [BN][SPB / 4] tile; a thread past the
+  // tile loads a duplicate it does not store, so no load sits in a branch).
+  auto load_scales = [&](uint32_t *dst, int it) {
 #pragma unroll
     for (int u = 0; u < SU; ++u) {
-      const int i = tid + NT * u;
-      if (i < SDW)
-        dst[u] = __builtin_amdgcn_raw_buffer_load_b32(
-            wr, (uint32_t)((i / (SPB / 4)) * row_bytes + (kbase + 2 * KT * per) / G * SB +
-                           4 * (i % (SPB / 4))), 0, 0);
+      const int i = (tid + NT * u) % SDW;
+      dst[u] = __builtin_amdgcn_raw_buffer_load_b32(
+          wr, (uint32_t)((i / (SPB / 4)) * row_bytes + (kbase + KT * it) / G * SB +
+                         4 * (i % (SPB / 4))), 0, 0);
     }
   };
   auto store_scales = [&](const uint32_t *src, int buf) {
@@ -252,6 +252,9 @@ void gemm_kernel(const uint8_t *__restrict__ w, int64_t row_bytes,
 #pragma unroll
       for (int v = 0; v < 16; ++v) acc[i][t][v] = 0.0f;
 
+  // Every iteration stages the tiles of the next one; loads past the split's
+  // K range read zeros or bytes that are never used, so none of them sits in
+  // a branch (a load in a branch makes the wave wait for all its loads).
   u32x4 ra[AU], rc[CU];
   uint32_t rs[SU];
   load_scales(rs, 0);
@@ -260,7 +263,7 @@ void gemm_kernel(const uint8_t *__restrict__ w, int64_t row_bytes,
   store_scales(rs, 0);
   store_codes(rc, 0);
   store_a(ra, 0);
-  if (nit > 2) load_scales(rs, 1);
+  load_scales(rs, 1);
   load_codes(rc, 1);
   load_a(ra, 1);
   __syncthreads();
@@ -268,7 +271,7 @@ void gemm_kernel(const uint8_t *__restrict__ w, int64_t row_bytes,
   const f16x2 zero2 = {(_Float16)0.0f, (_Float16)0.0f};
   for (int it = 0; it < nit; ++it) {
     const uint8_t *bt = Bs[it & 1];
-    const uint8_t *st = Ss[(it >> 1) & 1];
+    const uint8_t *st = Ss[it & 1];
     const uint16_t *at = As[it & 1];
 #pragma unroll
     for (int hh = 0; hh < 2 / NP; ++hh) {
@@ -285,7 +288,7 @@ void gemm_kernel(const uint8_t *__restrict__ w, int64_t row_bytes,
         const int sw = (r >> 1) & 7;
         cq[t][0] = *reinterpret_cast<const u32x4 *>(bt + r * KT + 16 * ((4 * h + (chunk0 >> 4)) ^ sw));
         cq[t][1] = *reinterpret_cast<const u32x4 *>(bt + r * KT + 16 * ((4 * h + (chunk1 >> 4)) ^ sw));
-        const uint8_t *sp = st + r * SPB + (2 * (it & 1) + h) * NG * SB;
+        const uint8_t *sp = st + r * SPB + h * NG * SB;
 #pragma unroll
         for (int g = 0; g < NG; ++g) {
           _Float16 hs;
@@ -323,19 +326,14 @@ void gemm_kernel(const uint8_t *__restrict__ w, int64_t row_bytes,
             acc[ii][t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[ks & 1][ii], bq[t], acc[ii][t], 0, 0, 0);
       }
     }
-    // stage the tiles of iteration it + 1 (period (it + 1) / 2 starts
-    // there when it is odd), then load those of it + 2
-    if (it + 1 < nit) {
-      store_codes(rc, (it + 1) & 1);
-      store_a(ra, (it + 1) & 1);
-      if (it & 1) store_scales(rs, ((it + 1) >> 1) & 1);
-    }
+    // stage the tiles of iteration it + 1, then load those of it + 2
+    store_scales(rs, (it + 1) & 1);
+    store_codes(rc, (it + 1) & 1);
+    store_a(ra, (it + 1) & 1);
     __syncthreads();
-    if (it + 2 < nit) {
-      load_codes(rc, it + 2);
-      load_a(ra, it + 2);
-    }
-    if ((it & 1) && it + 3 < nit) load_scales(rs, (it + 3) >> 1);
+    load_scales(rs, it + 2);
+    load_codes(rc, it + 2);
+    load_a(ra, it + 2);
   }
 
   // With two K parities, each column tile's parities meet in LDS (reusing
@@ -406,7 +404,6 @@ hipError_t launch_t(const LinearArgs &a, const uint16_t *x16, const float *rf, h
       splits *= 2;
   }
   int64_t nit = (nit_all + splits - 1) / splits;
-  nit = (nit + 1) / 2 * 2;                    // whole scale periods of 2 iterations
   dim3 grid((unsigned)gx, (unsigned)gy, (unsigned)splits), block(64 * NW);
   hipLaunchKernelGGL((gemm_kernel<G, KIND, BM, TN, NW>), grid, block, 0, st, a.w, a.row_bytes, x16,
                      rf, a.y, a.s, a.m, a.n, (int)nit, a.ws);
