@@ -51,7 +51,10 @@ constexpr int kWaves = 8;      // waves per workgroup: 8 (two K parities) or 4
 constexpr int LDA = KT + 8;    // halves per LDS row (16-byte pad)
 
 // ---- 1. activation rows to binary16 ----------------------------------------
-template <bool XF32>
+// One 256-thread block per row.  With CH > 0 the row (m <= 2048 CH) stays in
+// registers between the max and the conversion (one pass over memory);
+// CH = 0 reads it twice.
+template <bool XF32, int CH>
 __global__ __launch_bounds__(256) void act16_kernel(const void *__restrict__ xv, int64_t m,
                                                     uint16_t *__restrict__ x16,
                                                     float *__restrict__ rf) {
@@ -77,27 +80,7 @@ __global__ __launch_bounds__(256) void act16_kernel(const void *__restrict__ xv,
       }
     }
   };
-  float mx = 0.0f;
-  for (int64_t k = 8 * tid; k < m; k += 8 * 256) {
-    float v[8];
-    load8(k, v);
-#pragma unroll
-    for (int c = 0; c < 8; ++c) mx = fmaxf(mx, fabsf(v[c]));
-  }
-  mx = wave_max(mx);
-  if ((tid & 63) == 0) red[tid >> 6] = mx;
-  __syncthreads();
-  mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-  // largest |x| * 2^-e in [2^14, 2^15); rows of zeros, inf or NaN keep e = 0
-  int e = 0;
-  if (mx > 0.0f && mx <= 3.4028235e38f) {
-    e = (int)((__builtin_bit_cast(uint32_t, mx) >> 23) & 255u) - 127 - 14;
-    if (mx < 1.17549435e-38f) e = -126;       // subnormal maximum: as far as 2^126 goes
-    e = e < -126 ? -126 : e;
-  }
-  for (int64_t k = 8 * tid; k < m; k += 8 * 256) {
-    float v[8];
-    load8(k, v);
+  auto store8 = [&](int64_t k, const float (&v)[8], int e) {
     u32x4 o;
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
@@ -106,8 +89,70 @@ __global__ __launch_bounds__(256) void act16_kernel(const void *__restrict__ xv,
       o[c] = __builtin_bit_cast(uint32_t, hv);
     }
     *reinterpret_cast<u32x4 *>(x16 + r * m + k) = o;
+  };
+  auto exponent = [&](float mx) {
+    mx = wave_max(mx);
+    if ((tid & 63) == 0) red[tid >> 6] = mx;
+    __syncthreads();
+    mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    // largest |x| * 2^-e in [2^14, 2^15); rows of zeros, inf or NaN keep e = 0
+    int e = 0;
+    if (mx > 0.0f && mx <= 3.4028235e38f) {
+      e = (int)((__builtin_bit_cast(uint32_t, mx) >> 23) & 255u) - 127 - 14;
+      if (mx < 1.17549435e-38f) e = -126;     // subnormal maximum: as far as 2^126 goes
+      e = e < -126 ? -126 : e;
+    }
+    return e;
+  };
+  float mx = 0.0f;
+  int e;
+  if constexpr (CH > 0) {
+    float v[CH][8];
+#pragma unroll
+    for (int c = 0; c < CH; ++c) {
+      const int64_t k = 8 * tid + 2048 * c;
+      if (k < m) {
+        load8(k, v[c]);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) mx = fmaxf(mx, fabsf(v[c][j]));
+      }
+    }
+    e = exponent(mx);
+#pragma unroll
+    for (int c = 0; c < CH; ++c) {
+      const int64_t k = 8 * tid + 2048 * c;
+      if (k < m) store8(k, v[c], e);
+    }
+  } else {
+    for (int64_t k = 8 * tid; k < m; k += 2048) {
+      float v[8];
+      load8(k, v);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) mx = fmaxf(mx, fabsf(v[j]));
+    }
+    e = exponent(mx);
+    for (int64_t k = 8 * tid; k < m; k += 2048) {
+      float v[8];
+      load8(k, v);
+      store8(k, v, e);
+    }
   }
   if (tid == 0) rf[r] = __builtin_ldexpf(1.0f, e);
+}
+
+template <bool XF32>
+void launch_act16(const LinearArgs &a, uint16_t *x16, float *rf, hipStream_t st) {
+  const dim3 grid((unsigned)a.s), block(256);
+  if (a.m <= 2048)
+    hipLaunchKernelGGL((act16_kernel<XF32, 1>), grid, block, 0, st, a.x, a.m, x16, rf);
+  else if (a.m <= 4096)
+    hipLaunchKernelGGL((act16_kernel<XF32, 2>), grid, block, 0, st, a.x, a.m, x16, rf);
+  else if (a.m <= 8192)
+    hipLaunchKernelGGL((act16_kernel<XF32, 4>), grid, block, 0, st, a.x, a.m, x16, rf);
+  else if (a.m <= 16384)
+    hipLaunchKernelGGL((act16_kernel<XF32, 8>), grid, block, 0, st, a.x, a.m, x16, rf);
+  else
+    hipLaunchKernelGGL((act16_kernel<XF32, 0>), grid, block, 0, st, a.x, a.m, x16, rf);
 }
 
 // ---- 2. the GEMM --------------------------------------------------------------
@@ -436,9 +481,9 @@ hipError_t launch_splitk_reduce(const float *ws, float *y, int64_t count, int sp
 hipError_t launch_gemm(const LinearArgs &a, uint16_t *x16, float *rf, hipStream_t st) {
   if (a.s == 0 || a.n == 0) return hipSuccess;
   if (a.x_is_bf16)
-    hipLaunchKernelGGL((act16_kernel<false>), dim3((unsigned)a.s), dim3(256), 0, st, a.x, a.m, x16, rf);
+    launch_act16<false>(a, x16, rf, st);
   else
-    hipLaunchKernelGGL((act16_kernel<true>), dim3((unsigned)a.s), dim3(256), 0, st, a.x, a.m, x16, rf);
+    launch_act16<true>(a, x16, rf, st);
   if (a.G == 64 && a.kind == SCALE_F16) return launch_g<64, SCALE_F16>(a, x16, rf, st);
   if (a.G == 64 && a.kind == SCALE_F32) return launch_g<64, SCALE_F32>(a, x16, rf, st);
   if (a.G == 32 && a.kind == SCALE_F16) return launch_g<32, SCALE_F16>(a, x16, rf, st);
