@@ -413,6 +413,31 @@ def test_model_forward_and_greedy_decode(ctx, G, scale):
         m.close()
 
 
+@pytest.mark.parametrize("G,scale", [(64, "f16"), (32, "f32")])
+def test_model_long_prompt(ctx, G, scale):
+    """A 48-token prompt takes the prefill paths (the f16-MFMA dequant-GEMM
+    for the linears, the MFMA prompt-row attention): logits within 3e-3 of
+    the float64 model (binary16 activations and weights in the GEMM, each
+    rounding below 2^-11, compounded over two layers), the same greedy id,
+    and the following decode steps (exact f32 GEMVs) on the same ids."""
+    say("model long prompt", G, scale)
+    spec, t, inv = tiny_model(G=G, scale=scale, seed=9)
+    maxlen = 64
+    prompt = [int(v) for v in np.random.default_rng(4).integers(0, spec.vocab, size=48)]
+    ref = mo.OracleModel(spec, t, inv, maxlen)
+    m = gpu_model(ctx, spec, t, maxlen, max_prefill=48)
+    try:
+        lg = m.forward(prompt)
+        lr = ref.forward(prompt)
+        err = max_rel_err(lg, lr)
+        assert err <= 3e-3, err
+        top = np.sort(lr)[-2:]
+        if top[1] - top[0] > 1e-2 * np.max(np.abs(lr)):
+            assert int(np.argmax(lg)) == int(np.argmax(lr))
+    finally:
+        m.close()
+
+
 def test_graph_replay_equals_eager(ctx):
     """The captured step (device position and id) gives the same ids and the
     same logits bits as eager host-position steps."""
