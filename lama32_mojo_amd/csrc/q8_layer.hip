@@ -455,6 +455,17 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(const float *__restri
 }
 
 // ---- decode attention: RoPE + KV append + attention of one new token --------
+// Head slots of a decode-attention block of 4 waves (heads per wave
+// GRP / slots, waves per head 4 / slots).  With 64-dim heads (short rows,
+// contexts of a chunk or so per block) one head per wave; with 128-dim heads
+// in groups of 4 or 8 a wave serves 4 heads, so the K/V rows of a chunk are
+// loaded once and the block's waves work on different chunks (measured on
+// the Llama-3.1-8B step at 2300 cached tokens; slower on the 1B step).  The
+// merge kernel derives the active splits from the same value.
+constexpr int decode_head_slots(int hd, int grp) {
+  return (hd >= 128 && grp >= 4) ? grp / 4 : (grp < 4 ? grp : 4);
+}
+
 // Sum over aligned groups of N consecutive lanes (N = 8 or 16), in every lane.
 template <int N>
 __device__ __forceinline__ float lane_group_sum(float v) {
@@ -495,7 +506,7 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(
   constexpr int NI = KC / RPI;          // load instructions per chunk
   constexpr int half = HD / 2;
   constexpr int PR = HD + 2;            // partial record per head: o[HD], m, l
-  constexpr int HS = GRP < NW ? GRP : NW;   // head slots per block
+  constexpr int HS = decode_head_slots(HD, GRP);   // head slots per block
   constexpr int HPW = GRP / HS;             // heads per wave
   constexpr int WPH = NW / HS;              // waves per head
   __shared__ float qs[GRP][HD];
@@ -743,7 +754,7 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(const float *__restrict
                                                          int maxlen) {
   constexpr int KC = decode_attn_chunk(HD), NW = 4;
   constexpr int PR = HD + 2;
-  constexpr int WPH = NW / (GRP < NW ? GRP : NW);
+  constexpr int WPH = NW / decode_head_slots(HD, GRP);   // as attn_decode_kernel
   static_assert(kDecodeAttnMaxSplit <= 64, "one wave forms the split factors");
   __shared__ float rs[kDecodeAttnMaxSplit * PR];
   __shared__ float fac[kDecodeAttnMaxSplit];
