@@ -74,6 +74,10 @@ hipError_t launch_splitk_reduce(const float *ws, float *y, int64_t count, int sp
                                 hipStream_t st);
 // Small batches (2 <= s <= 32, f32 x): MFMA over zero-padded 16-row tiles.
 hipError_t launch_skinny(const LinearArgs &a, hipStream_t st);
+// A few rows (2 <= s <= kSkinny4MaxRows, f32 x): f32 4x4 MFMA blocks over
+// 16-code runs, exact f32 products.
+constexpr int kSkinny4MaxRows = 4;
+hipError_t launch_skinny4(const LinearArgs &a, hipStream_t st);
 
 struct GatherArgs {
   const uint8_t *w;      // byte address of packed row 0 of the table

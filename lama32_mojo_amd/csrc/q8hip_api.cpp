@@ -414,8 +414,9 @@ bool gemm_aligned(const q8::LinearArgs &a) {
 }
 
 // Activation rows at which the W8A32 path switches from the VALU GEMV to the
-// small-batch MFMA kernel (f32 x split into two bf16 terms), and from that
-// to the dequant-GEMM on f16 MFMA.
+// small-batch MFMA kernels (f32 4x4 blocks up to q8::kSkinny4MaxRows rows,
+// then f32 x split into two bf16 terms), and from those to the dequant-GEMM
+// on f16 MFMA.
 constexpr int64_t kSkinnyMinRows = 2;
 constexpr int64_t kGemmMinRows = 32;
 
@@ -480,6 +481,8 @@ int q8_linear(q8_ctx *ctx, q8_buf *w, uint64_t owt_u16, q8_buf *a, uint64_t ox_f
   hipError_t e;
   if (s >= kGemmMinRows && gemm_aligned(la)) {
     e = run_gemm(ctx, la);
+  } else if (s >= kSkinnyMinRows && s <= q8::kSkinny4MaxRows && gemm_aligned(la)) {
+    e = q8::launch_skinny4(la, ctx->stream);
   } else if (s >= kSkinnyMinRows && gemm_aligned(la)) {
     e = q8::launch_skinny(la, ctx->stream);
   } else {

@@ -125,7 +125,7 @@ SHAPES = [(8192, 2048), (3072, 2048), (2048, 8192), (1000, 1536), (1, 64), (7, 9
 
 @pytest.mark.parametrize("G,scale", LAYOUTS)
 @pytest.mark.parametrize("n,m", SHAPES)
-@pytest.mark.parametrize("s", [1, 2, 3, 4, 5, 16, 24])
+@pytest.mark.parametrize("s", [1, 2, 3, 4, 5, 8, 9, 16, 24])
 def test_linear_matches_closed_form(ctx, cor, G, scale, n, m, s):
     if m % G:
         pytest.skip("m not a multiple of G")
@@ -138,6 +138,29 @@ def test_linear_matches_closed_form(ctx, cor, G, scale, n, m, s):
     err = max_rel_err(y, ref)
     assert err <= TOL, err
     assert err <= 1e-5, err      # fp32 accumulation is far inside the bar
+
+
+@pytest.mark.parametrize("G,scale,n,m", [(32, "f32", 4099, 640), (32, "f32", 16386, 640),
+                                         (64, "f16", 8195, 1536), (32, "f32", 24, 12288),
+                                         (64, "f16", 16384, 512)])
+@pytest.mark.parametrize("s", [2, 4, 6, 7, 8])
+def test_few_rows_ragged(ctx, cor, G, scale, n, m, s):
+    """2 <= s <= 8 rows (the f32 4x4-block kernel up to 4 rows, the split
+    bf16 kernel above): ragged weight-row blocks (n not a multiple of the
+    block's rows), K ending inside a 256-code slab, each block size the
+    launchers pick, long K split over the waves; the error stays at f32
+    accumulation level."""
+    say("few rows", G, scale, n, m, s)
+    wb = synth_weights_bf16(n, m, seed=n + s)
+    pk = cor.pack_bf16(wb, G, scale)
+    x = synth_x(s, m, seed=40 + s)
+    y = gpu_linear(ctx, pk, x, G, scale)
+    ref = cor.linear_f64(pk, x, G, scale)
+    err = max_rel_err(y, ref)
+    assert err <= 1e-5, err
+    # row-wise too: every batch row, not only the largest
+    for b in range(s):
+        assert max_rel_err(y[b], ref[b]) <= 1e-5, b
 
 
 @pytest.mark.parametrize("G,scale", LAYOUTS)
