@@ -72,7 +72,8 @@ hipError_t launch_gemm(const LinearArgs &a, uint16_t *x16, float *rf, hipStream_
 // y[i] = sum over z < splits of ws[z * count + i] (split-K partial sums).
 hipError_t launch_splitk_reduce(const float *ws, float *y, int64_t count, int splits,
                                 hipStream_t st);
-// Small batches (2 <= s <= 32, f32 x): MFMA over zero-padded 16-row tiles.
+// Small batches (s <= 32, f32 x; the C ABI sends it 5 <= s < 32): bf16 MFMA
+// over zero-padded 16-row tiles with x split into two bf16 terms.
 hipError_t launch_skinny(const LinearArgs &a, hipStream_t st);
 // A few rows (2 <= s <= kSkinny4MaxRows, f32 x): f32 4x4 MFMA blocks over
 // 16-code runs, exact f32 products.

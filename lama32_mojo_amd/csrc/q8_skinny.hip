@@ -1,4 +1,4 @@
-// q8_skinny.hip -- decode-path Q8 linear for small batches (2 <= s < 32,
+// q8_skinny.hip -- decode-path Q8 linear for small batches (5 <= s < 32,
 // f32 activations) on gfx950 bf16 MFMA.
 //
 // y[b, j] = sum_g scale[j, g] * sum_{k in g} x[b, k] * q[j, k]
