@@ -177,6 +177,40 @@ def test_linear_one_hot_exact(ctx, cor, G, scale):
         assert np.array_equal(y[0], want)
 
 
+def ones_packed(n, m, G, scale):
+    """Packed rows whose codes are all 1 and whose scales are all 1.0."""
+    ng = m // G
+    if scale == "f16":
+        sc = np.full((n, ng), 1.0, np.float16).view(np.uint16)
+    else:
+        sc = np.full((n, ng), 1.0, np.float32).view(np.uint16).reshape(n, 2 * ng)
+    codes = np.ones((n, m), np.int8).view(np.uint16).reshape(n, m // 2)
+    pk = np.concatenate([sc, codes], axis=1)
+    assert pk.shape[1] == rowstride_u16(m, G, scale)
+    return pk
+
+
+@pytest.mark.parametrize("G,scale", LAYOUTS)
+@pytest.mark.parametrize("s", [1, 3, 8, 40])
+def test_linear_all_ones_gives_row_sums(ctx, cor, G, scale, s):
+    """Codes all 1 with scales 1.0: every output is sum(x) of its row (the
+    s = 1 GEMV, both small-batch kernels and the GEMM).  x >= 0, so the sum
+    is well conditioned: the f32 paths stay within 1e-5 of it, the GEMM
+    (binary16 copy of x, 2^-12 per element) within 3e-4.  Columns with
+    equal weights take equal steps, so each row's outputs are all equal."""
+    say("all ones", G, scale, s)
+    n, m = 300, 4096
+    pk = ones_packed(n, m, G, scale)
+    codes, sc = unpack_q8_np(pk, m, G, scale)
+    assert np.all(codes == 1) and np.all(sc == 1.0)
+    x = np.random.default_rng(50 + s).random((s, m), dtype=np.float32)
+    y = gpu_linear(ctx, pk, x, G, scale)
+    want = x.astype(np.float64).sum(axis=1)
+    tol = 1e-5 if s < 32 else 3e-4
+    assert np.all(np.abs(y - want[:, None]) <= tol * want[:, None]), np.abs(y / want[:, None] - 1).max()
+    assert np.all(y == y[:, :1])
+
+
 def test_linear_zero_input(ctx, cor):
     pk = cor.pack_bf16(synth_weights_bf16(300, 512, seed=32))
     y = gpu_linear(ctx, pk, np.zeros((2, 512), np.float32), 64, "f16")
