@@ -22,9 +22,11 @@
 //     rotations and LDS at the end, together with the waves' K ranges.
 // Per 16 codes a lane spends 16 conversions, 4 FMAs and one scale
 // conversion; the matrix cores spend 16 x 8 cycles per TR row groups.
-// A wave covers Q quads of weight rows (x loaded once per slab and reused
-// Q times) over a contiguous range of slabs; the KW waves of a workgroup
-// split K.  Nothing is read from memory in the MFMA layout (lanes 4b .. 4b+3
+// Two forms.  skinny4_kernel: a wave covers Q quads of weight rows (x
+// loaded once per slab and reused Q times) over a contiguous range of
+// slabs, and the KW waves of a workgroup split K.  skinny4x_kernel (wide
+// matrices): the waves walk all of K together over their own rows and share
+// each x slab through LDS.  Nothing is read from memory in the MFMA layout (lanes 4b .. 4b+3
 // sit on four different rows, so neighbouring lanes never touch
 // neighbouring bytes and the L1 splits such a load into one access per
 // lane): codes are loaded 16 lanes per row (256 contiguous bytes), each x row
@@ -281,6 +283,173 @@ __global__ __launch_bounds__(64 * KW) void skinny4_kernel(const uint8_t *__restr
   }
 }
 
+// Shared-x form, for matrices with many rows: the KW waves of a workgroup
+// walk every slab of K together, each over its own Q quads of weight rows,
+// so a slab of x (4 TR rows x 1 KiB) is loaded once per workgroup (its rows
+// split over the waves, each row one coalesced load) into a double-buffered
+// LDS region, with one barrier per slab; a workgroup then reads x once per
+// 4 Q KW weight rows instead of once per 4 Q.  Codes and scales go through
+// the wave's own LDS region as in skinny4_kernel, and no K ranges meet.
+template <int G, int KIND, int TR, int Q, int KW>
+__global__ __launch_bounds__(64 * KW) void skinny4x_kernel(const uint8_t *__restrict__ w,
+                                                           int64_t row_bytes,
+                                                           const float *__restrict__ x,
+                                                           float *__restrict__ y, int s, int m,
+                                                           int64_t n, int nslab) {
+  constexpr int SB = ScaleTraits<KIND>::bytes;
+  constexpr int XR = 4 * TR;                 // staged x rows
+  constexpr int XPW = (XR + KW - 1) / KW;    // x rows each wave loads
+  typedef SlabScales<G, KIND, Q> SS;
+  __shared__ __attribute__((aligned(16))) float xs[2][XR][kXRow];
+  __shared__ uint32_t ss[KW][SS::NDW];
+  __shared__ __attribute__((aligned(16))) uint8_t cs_lds[KW][4 * Q][kCodeRow];
+  __shared__ f32x4 red[KW][Q * TR][16];
+
+  const int lane = threadIdx.x & 63;
+  const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int b = lane >> 2, c = lane & 3;
+  // this wave's rows [j0, j0 + 4Q); a wave past n reads zeros
+  const int64_t j0 = ((int64_t)blockIdx.x * KW + wid) * 4 * Q;
+  const int64_t nrows = n - j0 < 0 ? 0 : n - j0 < 4 * Q ? n - j0 : 4 * Q;
+  const rsrc_t wr = make_rsrc(w + (nrows > 0 ? j0 : 0) * row_bytes, (uint32_t)(nrows * row_bytes));
+  // x rows wid, wid + KW, ... of the staged XR (empty buffers past s and XR)
+  rsrc_t xr[XPW];
+#pragma unroll
+  for (int u = 0; u < XPW; ++u) {
+    const int r = wid + KW * u;
+    xr[u] = make_rsrc(x + (int64_t)(r < s ? r : 0) * m, r < s && r < XR ? (uint32_t)m * 4 : 0u);
+  }
+  const uint32_t cbase = (uint32_t)((m / G) * SB);
+  uint32_t co[Q], so[SS::NL];
+#pragma unroll
+  for (int q = 0; q < Q; ++q)
+    co[q] = (uint32_t)((4 * q + (lane >> 4)) * row_bytes) + cbase + 16 * (lane & 15);
+#pragma unroll
+  for (int j = 0; j < SS::NL; ++j) {
+    const int i = lane + 64 * j, row = i / (SS::SPS / 4);
+    so[j] = i < SS::NDW ? (uint32_t)(row * row_bytes) + 4 * (i % (SS::SPS / 4)) : kOutOfRange;
+  }
+
+  auto load_codes = [&](CodeSlab<Q, SS::NL> &sl, int slab) {
+    const int k0 = slab * kSlab;
+#pragma unroll
+    for (int q = 0; q < Q; ++q) sl.cq[q] = bload16(wr, co[q] + k0);
+#pragma unroll
+    for (int j = 0; j < SS::NL; ++j)
+      sl.sw[j] = __builtin_amdgcn_raw_buffer_load_b32(wr, so[j] + (uint32_t)(slab * SS::SPS), 0, 0);
+  };
+  auto load_x = [&](u32x4 (&xg)[XPW], int slab) {
+    const uint32_t o = (uint32_t)(slab * kSlab * 4) + 16 * lane;
+#pragma unroll
+    for (int u = 0; u < XPW; ++u) xg[u] = bload16(xr[u], o);
+  };
+  auto store_x = [&](const u32x4 (&xg)[XPW], int buf) {
+#pragma unroll
+    for (int u = 0; u < XPW; ++u)
+      if (wid + KW * u < XR)
+        *reinterpret_cast<u32x4 *>(&xs[buf][wid + KW * u][4 * lane]) = xg[u];
+  };
+
+  f32x4 acc[Q][TR];
+#pragma unroll
+  for (int q = 0; q < Q; ++q)
+#pragma unroll
+    for (int t = 0; t < TR; ++t) acc[q][t] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+
+  uint32_t *sw = &ss[wid][0];
+  uint8_t *cw = &cs_lds[wid][0][0];
+  auto compute = [&](const CodeSlab<Q, SS::NL> &cs, int buf, int slab) {
+    u32x4 xq[TR][4];
+#pragma unroll
+    for (int t = 0; t < TR; ++t)
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        xq[t][j] = *reinterpret_cast<const u32x4 *>(&xs[buf][4 * t + c][16 * b + 4 * j]);
+    u32x4 cq[Q];
+#pragma unroll
+    for (int q = 0; q < Q; ++q)
+      *reinterpret_cast<u32x4 *>(cw + (4 * q + (lane >> 4)) * kCodeRow + 16 * (lane & 15)) =
+          cs.cq[q];
+#pragma unroll
+    for (int j = 0; j < SS::NL; ++j)
+      if (lane + 64 * j < SS::NDW) sw[lane + 64 * j] = cs.sw[j];
+#pragma unroll
+    for (int q = 0; q < Q; ++q)
+      cq[q] = *reinterpret_cast<const u32x4 *>(cw + (4 * q + c) * kCodeRow + 16 * b);
+    uint32_t sraw[Q];
+#pragma unroll
+    for (int q = 0; q < Q; ++q) {
+      const int byte = (4 * q + c) * SS::SPS + (16 * b / G) * SB;
+      const uint32_t wd = sw[byte >> 2];
+      sraw[q] = KIND == SCALE_F16 ? (wd >> (8 * (byte & 3))) & 0xffffu : wd;
+    }
+    f32x4 d[Q][TR];
+    mfma_run<TR, Q>(cq, xq, d, std::make_integer_sequence<int, 16>{});
+    const bool live = slab * kSlab + 16 * b < m;
+#pragma unroll
+    for (int q = 0; q < Q; ++q) {
+      const float sc = live ? scale_bits_to_f32<KIND>(sraw[q]) : 0.0f;
+#pragma unroll
+      for (int t = 0; t < TR; ++t)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) acc[q][t][v] = __builtin_fmaf(d[q][t][v], sc, acc[q][t][v]);
+    }
+  };
+
+  // Slab i uses x buffer i % 2.  A buffer is rewritten only after the
+  // barrier that follows every wave's last read of it; an odd last slab is
+  // skipped by a uniform branch that holds no loads.
+  CodeSlab<Q, SS::NL> C0, C1;
+  u32x4 X0[XPW], X1[XPW];
+  load_codes(C0, 0);
+  load_x(X0, 0);
+  store_x(X0, 0);
+  load_codes(C1, 1);
+  load_x(X1, 1);
+  __syncthreads();
+  for (int i = 0; i < nslab; i += 2) {
+    compute(C0, 0, i);
+    store_x(X1, 1);
+    __syncthreads();
+    load_codes(C0, i + 2);
+    load_x(X0, i + 2);
+    if (i + 1 < nslab) compute(C1, 1, i + 1);
+    store_x(X0, 0);
+    __syncthreads();
+    load_codes(C1, i + 3);
+    load_x(X1, i + 3);
+  }
+
+  // Sum over the 16 blocks (two rotations within each 16-lane row, then the
+  // four rows through the wave's LDS region) and store.
+#pragma unroll
+  for (int q = 0; q < Q; ++q)
+#pragma unroll
+    for (int t = 0; t < TR; ++t) {
+      f32x4 v = acc[q][t];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        v[e] += dpp_mov<0x128>(v[e]);   // row_ror:8
+        v[e] += dpp_mov<0x124>(v[e]);   // row_ror:4
+      }
+      if ((lane & 15) < 4) red[wid][q * TR + t][(lane >> 4) * 4 + c] = v;
+    }
+  constexpr int NOUT = 16 * Q * TR;
+#pragma unroll
+  for (int o0 = 0; o0 < NOUT; o0 += 64) {
+    const int o = o0 + lane;
+    if (o < NOUT) {
+      const int cc = o & 3, q = (o >> 2) % Q, r = (o / (4 * Q)) & 3, t = o / (16 * Q);
+      float sum = 0.0f;
+#pragma unroll
+      for (int rr = 0; rr < 4; ++rr) sum += red[wid][q * TR + t][rr * 4 + cc][r];
+      const int64_t j = j0 + 4 * q + cc;
+      const int bb = 4 * t + r;
+      if (j < n && bb < s) y[(int64_t)bb * n + j] = sum;
+    }
+  }
+}
+
 template <int G, int KIND, int TR, int Q, int KW>
 hipError_t launch_q(const LinearArgs &a, int per, hipStream_t st) {
   const int64_t blocks = (a.n + 4 * Q - 1) / (4 * Q);
@@ -320,8 +489,21 @@ hipError_t launch_tr(const LinearArgs &a, hipStream_t st) {
   return launch_kw<G, KIND, TR, 1>(a, st);
 }
 
+template <int G, int KIND, int TR, int Q, int KW>
+hipError_t launch_x(const LinearArgs &a, hipStream_t st) {
+  const int64_t blocks = (a.n + 4 * Q * KW - 1) / (4 * Q * KW);
+  const int nslab = (int)((a.m + kSlab - 1) / kSlab);
+  hipLaunchKernelGGL((skinny4x_kernel<G, KIND, TR, Q, KW>), dim3((unsigned)blocks),
+                     dim3(64 * KW), 0, st, a.w, a.row_bytes, static_cast<const float *>(a.x),
+                     a.y, (int)a.s, (int)a.m, a.n, nslab);
+  return hipGetLastError();
+}
+
 template <int G, int KIND>
 hipError_t launch_g(const LinearArgs &a, hipStream_t st) {
+  // Wide matrices read x once per 32 weight rows (shared-x form: 512 or
+  // more workgroups from n = 16384); narrower ones split K over the waves.
+  if (a.n >= 16384) return launch_x<G, KIND, 1, 2, 4>(a, st);
   return launch_tr<G, KIND, 1>(a, st);
 }
 
