@@ -30,7 +30,7 @@
 //     meet in LDS; a workgroup covers NC tiles of 16 weight rows, NC chosen so
 //     that the grid still fills the chip.
 // All loads are range-checked buffer loads: batch rows past s and weight rows
-// past n read as zero.
+// past n read as zero.  Wide matrices take the shared-x form further below.
 #include "q8_device.h"
 #include "q8_launch.h"
 
@@ -296,6 +296,216 @@ __global__ __launch_bounds__(64 * KW) void skinny_kernel(const uint8_t *__restri
   }
 }
 
+// ---- shared-x form, for matrices with many rows ---------------------------
+// The KW waves of a workgroup walk every 256-code slab of K together, each
+// over NC tiles of 16 weight rows of its own.  Per slab, each of the 16 TR
+// x rows is loaded once per workgroup (one coalesced 1 KiB load, rows split
+// over the waves), split once into bf16 hi and lo and stored in a
+// double-buffered LDS region (one barrier per slab), so x is read and split
+// once per 16 NC KW weight rows.  Codes are loaded 16 lanes per row (256
+// contiguous bytes) and the slab's scales as whole dwords, both staged in
+// an LDS region private to the wave, and read back in the MFMA layout:
+// in k-step ks lane (c, q) takes codes and x at k = 32 ks + 8 q .. +8 of
+// weight row c and batch row c.  A k-step lies in one scale group; its
+// partial is folded into the output with the lane's scale (G = 64: every
+// two k-steps).  Rows are padded in LDS (x by 8 bf16, codes by 16 bytes) so
+// the ds_read passes are conflict-free.  No K ranges meet: each wave's
+// accumulators are its outputs.
+constexpr int kXSlab = 256;                // codes of a row per slab
+constexpr int kXbRow = kXSlab + 8;         // LDS bf16 per staged x row
+constexpr int kCbRow = kXSlab + 16;        // LDS bytes per staged code row
+
+template <int G, int KIND, int TR, int NC, int KW>
+__global__ __launch_bounds__(64 * KW) void skinny_x_kernel(const uint8_t *__restrict__ w,
+                                                           int64_t row_bytes,
+                                                           const float *__restrict__ x,
+                                                           float *__restrict__ y, int s, int m,
+                                                           int64_t n, int nslab) {
+  constexpr int SB = ScaleTraits<KIND>::bytes;
+  constexpr int XR = 16 * TR;                  // staged x rows
+  static_assert(XR % KW == 0, "x rows split evenly over the waves");
+  constexpr int XPW = XR / KW;                 // x rows each wave loads
+  constexpr int SPS = (kXSlab / G) * SB;       // scale bytes of a row per slab
+  constexpr int NDW = NC * 16 * SPS / 4;       // scale dwords of a wave per slab
+  constexpr int NL = (NDW + 63) / 64;
+  constexpr int KPG = G / 32;                  // k-steps per scale group
+  __shared__ __attribute__((aligned(16))) uint16_t xh[2][XR][kXbRow];
+  __shared__ __attribute__((aligned(16))) uint16_t xl[2][XR][kXbRow];
+  __shared__ __attribute__((aligned(16))) uint8_t cs[KW][NC * 16][kCbRow];
+  __shared__ uint32_t ss[KW][NDW];
+
+  const int lane = threadIdx.x & 63;
+  const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int c = lane & 15, q = lane >> 4;
+  // this wave's rows [j0, j0 + 16 NC); a wave past n reads zeros
+  const int64_t j0 = ((int64_t)blockIdx.x * KW + wid) * 16 * NC;
+  const int64_t nrows = n - j0 < 0 ? 0 : n - j0 < 16 * NC ? n - j0 : 16 * NC;
+  const rsrc_t wr = make_rsrc(w + (nrows > 0 ? j0 : 0) * row_bytes, (uint32_t)(nrows * row_bytes));
+  // x rows wid, wid + KW, ... (empty buffers past s: zeros; reads past m: zeros)
+  rsrc_t xr[XPW];
+#pragma unroll
+  for (int u = 0; u < XPW; ++u) {
+    const int r = wid + KW * u;
+    xr[u] = make_rsrc(x + (int64_t)(r < s ? r : 0) * m, r < s ? (uint32_t)m * 4 : 0u);
+  }
+  const uint32_t cbase = (uint32_t)((m / G) * SB);
+  uint32_t co[NC][4], so[NL];
+#pragma unroll
+  for (int t = 0; t < NC; ++t)
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+      co[t][u] = (uint32_t)((16 * t + 4 * u + (lane >> 4)) * row_bytes) + cbase + 16 * (lane & 15);
+#pragma unroll
+  for (int j = 0; j < NL; ++j) {
+    const int i = lane + 64 * j, row = i / (SPS / 4);
+    so[j] = i < NDW ? (uint32_t)(row * row_bytes) + 4 * (i % (SPS / 4)) : kOutOfRange;
+  }
+
+  struct Slab {
+    u32x4 cq[NC][4];
+    uint32_t sw[NL];
+  };
+  auto load_codes = [&](Slab &sl, int slab) {
+#pragma unroll
+    for (int t = 0; t < NC; ++t)
+#pragma unroll
+      for (int u = 0; u < 4; ++u) sl.cq[t][u] = bload16(wr, co[t][u] + slab * kXSlab);
+#pragma unroll
+    for (int j = 0; j < NL; ++j)
+      sl.sw[j] = __builtin_amdgcn_raw_buffer_load_b32(wr, so[j] + (uint32_t)(slab * SPS), 0, 0);
+  };
+  auto load_x = [&](u32x4 (&xg)[XPW], int slab) {
+    const uint32_t o = (uint32_t)(slab * kXSlab * 4) + 16 * lane;
+#pragma unroll
+    for (int u = 0; u < XPW; ++u) xg[u] = bload16(xr[u], o);
+  };
+  // split this lane's 4 values of each loaded row into hi and lo bf16
+  auto store_x = [&](const u32x4 (&xg)[XPW], int buf) {
+#pragma unroll
+    for (int u = 0; u < XPW; ++u) {
+      uint32_t h0, l0, h1, l1;
+      split2(xg[u].x, xg[u].y, h0, l0);
+      split2(xg[u].z, xg[u].w, h1, l1);
+      const int r = wid + KW * u;
+      *reinterpret_cast<u32x2 *>(&xh[buf][r][4 * lane]) = u32x2{h0, h1};
+      *reinterpret_cast<u32x2 *>(&xl[buf][r][4 * lane]) = u32x2{l0, l1};
+    }
+  };
+
+  f32x4 acc[NC][TR];
+#pragma unroll
+  for (int t = 0; t < NC; ++t)
+#pragma unroll
+    for (int tr = 0; tr < TR; ++tr) acc[t][tr] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+
+  uint8_t *cw = &cs[wid][0][0];
+  uint32_t *sws = &ss[wid][0];
+  auto compute = [&](const Slab &sl, int buf, int slab) {
+#pragma unroll
+    for (int t = 0; t < NC; ++t)
+#pragma unroll
+      for (int u = 0; u < 4; ++u)
+        *reinterpret_cast<u32x4 *>(cw + (16 * t + 4 * u + (lane >> 4)) * kCbRow + 16 * (lane & 15)) =
+            sl.cq[t][u];
+#pragma unroll
+    for (int j = 0; j < NL; ++j)
+      if (lane + 64 * j < NDW) sws[lane + 64 * j] = sl.sw[j];
+#pragma unroll
+    for (int g = 0; g < 8 / KPG; ++g) {
+      // scale group g of the slab (k-steps KPG g ..), forced to 0 past m
+      const bool live = slab * kXSlab + 32 * KPG * g < m;
+      float sc[NC];
+#pragma unroll
+      for (int t = 0; t < NC; ++t) {
+        const int byte = (16 * t + c) * SPS + g * SB;
+        const uint32_t wd = sws[byte >> 2];
+        const uint32_t raw = KIND == SCALE_F16 ? (wd >> (8 * (byte & 3))) & 0xffffu : wd;
+        sc[t] = live ? (KIND == SCALE_F16 ? f16_bits_to_f32((uint16_t)raw)
+                                          : __builtin_bit_cast(float, raw))
+                     : 0.0f;
+      }
+      f32x4 d[NC][TR];
+#pragma unroll
+      for (int kk = 0; kk < KPG; ++kk) {
+        const int ks = KPG * g + kk;
+        bf16x8_t ah[TR], al[TR];
+#pragma unroll
+        for (int tr = 0; tr < TR; ++tr) {
+          ah[tr] = *reinterpret_cast<const bf16x8_t *>(&xh[buf][16 * tr + c][32 * ks + 8 * q]);
+          al[tr] = *reinterpret_cast<const bf16x8_t *>(&xl[buf][16 * tr + c][32 * ks + 8 * q]);
+        }
+#pragma unroll
+        for (int t = 0; t < NC; ++t) {
+          const u32x2 qq = *reinterpret_cast<const u32x2 *>(cw + (16 * t + c) * kCbRow + 32 * ks + 8 * q);
+          const bf16x8_t bq = codes_to_bf16(qq.x, qq.y);
+#pragma unroll
+          for (int tr = 0; tr < TR; ++tr) {
+            const f32x4 z = {0.0f, 0.0f, 0.0f, 0.0f};
+            f32x4 dd = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah[tr], bq, kk == 0 ? z : d[t][tr], 0, 0, 0);
+            d[t][tr] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al[tr], bq, dd, 0, 0, 0);
+          }
+        }
+      }
+#pragma unroll
+      for (int t = 0; t < NC; ++t)
+#pragma unroll
+        for (int tr = 0; tr < TR; ++tr)
+#pragma unroll
+          for (int v = 0; v < 4; ++v) acc[t][tr][v] = __builtin_fmaf(sc[t], d[t][tr][v], acc[t][tr][v]);
+    }
+  };
+
+  // Slab i uses x buffer i % 2; a buffer is rewritten only after the barrier
+  // that follows every wave's last read of it; an odd last slab is skipped
+  // by a uniform branch that holds no loads.
+  Slab C0, C1;
+  u32x4 X0[XPW], X1[XPW];
+  load_codes(C0, 0);
+  load_x(X0, 0);
+  store_x(X0, 0);
+  load_codes(C1, 1);
+  load_x(X1, 1);
+  __syncthreads();
+  for (int i = 0; i < nslab; i += 2) {
+    compute(C0, 0, i);
+    store_x(X1, 1);
+    __syncthreads();
+    load_codes(C0, i + 2);
+    load_x(X0, i + 2);
+    if (i + 1 < nslab) compute(C1, 1, i + 1);
+    store_x(X0, 0);
+    __syncthreads();
+    load_codes(C1, i + 3);
+    load_x(X1, i + 3);
+  }
+
+  // D layout of v_mfma_f32_16x16x32: lane -> weight row lane % 16, element
+  // v -> batch row 4 (lane / 16) + v
+#pragma unroll
+  for (int t = 0; t < NC; ++t) {
+    const int64_t j = j0 + 16 * t + c;
+    if (j < n) {
+#pragma unroll
+      for (int tr = 0; tr < TR; ++tr)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+          const int bb = 16 * tr + 4 * q + v;
+          if (bb < s) y[(int64_t)bb * n + j] = acc[t][tr][v];
+        }
+    }
+  }
+}
+
+template <int G, int KIND, int TR, int NC, int KW>
+hipError_t launch_x(const LinearArgs &a, hipStream_t st) {
+  const int64_t blocks = (a.n + 16 * NC * KW - 1) / (16 * NC * KW);
+  const int nslab = (int)((a.m + kXSlab - 1) / kXSlab);
+  hipLaunchKernelGGL((skinny_x_kernel<G, KIND, TR, NC, KW>), dim3((unsigned)blocks),
+                     dim3(64 * KW), 0, st, a.w, a.row_bytes, static_cast<const float *>(a.x),
+                     a.y, (int)a.s, (int)a.m, a.n, nslab);
+  return hipGetLastError();
+}
+
 template <int G, int KIND, int NC, int TR, int KW>
 hipError_t launch_nc(const LinearArgs &a, hipStream_t st) {
   const int64_t blocks = (a.n + 16 * NC - 1) / (16 * NC);
@@ -319,7 +529,14 @@ hipError_t launch_tr(const LinearArgs &a, hipStream_t st) {
 
 template <int G, int KIND>
 hipError_t launch_g(const LinearArgs &a, hipStream_t st) {
-  if (a.s <= 16) return launch_tr<G, KIND, 1>(a, st);
+  // Shared x where the matrix gives it enough workgroups (one 16-row tile
+  // per wave, 64 rows per workgroup, from n = 16384; with two row tiles,
+  // 256 rows per 8-wave workgroup, vocabulary-sized matrices only).
+  if (a.s <= 16) {
+    if (a.n >= 16384) return launch_x<G, KIND, 1, 1, 4>(a, st);
+    return launch_tr<G, KIND, 1>(a, st);
+  }
+  if (a.n >= 65536) return launch_x<G, KIND, 2, 2, 8>(a, st);
   return launch_tr<G, KIND, 2>(a, st);
 }
 

@@ -142,15 +142,15 @@ def test_linear_matches_closed_form(ctx, cor, G, scale, n, m, s):
 
 @pytest.mark.parametrize("G,scale,n,m", [(32, "f32", 4099, 640), (32, "f32", 16386, 640),
                                          (64, "f16", 8195, 1536), (32, "f32", 24, 12288),
-                                         (64, "f16", 16384, 512), (64, "f16", 16400, 1536)])
-@pytest.mark.parametrize("s", [2, 4, 6, 7, 8])
+                                         (64, "f16", 16384, 512), (64, "f16", 16400, 1536),
+                                         (32, "f32", 65600, 1024)])
+@pytest.mark.parametrize("s", [2, 4, 6, 7, 8, 16, 23])
 def test_few_rows_ragged(ctx, cor, G, scale, n, m, s):
-    """2 <= s <= 8 rows (the f32 4x4-block kernels up to 4 rows: K split
-    over the waves below n = 16384, shared x from there; the split bf16
-    kernel above): ragged weight-row blocks (n not a multiple of the
-    block's rows, whole waves past n), K ending inside a 256-code slab, odd
-    and even slab counts, long K; the error stays at f32 accumulation
-    level."""
+    """2 <= s <= 23 rows (the f32 4x4-block kernels up to 4 rows, the split
+    bf16 kernels above; K split over the waves below n = 16384, shared x
+    from there): ragged weight-row blocks (n not a multiple of the block's
+    rows, whole waves past n), K ending inside a 256-code slab, odd and even
+    slab counts, long K; the error stays at f32 accumulation level."""
     say("few rows", G, scale, n, m, s)
     wb = synth_weights_bf16(n, m, seed=n + s)
     pk = cor.pack_bf16(wb, G, scale)
