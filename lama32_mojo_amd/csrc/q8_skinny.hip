@@ -315,12 +315,20 @@ constexpr int kXSlab = 256;                // codes of a row per slab
 constexpr int kXbRow = kXSlab + 8;         // LDS bf16 per staged x row
 constexpr int kCbRow = kXSlab + 16;        // LDS bytes per staged code row
 
+// Narrow matrices split K over KS workgroups per row block (slabs
+// [k spk, (k + 1) spk) for workgroup k): each writes its partial tile to ws
+// with device-scope stores, waits for them and counts itself in cnt[row
+// block]; the last to arrive adds the KS partials in order 0 .. KS-1 (so
+// the result does not depend on arrival order), stores y and resets the
+// counter.  No workgroup waits for another.
 template <int G, int KIND, int TR, int NC, int KW>
 __global__ __launch_bounds__(64 * KW) void skinny_x_kernel(const uint8_t *__restrict__ w,
                                                            int64_t row_bytes,
                                                            const float *__restrict__ x,
                                                            float *__restrict__ y, int s, int m,
-                                                           int64_t n, int nslab) {
+                                                           int64_t n, int nslab, int ks_n,
+                                                           int spk, float *__restrict__ ws,
+                                                           int *__restrict__ cnt) {
   constexpr int SB = ScaleTraits<KIND>::bytes;
   constexpr int XR = 16 * TR;                  // staged x rows
   static_assert(XR % KW == 0, "x rows split evenly over the waves");
@@ -334,11 +342,16 @@ __global__ __launch_bounds__(64 * KW) void skinny_x_kernel(const uint8_t *__rest
   __shared__ __attribute__((aligned(16))) uint8_t cs[KW][NC * 16][kCbRow];
   __shared__ uint32_t ss[KW][NDW];
 
+  constexpr int ROWS = 16 * NC * KW;           // weight rows of a workgroup
   const int lane = threadIdx.x & 63;
   const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int c = lane & 15, q = lane >> 4;
+  const int rb = (int)blockIdx.x / ks_n, kp = (int)blockIdx.x % ks_n;
+  // this workgroup's slabs [sb, sb + ns)
+  const int sb = kp * spk;
+  const int ns = nslab - sb < spk ? nslab - sb : spk;
   // this wave's rows [j0, j0 + 16 NC); a wave past n reads zeros
-  const int64_t j0 = ((int64_t)blockIdx.x * KW + wid) * 16 * NC;
+  const int64_t j0 = ((int64_t)rb * KW + wid) * 16 * NC;
   const int64_t nrows = n - j0 < 0 ? 0 : n - j0 < 16 * NC ? n - j0 : 16 * NC;
   const rsrc_t wr = make_rsrc(w + (nrows > 0 ? j0 : 0) * row_bytes, (uint32_t)(nrows * row_bytes));
   // x rows wid, wid + KW, ... (empty buffers past s: zeros; reads past m: zeros)
@@ -460,49 +473,93 @@ __global__ __launch_bounds__(64 * KW) void skinny_x_kernel(const uint8_t *__rest
   // by a uniform branch that holds no loads.
   Slab C0, C1;
   u32x4 X0[XPW], X1[XPW];
-  load_codes(C0, 0);
-  load_x(X0, 0);
+  load_codes(C0, sb);
+  load_x(X0, sb);
   store_x(X0, 0);
-  load_codes(C1, 1);
-  load_x(X1, 1);
+  load_codes(C1, sb + 1);
+  load_x(X1, sb + 1);
   __syncthreads();
-  for (int i = 0; i < nslab; i += 2) {
-    compute(C0, 0, i);
+  for (int i = 0; i < ns; i += 2) {
+    compute(C0, 0, sb + i);
     store_x(X1, 1);
     __syncthreads();
-    load_codes(C0, i + 2);
-    load_x(X0, i + 2);
-    if (i + 1 < nslab) compute(C1, 1, i + 1);
+    load_codes(C0, sb + i + 2);
+    load_x(X0, sb + i + 2);
+    if (i + 1 < ns) compute(C1, 1, sb + i + 1);
     store_x(X0, 0);
     __syncthreads();
-    load_codes(C1, i + 3);
-    load_x(X1, i + 3);
+    load_codes(C1, sb + i + 3);
+    load_x(X1, sb + i + 3);
   }
 
   // D layout of v_mfma_f32_16x16x32: lane -> weight row lane % 16, element
   // v -> batch row 4 (lane / 16) + v
+  if (ks_n == 1) {
 #pragma unroll
-  for (int t = 0; t < NC; ++t) {
-    const int64_t j = j0 + 16 * t + c;
-    if (j < n) {
+    for (int t = 0; t < NC; ++t) {
+      const int64_t j = j0 + 16 * t + c;
+      if (j < n) {
 #pragma unroll
-      for (int tr = 0; tr < TR; ++tr)
+        for (int tr = 0; tr < TR; ++tr)
 #pragma unroll
-        for (int v = 0; v < 4; ++v) {
-          const int bb = 16 * tr + 4 * q + v;
-          if (bb < s) y[(int64_t)bb * n + j] = acc[t][tr][v];
-        }
+          for (int v = 0; v < 4; ++v) {
+            const int bb = 16 * tr + 4 * q + v;
+            if (bb < s) y[(int64_t)bb * n + j] = acc[t][tr][v];
+          }
+      }
     }
+    return;
   }
+  // partial tile [XR batch rows][ROWS weight rows] of this workgroup
+  constexpr int PT = XR * ROWS;
+  float *part = ws + ((int64_t)rb * ks_n + kp) * PT;
+#pragma unroll
+  for (int t = 0; t < NC; ++t)
+#pragma unroll
+    for (int tr = 0; tr < TR; ++tr)
+#pragma unroll
+      for (int v = 0; v < 4; ++v)
+        __hip_atomic_store(&part[(16 * tr + 4 * q + v) * ROWS + wid * 16 * NC + 16 * t + c],
+                           acc[t][tr][v], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  // every wave's partial stores have completed before the workgroup counts
+  // itself
+  __builtin_amdgcn_s_waitcnt(0);
+  __shared__ int last;
+  __syncthreads();
+  if (threadIdx.x == 0)
+    last = __hip_atomic_fetch_add(&cnt[rb], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+           ks_n - 1;
+  __syncthreads();
+  if (!last) return;
+  const float *p0 = ws + (int64_t)rb * ks_n * PT;
+  const int64_t r0 = (int64_t)rb * ROWS;
+  for (int o = threadIdx.x; o < PT; o += 64 * KW) {
+    float sum = 0.0f;
+    for (int k = 0; k < ks_n; ++k)
+      sum += __hip_atomic_load(&p0[(int64_t)k * PT + o], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const int bb = o / ROWS;
+    const int64_t j = r0 + o % ROWS;
+    if (bb < s && j < n) y[(int64_t)bb * n + j] = sum;
+  }
+  if (threadIdx.x == 0) __hip_atomic_store(&cnt[rb], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// Row blocks of 16 NC KW weight rows; with ks_n > 1 each is split over
+// ks_n workgroups of spk slabs (needs a workspace and counters).
 template <int G, int KIND, int TR, int NC, int KW>
-hipError_t launch_x(const LinearArgs &a, hipStream_t st) {
-  const int64_t blocks = (a.n + 16 * NC * KW - 1) / (16 * NC * KW);
+hipError_t launch_x(const LinearArgs &a, int ks_n, hipStream_t st) {
+  constexpr int ROWS = 16 * NC * KW;
+  const int64_t nrb = (a.n + ROWS - 1) / ROWS;
   const int nslab = (int)((a.m + kXSlab - 1) / kXSlab);
-  hipLaunchKernelGGL((skinny_x_kernel<G, KIND, TR, NC, KW>), dim3((unsigned)blocks),
+  if (ks_n > nslab) ks_n = nslab;
+  if (ks_n > 1 && (!a.ws || !a.cnt || nrb > a.cnt_n ||
+                   nrb * ks_n * (16 * TR) * ROWS > a.ws_floats))
+    ks_n = 1;
+  const int spk = (nslab + ks_n - 1) / ks_n;
+  ks_n = (nslab + spk - 1) / spk;   // no empty split
+  hipLaunchKernelGGL((skinny_x_kernel<G, KIND, TR, NC, KW>), dim3((unsigned)(nrb * ks_n)),
                      dim3(64 * KW), 0, st, a.w, a.row_bytes, static_cast<const float *>(a.x),
-                     a.y, (int)a.s, (int)a.m, a.n, nslab);
+                     a.y, (int)a.s, (int)a.m, a.n, nslab, ks_n, spk, a.ws, a.cnt);
   return hipGetLastError();
 }
 
@@ -531,12 +588,18 @@ template <int G, int KIND>
 hipError_t launch_g(const LinearArgs &a, hipStream_t st) {
   // Shared x where the matrix gives it enough workgroups (one 16-row tile
   // per wave, 64 rows per workgroup, from n = 16384; with two row tiles,
-  // 256 rows per 8-wave workgroup, vocabulary-sized matrices only).
+  // 256 rows per 8-wave workgroup, vocabulary-sized matrices only), or where
+  // long rows let K be split over workgroups.
   if (a.s <= 16) {
-    if (a.n >= 16384) return launch_x<G, KIND, 1, 1, 4>(a, st);
+    if (a.n >= 16384) return launch_x<G, KIND, 1, 1, 4>(a, 1, st);
+    // long rows: K split over workgroups of 64 rows, about 256 in all
+    if (a.m >= 8192) {
+      const int64_t nrb = (a.n + 63) / 64;
+      return launch_x<G, KIND, 1, 1, 4>(a, (int)((256 + nrb - 1) / nrb), st);
+    }
     return launch_tr<G, KIND, 1>(a, st);
   }
-  if (a.n >= 65536) return launch_x<G, KIND, 2, 2, 8>(a, st);
+  if (a.n >= 65536) return launch_x<G, KIND, 2, 2, 8>(a, 1, st);
   return launch_tr<G, KIND, 2>(a, st);
 }
 

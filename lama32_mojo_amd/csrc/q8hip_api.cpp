@@ -31,6 +31,9 @@ struct q8_ctx {
   // The decode attention's partial records use it too: both run in stream
   // order on this context.
   float *gemm_ws = nullptr;
+  // Arrival counters of the small-batch kernels' cross-workgroup K splits
+  // (zeroed at creation; the last workgroup of a row block resets its own).
+  int *kcount = nullptr;
   // Binary16 copy of the activation rows of a prefill GEMM and their
   // power-of-two factors (launch_gemm); longer inputs run in row chunks.
   void *act16 = nullptr;
@@ -43,6 +46,7 @@ struct q8_ctx {
 namespace {
 constexpr int64_t kGemmWsFloats = (int64_t)4 << 20;
 constexpr int64_t kAct16Bytes = (int64_t)64 << 20;
+constexpr int64_t kCountInts = (int64_t)1 << 16;
 }
 
 struct q8_buf {
@@ -158,8 +162,13 @@ int q8_create(int device_ordinal, q8_ctx **out) {
     // Split-K workspace of the prefill GEMM, allocated up front so that
     // calls captured into HIP graphs can use it too.
     if (hipMalloc(&ctx->gemm_ws, kGemmWsFloats * sizeof(float)) != hipSuccess ||
-        hipMalloc(&ctx->act16, kAct16Bytes) != hipSuccess) {
+        hipMalloc(&ctx->act16, kAct16Bytes) != hipSuccess ||
+        hipMalloc(&ctx->kcount, kCountInts * sizeof(int)) != hipSuccess ||
+        hipMemset(ctx->kcount, 0, kCountInts * sizeof(int)) != hipSuccess ||
+        hipDeviceSynchronize() != hipSuccess) {
       if (ctx->gemm_ws) (void)hipFree(ctx->gemm_ws);
+      if (ctx->act16) (void)hipFree(ctx->act16);
+      if (ctx->kcount) (void)hipFree(ctx->kcount);
       (void)hipStreamDestroy(ctx->own);
       delete ctx;
       return fail(nullptr, Q8_ERR_NOMEM, "q8_create: cannot allocate the GEMM workspace");
@@ -180,6 +189,7 @@ void q8_destroy(q8_ctx *ctx) {
     }
     if (ctx->gemm_ws) (void)hipFree(ctx->gemm_ws);
     if (ctx->act16) (void)hipFree(ctx->act16);
+    if (ctx->kcount) (void)hipFree(ctx->kcount);
     if (ctx->stage) (void)hipHostFree(ctx->stage);
     for (hipEvent_t &ev : ctx->stage_ev)
       if (ev) (void)hipEventDestroy(ev);
@@ -484,6 +494,9 @@ int q8_linear(q8_ctx *ctx, q8_buf *w, uint64_t owt_u16, q8_buf *a, uint64_t ox_f
   } else if (s >= kSkinnyMinRows && s <= q8::kSkinny4MaxRows && gemm_aligned(la)) {
     e = q8::launch_skinny4(la, ctx->stream);
   } else if (s >= kSkinnyMinRows && gemm_aligned(la)) {
+    attach_gemm_workspace(ctx, la);
+    la.cnt = ctx->kcount;
+    la.cnt_n = kCountInts;
     e = q8::launch_skinny(la, ctx->stream);
   } else {
     e = q8::launch_gemv(la, ctx->stream);

@@ -212,6 +212,30 @@ def test_linear_all_ones_gives_row_sums(ctx, cor, G, scale, s):
     assert np.all(y == y[:, :1])
 
 
+@pytest.mark.parametrize("s,n,m", [(16, 4096, 12288), (8, 24, 12288), (6, 2000, 8192)])
+def test_split_k_across_workgroups_repeats_bitwise(ctx, cor, s, n, m):
+    """Long rows at 5..16 activation rows split K over workgroups whose
+    partials the last to arrive adds in a fixed order: repeated calls give
+    the same bits (the arrival counters reset themselves) and match the
+    closed form."""
+    say("split-K repeats", s, n, m)
+    G, scale = 32, "f32"
+    pk = cor.pack_bf16(synth_weights_bf16(n, m, seed=60 + s), G, scale)
+    x = synth_x(s, m, seed=61)
+    w = upload(ctx, pk)
+    a = ctx.alloc(4 * (s * m + s * n))
+    a.upload(np.ascontiguousarray(x, dtype=np.float32))
+    ys = []
+    for _ in range(4):
+        q8hip.linear(ctx, w, 0, a, 0, s * m, s, m, n, G, scale)
+        ys.append(a.download((s, n), np.float32, 4 * s * m))
+    w.free()
+    a.free()
+    for y in ys[1:]:
+        assert np.array_equal(y, ys[0])
+    assert max_rel_err(ys[0], cor.linear_f64(pk, x, G, scale)) <= 1e-5
+
+
 def test_linear_zero_input(ctx, cor):
     pk = cor.pack_bf16(synth_weights_bf16(300, 512, seed=32))
     y = gpu_linear(ctx, pk, np.zeros((2, 512), np.float32), 64, "f16")
