@@ -492,8 +492,10 @@ __device__ __forceinline__ float lane_group_sum(float v) {
 //
 // Every block rotates q and the new k itself and takes cache row pos0 from
 // LDS (rounded to binary16 exactly as cached); split 0 writes the new k and
-// v to cache row pos0, and no block reads that row from memory.  The first
-// chunk's loads are issued before the rotation.
+// v to cache row pos0, and no block reads that row from memory.  Every
+// global load of the prologue (q, k, v, frequencies, norm weights) and the
+// first chunk's loads are issued before the position is read, so the
+// prologue waits for one round trip, not one per dependent load.
 template <int HD, int GRP>
 __global__ __launch_bounds__(256) void attn_decode_kernel(
     const float *__restrict__ q, const float *__restrict__ k, const float *__restrict__ v,
@@ -538,6 +540,51 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(
       for (int u = 0; u < NI; ++u) vr[u] = bload16(vrs, row_off(cc * KC + u * RPI + rl));
     }
   };
+  // Prologue inputs, all issued ahead of the first chunk so that one wait
+  // covers them: thread t's query pairs (d, half + d) of RoPE items
+  // t + 256 r, the new k pair (t < half) and v element (t < HD), the inverse
+  // frequencies, the norm weights (zeros when absent) and the two halves of
+  // the rows whose squares this wave sums for the per-head norms.
+  constexpr int NQ = (GRP * half + 255) / 256;   // RoPE items per thread
+  constexpr int NR = (GRP + 1 + NW - 1) / NW;    // norm rows per wave
+  const int t = threadIdx.x;
+  const rsrc_t qrs = make_rsrc(q + (int64_t)g * GRP * HD, GRP * HD * 4);
+  const rsrc_t knrs = make_rsrc(k + (int64_t)g * HD, HD * 4);
+  const rsrc_t vnrs = make_rsrc(v + (int64_t)g * HD, HD * 4);
+  const rsrc_t irs = make_rsrc(inv, half * 4);
+  const rsrc_t qwrs = make_rsrc(qnw, qnw ? HD * 2 : 0), kwrs = make_rsrc(knw, knw ? HD * 2 : 0);
+  float qa[NQ], qb[NQ], fq[NQ];
+  uint32_t wqa[NQ], wqb[NQ];
+#pragma unroll
+  for (int r = 0; r < NQ; ++r) {
+    const int idx = t + 256 * r, hh = idx / half, d = idx % half;
+    const bool ok = idx < GRP * half;
+    qa[r] = bload4f(qrs, ok ? (uint32_t)(hh * HD + d) * 4u : kOutOfRange);
+    qb[r] = bload4f(qrs, ok ? (uint32_t)(hh * HD + half + d) * 4u : kOutOfRange);
+    fq[r] = bload4f(irs, (uint32_t)d * 4u);
+    wqa[r] = bload2(qwrs, (uint32_t)d * 2u);
+    wqb[r] = bload2(qwrs, (uint32_t)(half + d) * 2u);
+  }
+  const float ka = bload4f(knrs, t < half ? (uint32_t)t * 4u : kOutOfRange);
+  const float kb = bload4f(knrs, t < half ? (uint32_t)(half + t) * 4u : kOutOfRange);
+  const uint32_t wka = bload2(kwrs, t < half ? (uint32_t)t * 2u : kOutOfRange);
+  const uint32_t wkb = bload2(kwrs, t < half ? (uint32_t)(half + t) * 2u : kOutOfRange);
+  const float vv = bload4f(vnrs, t < HD ? (uint32_t)t * 4u : kOutOfRange);
+  float na[NR], nb[NR];
+#pragma unroll
+  for (int x = 0; x < NR; ++x) {
+    const int r = w + NW * x;          // q rows 0 .. GRP-1, then the k row
+    const uint32_t o0 = (uint32_t)lane * 4u, o1 = (uint32_t)(64 + lane) * 4u;
+    const float q0 = bload4f(qrs, r < GRP ? (uint32_t)(r * HD) * 4u + o0 : kOutOfRange);
+    const float k0 = bload4f(knrs, r == GRP ? o0 : kOutOfRange);
+    na[x] = r < GRP ? q0 : k0;
+    nb[x] = 0.0f;
+    if constexpr (HD == 128) {
+      const float q1 = bload4f(qrs, r < GRP ? (uint32_t)(r * HD) * 4u + o1 : kOutOfRange);
+      const float k1 = bload4f(knrs, r == GRP ? o1 : kOutOfRange);
+      nb[x] = r < GRP ? q1 : k1;
+    }
+  }
   // The first chunk is loaded before the position is known, on the guess
   // that the block spans WPH chunks (true while chunks <= nsplit * WPH).
   const int c_guess = split * WPH + kg;
@@ -553,64 +600,70 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(
   const int c_end = min((split + 1) * cpb, chunks);
   int c = split * cpb + kg;
   if (c != c_guess && c < c_end) load_chunk(c, true);
-  // row r as read, with rows past the context zeroed and row pos0 from LDS
-  auto fix_row = [&](u32x4 raw, const __half *fresh, int r) -> u32x4 {
-    if (r == pos0) return *reinterpret_cast<const u32x4 *>(fresh + dd);
-    return r < nctx ? raw : u32x4{0u, 0u, 0u, 0u};
+  // row r as read, with rows past the context zeroed and row pos0 replaced
+  // by this lane's 8 dims of the new row (selects, no branch)
+  auto fix_row = [&](u32x4 raw, u32x4 fresh, int r) -> u32x4 {
+    const bool keep = r < nctx, mine = r == pos0;
+    u32x4 o;
+    o.x = mine ? fresh.x : keep ? raw.x : 0u;
+    o.y = mine ? fresh.y : keep ? raw.y : 0u;
+    o.z = mine ? fresh.z : keep ? raw.z : 0u;
+    o.w = mine ? fresh.w : keep ? raw.w : 0u;
+    return o;
   };
 
-  // prologue: per-head RMSNorm of q and the new k when norm weights are
-  // given (k_rmsnorm2_w: one wave per head, the row's two 64-element halves
-  // summed as block_sum256 sums them in q8_rmsnorm, so the normalised values
-  // are the same bits), then RoPE of the group's query heads and the new k;
+  // per-head RMSNorm factors of q and the new k when norm weights are given
+  // (k_rmsnorm2_w: one wave per row, the row's two 64-element halves summed
+  // as block_sum256 sums them in q8_rmsnorm, so the normalised values are
+  // the same bits), then RoPE of the group's query heads and the new k;
   // round k, v
-  if (qnw) {
-    for (int r = w; r < GRP + 1; r += NW) {
-      const float *src = r < GRP ? q + (g * GRP + r) * HD : k + g * HD;
-      const float a0 = src[lane];
-      float ss = wave_sum(a0 * a0);
-      if constexpr (HD == 128) {
-        const float a1 = src[64 + lane];
-        ss = ss + wave_sum(a1 * a1);
+  if (qnw || knw) {
+#pragma unroll
+    for (int x = 0; x < NR; ++x) {
+      const int r = w + NW * x;
+      if (r < GRP + 1) {
+        float ss = wave_sum(na[x] * na[x]);
+        if constexpr (HD == 128) ss = ss + wave_sum(nb[x] * nb[x]);
+        if (lane == 0) hinv[r] = 1.0f / sqrtf(ss / (float)HD + eps);
       }
-      if (lane == 0) hinv[r] = 1.0f / sqrtf(ss / (float)HD + eps);
     }
     __syncthreads();
   }
-  auto qval = [&](int hh, int d) -> float {
-    const float x = q[(g * GRP + hh) * HD + d];
-    return qnw ? bf16_bits_to_f32(qnw[d]) * x * hinv[hh] : x;
-  };
-  auto kval = [&](int d) -> float {
-    const float x = k[g * HD + d];
-    return knw ? bf16_bits_to_f32(knw[d]) * x * hinv[GRP] : x;
-  };
-  for (int t = threadIdx.x; t < GRP * half; t += 256) {
-    const int hh = t / half, d = t % half;
-    float cs, sn;
-    rope_cs((float)pos0 * inv[d], cs, sn);
-    rotate(qval(hh, d), qval(hh, half + d), cs, sn, qs[hh][d], qs[hh][half + d]);
-  }
-  for (int d = threadIdx.x; d < half; d += 256) {
-    float cs, sn, r0, r1;
-    rope_cs((float)pos0 * inv[d], cs, sn);
-    rotate(kval(d), kval(half + d), cs, sn, r0, r1);
-    const __half y0 = __float2half_rn(r0), y1 = __float2half_rn(r1);
-    kn[d] = y0;
-    kn[half + d] = y1;
-    if (room && split == 0) {
-      kc[(int64_t)pos0 * kvdim + g * HD + d] = y0;
-      kc[(int64_t)pos0 * kvdim + g * HD + half + d] = y1;
+#pragma unroll
+  for (int r = 0; r < NQ; ++r) {
+    const int idx = t + 256 * r, hh = idx / half, d = idx % half;
+    if (idx < GRP * half) {
+      float cs, sn;
+      rope_cs((float)pos0 * fq[r], cs, sn);
+      const float x0 = qnw ? bf16_bits_to_f32(wqa[r]) * qa[r] * hinv[hh] : qa[r];
+      const float x1 = qnw ? bf16_bits_to_f32(wqb[r]) * qb[r] * hinv[hh] : qb[r];
+      rotate(x0, x1, cs, sn, qs[hh][d], qs[hh][half + d]);
     }
   }
-  for (int d = threadIdx.x; d < HD; d += 256) {
-    const __half y = __float2half_rn(v[g * HD + d]);
-    vn[d] = y;
-    if (room && split == 0) vc[(int64_t)pos0 * kvdim + g * HD + d] = y;
+  if (t < half) {                      // inv[t] is fq[0] here (item t < half)
+    float cs, sn, r0, r1;
+    rope_cs((float)pos0 * fq[0], cs, sn);
+    const float x0 = knw ? bf16_bits_to_f32(wka) * ka * hinv[GRP] : ka;
+    const float x1 = knw ? bf16_bits_to_f32(wkb) * kb * hinv[GRP] : kb;
+    rotate(x0, x1, cs, sn, r0, r1);
+    const __half y0 = __float2half_rn(r0), y1 = __float2half_rn(r1);
+    kn[t] = y0;
+    kn[half + t] = y1;
+    if (room && split == 0) {
+      kc[(int64_t)pos0 * kvdim + g * HD + t] = y0;
+      kc[(int64_t)pos0 * kvdim + g * HD + half + t] = y1;
+    }
+  }
+  if (t < HD) {
+    const __half y = __float2half_rn(vv);
+    vn[t] = y;
+    if (room && split == 0) vc[(int64_t)pos0 * kvdim + g * HD + t] = y;
   }
   __syncthreads();
 
   const float rd = sqrtf((float)HD);
+  const u32x4 kfresh = *reinterpret_cast<const u32x4 *>(kn + dd);
+  const u32x4 vfresh = *reinterpret_cast<const u32x4 *>(vn + dd);
   float qv[HPW][8];
 #pragma unroll
   for (int j = 0; j < HPW; ++j)
@@ -630,7 +683,7 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(
     // scores of the chunk's rows
 #pragma unroll
     for (int u = 0; u < NI; ++u) {
-      const u32x4 kw = fix_row(kr[u], kn, j0 + u * RPI + rl);
+      const u32x4 kw = fix_row(kr[u], kfresh, j0 + u * RPI + rl);
       const uint32_t rw[4] = {kw.x, kw.y, kw.z, kw.w};
 #pragma unroll
       for (int j = 0; j < HPW; ++j) {
@@ -641,8 +694,9 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(
           dot = __builtin_fmaf(qv[j][2 * i], kf.x, dot);
           dot = __builtin_fmaf(qv[j][2 * i + 1], kf.y, dot);
         }
-        dot = lane_group_sum<LPR>(dot);
-        if (lane % LPR == 0) ps[w][j][u * RPI + rl] = dot / rd;
+        // every lane of the row holds the same sum: all store it (one
+        // address per row); the scale is applied below, one key per lane
+        ps[w][j][u * RPI + rl] = lane_group_sum<LPR>(dot);
       }
     }
     const int cn = c + WPH;             // this wave's next chunk
@@ -653,7 +707,7 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(
     float pnew[HPW], fa[HPW];
 #pragma unroll
     for (int j = 0; j < HPW; ++j) {
-      const float sc = key_ok ? ps[w][j][lane] : -INFINITY;
+      const float sc = key_ok ? ps[w][j][lane] / rd : -INFINITY;
       const float mx = wave_max(sc);
       const float p = key_ok ? expf(sc - mx) : 0.0f;
       const float l = wave_sum(p);
@@ -675,7 +729,7 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(
       for (int i = 0; i < 8; ++i) o_run[j][i] *= fa[j];
 #pragma unroll
     for (int u = 0; u < NI; ++u) {
-      const u32x4 vw = fix_row(vr[u], vn, j0 + u * RPI + rl);
+      const u32x4 vw = fix_row(vr[u], vfresh, j0 + u * RPI + rl);
       const uint32_t rw[4] = {vw.x, vw.y, vw.z, vw.w};
 #pragma unroll
       for (int j = 0; j < HPW; ++j) {
@@ -760,19 +814,22 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(const float *__restrict
   __shared__ float fac[kDecodeAttnMaxSplit];
   __shared__ float lsum;
   const int h = blockIdx.x, g = h / GRP, hh = h % GRP;
-  const float *recs = part + (int64_t)g * nsplit * (GRP * PR) + hh * PR;
-  // batches of 8 independent loads per thread, then the LDS stores
-  for (int t0 = threadIdx.x; t0 < nsplit * PR; t0 += 256 * 8) {
-    float r[8];
+  // every load of the head's records issued at once (offsets past the
+  // records read as zeros), then the LDS stores
+  constexpr int NB = (kDecodeAttnMaxSplit * PR + 255) / 256;
+  const int total = nsplit * PR;
+  const rsrc_t prs = make_rsrc(part + (int64_t)g * nsplit * (GRP * PR),
+                               (uint32_t)(nsplit * GRP * PR) * 4u);
+  float r[NB];
 #pragma unroll
-    for (int u = 0; u < 8; ++u) {
-      const int t = t0 + 256 * u;
-      r[u] = t < nsplit * PR ? recs[(t / PR) * GRP * PR + t % PR] : 0.0f;
-    }
-#pragma unroll
-    for (int u = 0; u < 8; ++u)
-      if (t0 + 256 * u < nsplit * PR) rs[t0 + 256 * u] = r[u];
+  for (int u = 0; u < NB; ++u) {
+    const int t = threadIdx.x + 256 * u;
+    r[u] = bload4f(prs, t < total ? (uint32_t)((t / PR) * GRP * PR + hh * PR + t % PR) * 4u
+                                  : kOutOfRange);
   }
+#pragma unroll
+  for (int u = 0; u < NB; ++u)
+    if (threadIdx.x + 256 * u < total) rs[threadIdx.x + 256 * u] = r[u];
   const int pos0 = posp ? *posp : pos0_host;
   const int nctx = pos0 < maxlen ? pos0 + 1 : maxlen;
   const int chunks = (nctx + KC - 1) / KC;
