@@ -139,15 +139,26 @@ struct DecodeAttnArgs {
 // 0 .. pos0: one launch of nsplit x nkv blocks over
 // context splits, then a merge launch.  Calls that share `part` must not
 // overlap.
-// Keys per chunk (one wave's unit of work) and the split count: one chunk
-// per block up to 32 chunks of context, then more chunks per block.  Every
-// launched block reads the position before it can leave, so more splits
-// than that cost more than they save (measured at 1024 and 2304 keys).
+// Keys per chunk (one wave's unit of work), head slots of a block of 4 waves
+// and the split count.  Head slots: heads per wave GRP / slots, waves per
+// head 4 / slots.  With 64-dim heads (short rows, contexts of a chunk or so
+// per block) one head per wave; with 128-dim heads in groups of 4 or 8 a
+// wave serves 4 heads, so the K/V rows of a chunk are loaded once and the
+// block's waves work on different chunks (measured on the Llama-3.1-8B step
+// at 2300 cached tokens; slower on the 1B step).  Splits: one chunk per wave
+// (blocks of 4 / slots chunks) up to 32 blocks per KV head, then more chunks
+// per block.  Every launched block reads the position before it can leave
+// and a launch of 256 blocks takes about 1.4 us to start them all, so the
+// grid holds no more blocks than the longest context keeps busy.
 constexpr int kDecodeAttnMaxSplit = 64;   // bound of the merge's LDS staging
 constexpr int decode_attn_chunk(int head_dim) { return head_dim > 64 ? 32 : 64; }
-inline int decode_attn_nsplit(int64_t maxlen, int head_dim) {
+constexpr int decode_head_slots(int hd, int grp) {
+  return (hd >= 128 && grp >= 4) ? grp / 4 : (grp < 4 ? grp : 4);
+}
+inline int decode_attn_nsplit(int64_t maxlen, int head_dim, int grp) {
   const int64_t kc = decode_attn_chunk(head_dim);
-  const int64_t n = (maxlen + kc - 1) / kc;
+  const int64_t wph = 4 / decode_head_slots(head_dim, grp);
+  const int64_t n = ((maxlen + kc - 1) / kc + wph - 1) / wph;
   return (int)(n < 1 ? 1 : n > 32 ? 32 : n);
 }
 hipError_t launch_decode_attention(const DecodeAttnArgs &a, hipStream_t st);

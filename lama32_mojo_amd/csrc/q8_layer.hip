@@ -455,16 +455,9 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(const float *__restri
 }
 
 // ---- decode attention: RoPE + KV append + attention of one new token --------
-// Head slots of a decode-attention block of 4 waves (heads per wave
-// GRP / slots, waves per head 4 / slots).  With 64-dim heads (short rows,
-// contexts of a chunk or so per block) one head per wave; with 128-dim heads
-// in groups of 4 or 8 a wave serves 4 heads, so the K/V rows of a chunk are
-// loaded once and the block's waves work on different chunks (measured on
-// the Llama-3.1-8B step at 2300 cached tokens; slower on the 1B step).  The
-// merge kernel derives the active splits from the same value.
-constexpr int decode_head_slots(int hd, int grp) {
-  return (hd >= 128 && grp >= 4) ? grp / 4 : (grp < 4 ? grp : 4);
-}
+// (chunk, head slots and split count: decode_attn_chunk, decode_head_slots
+// and decode_attn_nsplit; the merge kernel derives the active splits from
+// the same values)
 
 // Sum over aligned groups of N consecutive lanes (N = 8 or 16), in every lane.
 template <int N>
@@ -763,32 +756,43 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(
     }
   }
   __syncthreads();
-  // the block's waves of each head -> one record per head
-  float *rec = part + ((int64_t)g * nsplit + split) * (GRP * PR);
-  for (int t = threadIdx.x; t < GRP * HD; t += 256) {
-    const int hh = t / HD, d = t % HD;
+  // per head: the largest running max M of its waves and each wave's factor
+  // exp(m_w - M) (0 for a wave without keys), one thread per (head, wave)
+  __shared__ float wf[NW][HPW], hm[GRP];
+  if (threadIdx.x < GRP * WPH) {
+    const int hh = threadIdx.x / WPH, x0 = threadIdx.x % WPH;
     const int s0 = hh % HS, j = hh / HS;       // waves s0 + HS * x serve head hh
     float mx = -INFINITY;
 #pragma unroll
     for (int x = 0; x < WPH; ++x) mx = fmaxf(mx, wm[s0 + HS * x][j]);
-    float l = 0.0f, o = 0.0f;
+    const int wx = s0 + HS * x0;
+    wf[wx][j] = wl[wx][j] != 0.0f ? expf(wm[wx][j] - mx) : 0.0f;
+    if (x0 == 0) hm[hh] = mx;
+  }
+  __syncthreads();
+  // the block's waves of each head -> one record per head: o = sum_w f_w o_w
+  // and l = sum_w l_w f_w in wave order (a wave without keys adds l_w = 0
+  // times f_w = 0, and its o_w is 0)
+  float *rec = part + ((int64_t)g * nsplit + split) * (GRP * PR);
+  for (int t = threadIdx.x; t < GRP * HD; t += 256) {
+    const int hh = t / HD, d = t % HD;
+    const int s0 = hh % HS, j = hh / HS;
+    float o = 0.0f, l = 0.0f;
 #pragma unroll
     for (int x = 0; x < WPH; ++x) {
       const int wx = s0 + HS * x;
-      if (wl[wx][j] == 0.0f) continue;
       float os = 0.0f;
 #pragma unroll
       for (int r = 0; r < RPI; ++r) os += wo[wx][j][r][d];
-      const float f = expf(wm[wx][j] - mx);
-      l = __builtin_fmaf(wl[wx][j], f, l);
-      o = __builtin_fmaf(os, f, o);
+      o = __builtin_fmaf(os, wf[wx][j], o);
+      l = __builtin_fmaf(wl[wx][j], wf[wx][j], l);
     }
     if (active == 1) {
       out[(g * GRP + hh) * HD + d] = o / l;
     } else {                             // merged by attn_merge_kernel
       rec[hh * PR + d] = o;
       if (d == 0) {
-        rec[hh * PR + HD] = mx;
+        rec[hh * PR + HD] = hm[hh];
         rec[hh * PR + HD + 1] = l;
       }
     }

@@ -927,7 +927,7 @@ int q8_decode_attention(q8_ctx *ctx, q8_buf *a, uint64_t oq_f32, uint64_t ok_f32
     return fail(ctx, Q8_ERR_SHAPE, "q8_decode_attention: maxlen=%lld (a cache block must stay "
                 "under 2 GiB)", (long long)maxlen);
   const uint64_t cn = (uint64_t)maxlen * kn;
-  const int nsplit = q8::decode_attn_nsplit(maxlen, head_dim);
+  const int nsplit = q8::decode_attn_nsplit(maxlen, head_dim, grp);
   if ((uint64_t)nheads * nsplit * (head_dim + 2) > (uint64_t)kGemmWsFloats)
     return fail(ctx, Q8_ERR_UNSUPPORTED, "q8_decode_attention: nheads=%d exceeds the context's "
                 "attention scratch", nheads);
