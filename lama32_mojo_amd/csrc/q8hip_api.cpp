@@ -430,10 +430,12 @@ bool gemm_aligned(const q8::LinearArgs &a) {
 constexpr int64_t kSkinnyMinRows = 2;
 constexpr int64_t kGemmMinRows = 32;
 
-// Attach the context's split-K workspace to a GEMM launch.
+// Attach the context's split-K workspace and arrival counters to a launch.
 void attach_gemm_workspace(q8_ctx *ctx, q8::LinearArgs &la) {
   la.ws = ctx->gemm_ws;
   la.ws_floats = kGemmWsFloats;
+  la.cnt = ctx->kcount;
+  la.cnt_n = kCountInts;
 }
 
 // Prefill GEMM on f16 MFMA through the context's binary16 activation
@@ -495,8 +497,6 @@ int q8_linear(q8_ctx *ctx, q8_buf *w, uint64_t owt_u16, q8_buf *a, uint64_t ox_f
     e = q8::launch_skinny4(la, ctx->stream);
   } else if (s >= kSkinnyMinRows && gemm_aligned(la)) {
     attach_gemm_workspace(ctx, la);
-    la.cnt = ctx->kcount;
-    la.cnt_n = kCountInts;
     e = q8::launch_skinny(la, ctx->stream);
   } else {
     e = q8::launch_gemv(la, ctx->stream);
