@@ -150,7 +150,7 @@ struct DecodeAttnArgs {
 // per block.  Every launched block reads the position before it can leave
 // and a launch of 256 blocks takes about 1.4 us to start them all, so the
 // grid holds no more blocks than the longest context keeps busy.
-constexpr int kDecodeAttnMaxSplit = 64;   // bound of the merge's LDS staging
+constexpr int kDecodeAttnMaxSplit = 32;   // bound of the merge's per-thread loads
 constexpr int decode_attn_chunk(int head_dim) { return head_dim > 64 ? 32 : 64; }
 constexpr int decode_head_slots(int hd, int grp) {
   return (hd >= 128 && grp >= 4) ? grp / 4 : (grp < 4 ? grp : 4);

@@ -799,63 +799,52 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(
   }
 }
 
-// Merge of the partial records of attn_decode_kernel: block h (256 threads)
-// stages head h's records of all nsplit splits in LDS (independent loads,
-// issued before the position is known); one wave forms each active split's
-// factor exp(m_x - M) and the total l = sum_x l_x exp(m_x - M); then thread
-// d < HD forms o[d] = sum_x f_x o_x[d] / l.  Does nothing when one block per
-// KV head was active (it wrote the output itself).
+// Merge of the partial records of attn_decode_kernel: block h (HD threads)
+// serves head h, thread d its output dim d.  Every load is issued before
+// the position is read: lane x takes split x's m and l, thread d split x's
+// o[d] for every split (offsets past the records read as zeros).  Each wave
+// then forms the active splits' factors exp(m_x - M) and l = sum_x l_x f_x
+// itself (wave reductions, no LDS, no barrier), and thread d forms
+// o[d] = sum_x f_x o_x[d] / l with f_x read from lane x.  Does nothing when
+// one block per KV head was active (it wrote the output itself).
 template <int HD, int GRP>
-__global__ __launch_bounds__(256) void attn_merge_kernel(const float *__restrict__ part,
-                                                         float *__restrict__ out, int nsplit,
-                                                         const int *posp, int pos0_host,
-                                                         int maxlen) {
+__global__ __launch_bounds__(HD) void attn_merge_kernel(const float *__restrict__ part,
+                                                        float *__restrict__ out, int nsplit,
+                                                        const int *posp, int pos0_host,
+                                                        int maxlen) {
   constexpr int KC = decode_attn_chunk(HD), NW = 4;
   constexpr int PR = HD + 2;
   constexpr int WPH = NW / decode_head_slots(HD, GRP);   // as attn_decode_kernel
-  static_assert(kDecodeAttnMaxSplit <= 64, "one wave forms the split factors");
-  __shared__ float rs[kDecodeAttnMaxSplit * PR];
-  __shared__ float fac[kDecodeAttnMaxSplit];
-  __shared__ float lsum;
+  constexpr int NX = kDecodeAttnMaxSplit;
+  static_assert(NX <= 64, "one lane per split");
   const int h = blockIdx.x, g = h / GRP, hh = h % GRP;
-  // every load of the head's records issued at once (offsets past the
-  // records read as zeros), then the LDS stores
-  constexpr int NB = (kDecodeAttnMaxSplit * PR + 255) / 256;
-  const int total = nsplit * PR;
+  const int d = threadIdx.x, lane = threadIdx.x & 63;
   const rsrc_t prs = make_rsrc(part + (int64_t)g * nsplit * (GRP * PR),
                                (uint32_t)(nsplit * GRP * PR) * 4u);
-  float r[NB];
+  auto off = [&](int x, int e) -> uint32_t {
+    return x < nsplit ? (uint32_t)(x * GRP * PR + hh * PR + e) * 4u : kOutOfRange;
+  };
+  const float m_lane = bload4f(prs, off(lane, HD));
+  const float l_lane = bload4f(prs, off(lane, HD + 1));
+  float ov[NX];
 #pragma unroll
-  for (int u = 0; u < NB; ++u) {
-    const int t = threadIdx.x + 256 * u;
-    r[u] = bload4f(prs, t < total ? (uint32_t)((t / PR) * GRP * PR + hh * PR + t % PR) * 4u
-                                  : kOutOfRange);
-  }
-#pragma unroll
-  for (int u = 0; u < NB; ++u)
-    if (threadIdx.x + 256 * u < total) rs[threadIdx.x + 256 * u] = r[u];
+  for (int x = 0; x < NX; ++x) ov[x] = bload4f(prs, off(x, d));
   const int pos0 = posp ? *posp : pos0_host;
   const int nctx = pos0 < maxlen ? pos0 + 1 : maxlen;
   const int chunks = (nctx + KC - 1) / KC;
   const int cpb = max(WPH, (chunks + nsplit - 1) / nsplit);
   const int active = (chunks + cpb - 1) / cpb;
   if (active <= 1) return;
-  __syncthreads();
-  if (threadIdx.x < 64) {
-    const int x = threadIdx.x;
-    const float mx = x < active ? rs[x * PR + HD] : -INFINITY;
-    const float big = wave_max(mx);
-    const float f = x < active ? expf(mx - big) : 0.0f;
-    const float l = wave_sum(x < active ? rs[x * PR + HD + 1] * f : 0.0f);
-    fac[x] = f;
-    if (x == 0) lsum = l;
+  const float mx = lane < active ? m_lane : -INFINITY;
+  const float big = wave_max(mx);
+  const float f = lane < active ? expf(mx - big) : 0.0f;
+  const float l = wave_sum(lane < active ? l_lane * f : 0.0f);
+  float o = 0.0f;
+  for (int x = 0; x < active; ++x) {     // ov[x]: indexed register reads
+    const float fx = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, f), x));
+    o = __builtin_fmaf(ov[x], fx, o);
   }
-  __syncthreads();
-  for (int d = threadIdx.x; d < HD; d += 256) {
-    float o = 0.0f;
-    for (int x = 0; x < active; ++x) o = __builtin_fmaf(rs[x * PR + d], fac[x], o);
-    out[h * HD + d] = o / lsum;
-  }
+  out[h * HD + d] = o / l;
 }
 
 // ---- elementwise (k_swiglu_mul, k_res_add, k_add) ----------------------------
@@ -1004,7 +993,7 @@ hipError_t launch_decode_attn_t(const DecodeAttnArgs &a, hipStream_t st) {
   hipLaunchKernelGGL((attn_decode_kernel<HD, GRP>), dim3((unsigned)a.nsplit, (unsigned)a.nkv),
                      dim3(256), 0, st, a.q, a.k, a.v, a.inv, a.kc, a.vc, a.part, a.out, a.nkv,
                      a.posp, a.pos0, a.maxlen, a.qnorm, a.knorm, a.eps);
-  hipLaunchKernelGGL((attn_merge_kernel<HD, GRP>), dim3((unsigned)a.nheads), dim3(256), 0, st,
+  hipLaunchKernelGGL((attn_merge_kernel<HD, GRP>), dim3((unsigned)a.nheads), dim3(HD), 0, st,
                      a.part, a.out, a.nsplit, a.posp, a.pos0, a.maxlen);
   return hipGetLastError();
 }
