@@ -185,13 +185,27 @@ def test_attention_prompt_rows_any_q_scale(ctx, head_dim, nh, nkv):
 def test_decode_attention_equals_rope_then_attention(ctx, head_dim, nh, nkv, pos0):
     """The one-launch token step writes the same cache bits as q8_rope_kv and
     matches q8_rope_kv + q8_attention within 2e-6 (it sums the splits in
-    another order).  maxlen 1536 gives 24 (head_dim 64) or 32 (head_dim 128)
-    context splits of one chunk each: pos0 < 64 (32) is served by one block
-    per KV head, larger pos0 by up to 24 blocks whose records the merge
-    launch combines; a second call must reproduce the first."""
-    say("decode attention", head_dim, nh, nkv, pos0)
+    another order).  maxlen 1536 gives 24 splits of one 64-key chunk
+    (head_dim 64, one head per wave) or, at head_dim 128, 12 splits of four
+    32-key chunks (groups of 4) or 24 of two (groups of 8), each wave one
+    chunk for 4 heads: small pos0 is served by one block per KV head,
+    larger pos0 by several blocks whose records the merge launch combines;
+    a second call must reproduce the first."""
+    decode_attention_case(ctx, head_dim, nh, nkv, pos0, 1536)
+
+
+@pytest.mark.parametrize("head_dim,nh,nkv", [(64, 32, 8), (128, 32, 8), (64, 8, 1)])
+@pytest.mark.parametrize("pos0", [2100, 5000, 6143])
+def test_decode_attention_long_context(ctx, head_dim, nh, nkv, pos0):
+    """maxlen 6144 caps the splits at 32, so each block takes several chunks
+    per wave (the first chunk guessed before the position is read is then
+    reloaded), up to the last cache row."""
+    decode_attention_case(ctx, head_dim, nh, nkv, pos0, 6144)
+
+
+def decode_attention_case(ctx, head_dim, nh, nkv, pos0, maxlen):
+    say("decode attention", head_dim, nh, nkv, pos0, maxlen)
     rng = np.random.default_rng(4)
-    maxlen = 1536
     qd, kvd = nh * head_dim, nkv * head_dim
     inv = mo.llama3_inv_freq(head_dim, 500000.0, 32.0, 1.0, 4.0, 8192.0)
     cache = rng.standard_normal((2, maxlen, kvd)).astype(np.float16)
