@@ -137,8 +137,8 @@ struct DecodeAttnArgs {
 // Per-head RMSNorm of q and k (with qnorm / knorm), RoPE of q and k, append
 // of k and v at cache row pos0 and attention of the one new token over rows
 // 0 .. pos0: one launch of nsplit x nkv blocks over
-// context splits, then a merge launch.  Calls that share `part` must not
-// overlap.
+// context splits, then (nsplit > 1) a merge launch.  Calls that share
+// `part` must not overlap.
 // Keys per chunk (one wave's unit of work), head slots of a block of 4 waves
 // and the split count.  Head slots: heads per wave GRP / slots, waves per
 // head 4 / slots.  With 64-dim heads (short rows, contexts of a chunk or so
@@ -149,7 +149,11 @@ struct DecodeAttnArgs {
 // (blocks of 4 / slots chunks) up to 32 blocks per KV head, then more chunks
 // per block.  Every launched block reads the position before it can leave
 // and a launch of 256 blocks takes about 1.4 us to start them all, so the
-// grid holds no more blocks than the longest context keeps busy.
+// grid holds no more blocks than the longest context keeps busy.  A cache
+// of at most 4 chunks per wave gets one block per KV head, which writes the
+// output itself, and no merge launch (the merge costs more than the
+// chunks: Qwen3-0.6B at 128 cached tokens).
+constexpr int kDecodeAttnOneBlockChunks = 4;
 constexpr int kDecodeAttnMaxSplit = 32;   // bound of the merge's per-thread loads
 constexpr int decode_attn_chunk(int head_dim) { return head_dim > 64 ? 32 : 64; }
 constexpr int decode_head_slots(int hd, int grp) {
@@ -159,7 +163,7 @@ inline int decode_attn_nsplit(int64_t maxlen, int head_dim, int grp) {
   const int64_t kc = decode_attn_chunk(head_dim);
   const int64_t wph = 4 / decode_head_slots(head_dim, grp);
   const int64_t n = ((maxlen + kc - 1) / kc + wph - 1) / wph;
-  return (int)(n < 1 ? 1 : n > 32 ? 32 : n);
+  return (int)(n <= kDecodeAttnOneBlockChunks ? 1 : n > 32 ? 32 : n);
 }
 hipError_t launch_decode_attention(const DecodeAttnArgs &a, hipStream_t st);
 hipError_t launch_swiglu(float *g, const float *u, int64_t n, hipStream_t st);

@@ -993,8 +993,9 @@ hipError_t launch_decode_attn_t(const DecodeAttnArgs &a, hipStream_t st) {
   hipLaunchKernelGGL((attn_decode_kernel<HD, GRP>), dim3((unsigned)a.nsplit, (unsigned)a.nkv),
                      dim3(256), 0, st, a.q, a.k, a.v, a.inv, a.kc, a.vc, a.part, a.out, a.nkv,
                      a.posp, a.pos0, a.maxlen, a.qnorm, a.knorm, a.eps);
-  hipLaunchKernelGGL((attn_merge_kernel<HD, GRP>), dim3((unsigned)a.nheads), dim3(HD), 0, st,
-                     a.part, a.out, a.nsplit, a.posp, a.pos0, a.maxlen);
+  if (a.nsplit > 1)      // one split: its blocks wrote the output
+    hipLaunchKernelGGL((attn_merge_kernel<HD, GRP>), dim3((unsigned)a.nheads), dim3(HD), 0, st,
+                       a.part, a.out, a.nsplit, a.posp, a.pos0, a.maxlen);
   return hipGetLastError();
 }
 

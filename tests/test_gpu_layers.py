@@ -203,6 +203,15 @@ def test_decode_attention_long_context(ctx, head_dim, nh, nkv, pos0):
     decode_attention_case(ctx, head_dim, nh, nkv, pos0, 6144)
 
 
+@pytest.mark.parametrize("head_dim,nh,nkv", [(128, 16, 8), (64, 32, 8), (128, 32, 8)])
+@pytest.mark.parametrize("pos0", [0, 40, 127, 159])
+def test_decode_attention_short_cache(ctx, head_dim, nh, nkv, pos0):
+    """A cache of at most 4 chunks per wave (maxlen 160) is served by one
+    block per KV head, which takes every chunk and writes the output, with
+    no merge launch."""
+    decode_attention_case(ctx, head_dim, nh, nkv, pos0, 160)
+
+
 def decode_attention_case(ctx, head_dim, nh, nkv, pos0, maxlen):
     say("decode attention", head_dim, nh, nkv, pos0, maxlen)
     rng = np.random.default_rng(4)
