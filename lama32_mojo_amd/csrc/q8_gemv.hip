@@ -397,8 +397,11 @@ hipError_t launch_fused_t(const FusedLinearArgs &f, int64_t cap, hipStream_t st)
   const int64_t tiles = (nout + rows_per_group - 1) / rows_per_group;
   dim3 grid(grid_for(tiles, cap)), block(256);
   const float *x = reinterpret_cast<const float *>(a.x);
+  // x read from L2 by every wave past the stage limit, and for short rows
+  // (m <= 2048), where the stage and its barrier cost more than they save
+  // (Qwen3-0.6B o projection: step 0.741 -> 0.737 ms)
   if constexpr (PRE == PRE_NONE) {
-    if (a.m > kLdsStageFloats) {
+    if (a.m > kLdsStageFloats || a.m <= 2048) {
       hipLaunchKernelGGL((gemv_kernel<G, KIND, 1, R, SPLITK, false, PRE, POST, NPF>), grid, block,
                          0, st, a.w, a.row_bytes, a.n, x, a.m, a.y, f.wn, f.eps, f.res, f.part);
       return hipGetLastError();
