@@ -350,6 +350,8 @@ hipError_t launch_rows(const LinearArgs &a, const float *x, float *y, hipStream_
   if (a.m > 4096 && a.m % 64 == 0) return launch_fast<G, KIND, S, 4, 4>(a, x, y, 1024, st);
   if (a.n >= 65536) return launch_fast<G, KIND, S, 2, 1, 1>(a, x, y, 8192, st);
   if (a.n >= 8192) return launch_fast<G, KIND, S, 4, 1>(a, x, y, 1024, st);
+  // one row, 4096 .. 8191 outputs: 2 rows per wave (Qwen3-8B o and q|k|v)
+  if (S == 1 && a.n >= 4096) return launch_fast<G, KIND, S, 2, 1>(a, x, y, 2048, st);
   return launch_fast<G, KIND, S, 1, 1>(a, x, y, 4096, st);
 }
 
