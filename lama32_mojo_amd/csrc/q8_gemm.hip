@@ -7,15 +7,22 @@
 //   1. act16_kernel: each activation row is scaled by a power of two 2^-e_i
 //      so that its largest |x| lies in [2^14, 2^15), rounded to binary16
 //      (exact for bf16 input: binary16 has three more mantissa bits and the
-//      scaled row sits inside its normal range), and written with 2^e_i;
+//      scaled row sits inside its normal range), and written with e_i.  With
+//      f32 scales the same launch gives every weight row j an exponent f_j
+//      that puts its largest scale in [2^7, 2^8) (binary16 scales need none:
+//      f_j = 0);
 //   2. gemm_kernel: each lane turns its column's int8 codes into binary16
-//      weights q * s in registers and feeds them to the MFMA as the B
+//      weights q * s 2^-f_j in registers and feeds them to the MFMA as the B
 //      operand; the activations come through LDS as the A operand; the f32
-//      accumulators need no per-group rescale, and each output is multiplied
-//      once by its row's 2^e_i.
+//      accumulators need no per-group rescale, and each output is scaled
+//      once by 2^(e_i + f_j).
 // Rounding: the binary16 weight carries one rounding of q * s (two with f32
-// scales, which are rounded to binary16 first), i.e. a relative error below
-// 2^-11; products and sums are f32.
+// scales: s 2^-f_j is rounded to binary16 first), i.e. a relative error
+// below 2^-11 each; products and sums are f32.  Without the row exponent
+// an f32 scale below 2^-14 (a group absmax under about 7.75e-3) would land
+// in binary16's subnormal range and lose relative precision; with it only
+// groups 2^21 times smaller than their row's largest group do, and their
+// share of any output is that much smaller.
 //
 // Cost model (per SIMD: 512 MFMA MACs or 16 VALU lanes per clock).  A weight
 // costs 1.75 VALU operations (one xor per 4 codes, then per 2 codes a v_perm
@@ -51,16 +58,46 @@ constexpr int kWaves = 8;      // waves per workgroup: 8 (two K parities) or 4
 constexpr int LDA = KT + 8;    // halves per LDS row (16-byte pad)
 
 // ---- 1. activation rows to binary16 ----------------------------------------
-// One 256-thread block per row.  With CH > 0 the row (m <= 2048 CH) stays in
-// registers between the max and the conversion (one pass over memory);
-// CH = 0 reads it twice.
-template <bool XF32, int CH>
-__global__ __launch_bounds__(256) void act16_kernel(const void *__restrict__ xv, int64_t m,
-                                                    uint16_t *__restrict__ x16,
-                                                    float *__restrict__ rf) {
+// Exponent f that puts a weight row's largest f32 scale mx in [2^7, 2^8):
+// then |q| * s 2^-f <= 127 * 2^8 stays far inside binary16's range and
+// every scale above 2^-21 mx is a normal binary16 number.  Zero, inf and
+// NaN maxima keep f = 0.
+__device__ __forceinline__ int weight_row_exponent(float mx) {
+  if (!(mx > 0.0f) || !(mx <= 3.4028235e38f)) return 0;
+  int bias = 0;
+  if (mx < 1.17549435e-38f) {              // subnormal: scale up exactly first
+    mx *= 18446744073709551616.0f;         // 2^64
+    bias = 64;
+  }
+  return (int)((__builtin_bit_cast(uint32_t, mx) >> 23) & 255u) - 127 - 7 - bias;
+}
+
+// Blocks [0, s): one 256-thread block per activation row.  With CH > 0 the
+// row (m <= 2048 CH) stays in registers between the max and the conversion
+// (one pass over memory); CH = 0 reads it twice.  Blocks [s, s + nwb): one
+// wave per weight row, the row exponent of its f32 scales (ew), f32 scales
+// only (nwb = 0 otherwise).
+template <bool XF32, int CH, int G>
+__global__ __launch_bounds__(256) void act16_kernel(const void *__restrict__ xv, int64_t s,
+                                                    int64_t m, uint16_t *__restrict__ x16,
+                                                    int *__restrict__ ex,
+                                                    const uint8_t *__restrict__ w,
+                                                    int64_t row_bytes, int64_t n,
+                                                    int *__restrict__ ew) {
   __shared__ float red[4];
   const int64_t r = blockIdx.x;
   const int tid = threadIdx.x;
+  if (r >= s) {
+    // the whole block takes this branch (no barrier in it)
+    const int64_t j = (r - s) * 4 + (tid >> 6);
+    if (j >= n) return;
+    const float *sc = reinterpret_cast<const float *>(w + j * row_bytes);
+    float mx = 0.0f;
+    for (int64_t g = tid & 63; g < m / G; g += 64) mx = fmaxf(mx, fabsf(sc[g]));
+    mx = wave_max(mx);
+    if ((tid & 63) == 0) ew[j] = weight_row_exponent(mx);
+    return;
+  }
   // 8 consecutive values per step (m is a multiple of 8)
   auto load8 = [&](int64_t k, float (&v)[8]) {
     if constexpr (XF32) {
@@ -137,22 +174,28 @@ __global__ __launch_bounds__(256) void act16_kernel(const void *__restrict__ xv,
       store8(k, v, e);
     }
   }
-  if (tid == 0) rf[r] = __builtin_ldexpf(1.0f, e);
+  if (tid == 0) ex[r] = e;
 }
 
-template <bool XF32>
-void launch_act16(const LinearArgs &a, uint16_t *x16, float *rf, hipStream_t st) {
-  const dim3 grid((unsigned)a.s), block(256);
+// nw weight rows get their exponents (0 for none).
+template <bool XF32, int G>
+void launch_act16(const LinearArgs &a, uint16_t *x16, int *ex, int *ew, int64_t nw,
+                  hipStream_t st) {
+  const dim3 grid((unsigned)(a.s + (nw + 3) / 4)), block(256);
+#define Q8_ACT16(CH)                                                                         \
+  hipLaunchKernelGGL((act16_kernel<XF32, CH, G>), grid, block, 0, st, a.x, a.s, a.m, x16, ex, \
+                     a.w, a.row_bytes, nw, ew)
   if (a.m <= 2048)
-    hipLaunchKernelGGL((act16_kernel<XF32, 1>), grid, block, 0, st, a.x, a.m, x16, rf);
+    Q8_ACT16(1);
   else if (a.m <= 4096)
-    hipLaunchKernelGGL((act16_kernel<XF32, 2>), grid, block, 0, st, a.x, a.m, x16, rf);
+    Q8_ACT16(2);
   else if (a.m <= 8192)
-    hipLaunchKernelGGL((act16_kernel<XF32, 4>), grid, block, 0, st, a.x, a.m, x16, rf);
+    Q8_ACT16(4);
   else if (a.m <= 16384)
-    hipLaunchKernelGGL((act16_kernel<XF32, 8>), grid, block, 0, st, a.x, a.m, x16, rf);
+    Q8_ACT16(8);
   else
-    hipLaunchKernelGGL((act16_kernel<XF32, 0>), grid, block, 0, st, a.x, a.m, x16, rf);
+    Q8_ACT16(0);
+#undef Q8_ACT16
 }
 
 // ---- 2. the GEMM --------------------------------------------------------------
@@ -171,9 +214,9 @@ __device__ __forceinline__ f16x8 dequant8(uint32_t d0, uint32_t d1, f16x2 s2) {
 template <int G, int KIND, int BM, int TN, int NW>
 __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(NW / 4, NW / 4)))
 void gemm_kernel(const uint8_t *__restrict__ w, int64_t row_bytes,
-                   const uint16_t *__restrict__ x16, const float *__restrict__ rf,
-                   float *__restrict__ y, int64_t s, int64_t m, int64_t n, int nit,
-                   float *__restrict__ ws) {
+                   const uint16_t *__restrict__ x16, const int *__restrict__ ex,
+                   const int *__restrict__ ew, float *__restrict__ y, int64_t s, int64_t m,
+                   int64_t n, int nit, float *__restrict__ ws) {
   // blockIdx.z selects a K range of nit iterations (split-K): with
   // gridDim.z == 1 y is written directly, otherwise split z writes its
   // partial sums to ws[z] and splitk_reduce_kernel adds them up.
@@ -191,7 +234,7 @@ void gemm_kernel(const uint8_t *__restrict__ w, int64_t row_bytes,
   __shared__ __attribute__((aligned(16))) uint16_t As[2][BM * LDA];
   __shared__ __attribute__((aligned(16))) uint8_t Bs[2][BN * KT];    // codes, swizzled rows
   __shared__ __attribute__((aligned(16))) uint8_t Ss[2][BN * SPB];   // scales
-  __shared__ float rfs[BM];
+  __shared__ int exs[BM];
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -287,7 +330,12 @@ void gemm_kernel(const uint8_t *__restrict__ w, int64_t row_bytes,
     return 64 * h + (G == 64 ? 32 * lh + 8 * ks : 32 * (ks >> 1) + 16 * lh + 8 * (ks & 1));
   };
 
-  if (tid < BM) rfs[tid] = tid < arows ? rf[m0 + tid] : 0.0f;
+  if (tid < BM) exs[tid] = tid < arows ? ex[m0 + tid] : 0;
+  // this lane's weight-row exponents (f32 scales) per column tile
+  int ewc[TN];
+#pragma unroll
+  for (int t = 0; t < TN; ++t)
+    ewc[t] = KIND == SCALE_F32 && n0 + bcol(t) < n ? ew[n0 + bcol(t)] : 0;
 
   f32x16 acc[TM][TN];
 #pragma unroll
@@ -340,7 +388,7 @@ void gemm_kernel(const uint8_t *__restrict__ w, int64_t row_bytes,
           if constexpr (KIND == SCALE_F16)
             hs = *reinterpret_cast<const _Float16 *>(sp + 2 * g);
           else
-            hs = (_Float16)*reinterpret_cast<const float *>(sp + 4 * g);
+            hs = (_Float16)__builtin_ldexpf(*reinterpret_cast<const float *>(sp + 4 * g), -ewc[t]);
           s2[t][g] = k0 + g * G < m ? f16x2{hs, hs} : zero2;
         }
       }
@@ -382,7 +430,7 @@ void gemm_kernel(const uint8_t *__restrict__ w, int64_t row_bytes,
   }
 
   // With two K parities, each column tile's parities meet in LDS (reusing
-  // As), one column tile at a time; each output is scaled by its row's 2^e.
+  // As), one column tile at a time; each output is scaled by 2^(e_i + f_j).
   float *red = reinterpret_cast<float *>(&As[0][0]);   // 4 * TM * 16 * 64 floats
   static_assert(4 * TM * 16 * 64 * 4 <= (int)sizeof(As), "reduction buffer too small");
   const int rows_left = (int)(s - m0 - lh * 4);
@@ -410,7 +458,7 @@ void gemm_kernel(const uint8_t *__restrict__ w, int64_t row_bytes,
           const int r = i * 32 + (v >> 2) * 8 + (v & 3);
           float o = acc[i][t][v];
           if constexpr (NP == 2) o += red[((p * TM + i) * 16 + v) * 64 + lane];
-          if (r < rows_left) out[(int64_t)r * n] = o * rfs[r + lh * 4];
+          if (r < rows_left) out[(int64_t)r * n] = __builtin_ldexpf(o, exs[r + lh * 4] + ewc[t]);
         }
     }
   }
@@ -436,7 +484,8 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float *__restr
 }
 
 template <int G, int KIND, int BM, int TN, int NW>
-hipError_t launch_t(const LinearArgs &a, const uint16_t *x16, const float *rf, hipStream_t st) {
+hipError_t launch_t(const LinearArgs &a, const uint16_t *x16, const int *ex, const int *ew,
+                    hipStream_t st) {
   constexpr int BN = 128 * TN;
   const int64_t nit_all = (a.m + KT - 1) / KT;
   const int64_t gx = (a.n + BN - 1) / BN, gy = (a.s + BM - 1) / BM;
@@ -451,21 +500,29 @@ hipError_t launch_t(const LinearArgs &a, const uint16_t *x16, const float *rf, h
   int64_t nit = (nit_all + splits - 1) / splits;
   dim3 grid((unsigned)gx, (unsigned)gy, (unsigned)splits), block(64 * NW);
   hipLaunchKernelGGL((gemm_kernel<G, KIND, BM, TN, NW>), grid, block, 0, st, a.w, a.row_bytes, x16,
-                     rf, a.y, a.s, a.m, a.n, (int)nit, a.ws);
+                     ex, ew, a.y, a.s, a.m, a.n, (int)nit, a.ws);
   if (splits > 1) return launch_splitk_reduce(a.ws, a.y, a.s * a.n, (int)splits, st);
   return hipGetLastError();
 }
 
 template <int G, int KIND>
-hipError_t launch_g(const LinearArgs &a, const uint16_t *x16, const float *rf, hipStream_t st) {
+hipError_t launch_g(const LinearArgs &a, uint16_t *x16, int *ex, int *ew, bool weights,
+                    hipStream_t st) {
+  // weight-row exponents only for f32 scales, and only when asked (a call
+  // split into row chunks computes them with its first chunk)
+  const int64_t nw = KIND == SCALE_F32 && weights ? a.n : 0;
+  if (a.x_is_bf16)
+    launch_act16<false, G>(a, x16, ex, ew, nw, st);
+  else
+    launch_act16<true, G>(a, x16, ex, ew, nw, st);
   // 128-row tiles once the rows fill them; two column tiles per wave when
   // the 256-column tiles still give every CU a workgroup.
   if (a.s > 64) {
     const int64_t tiles256 = (a.n + 255) / 256 * ((a.s + 127) / 128);
-    if (tiles256 >= 256) return launch_t<G, KIND, 128, 2, kWaves>(a, x16, rf, st);
-    return launch_t<G, KIND, 128, 1, kWaves>(a, x16, rf, st);
+    if (tiles256 >= 256) return launch_t<G, KIND, 128, 2, kWaves>(a, x16, ex, ew, st);
+    return launch_t<G, KIND, 128, 1, kWaves>(a, x16, ex, ew, st);
   }
-  return launch_t<G, KIND, 64, 1, kWaves>(a, x16, rf, st);
+  return launch_t<G, KIND, 64, 1, kWaves>(a, x16, ex, ew, st);
 }
 
 }  // namespace
@@ -478,16 +535,13 @@ hipError_t launch_splitk_reduce(const float *ws, float *y, int64_t count, int sp
   return hipGetLastError();
 }
 
-hipError_t launch_gemm(const LinearArgs &a, uint16_t *x16, float *rf, hipStream_t st) {
+hipError_t launch_gemm(const LinearArgs &a, uint16_t *x16, int *ex, int *ew, bool weights,
+                       hipStream_t st) {
   if (a.s == 0 || a.n == 0) return hipSuccess;
-  if (a.x_is_bf16)
-    launch_act16<false>(a, x16, rf, st);
-  else
-    launch_act16<true>(a, x16, rf, st);
-  if (a.G == 64 && a.kind == SCALE_F16) return launch_g<64, SCALE_F16>(a, x16, rf, st);
-  if (a.G == 64 && a.kind == SCALE_F32) return launch_g<64, SCALE_F32>(a, x16, rf, st);
-  if (a.G == 32 && a.kind == SCALE_F16) return launch_g<32, SCALE_F16>(a, x16, rf, st);
-  if (a.G == 32 && a.kind == SCALE_F32) return launch_g<32, SCALE_F32>(a, x16, rf, st);
+  if (a.G == 64 && a.kind == SCALE_F16) return launch_g<64, SCALE_F16>(a, x16, ex, ew, weights, st);
+  if (a.G == 64 && a.kind == SCALE_F32) return launch_g<64, SCALE_F32>(a, x16, ex, ew, weights, st);
+  if (a.G == 32 && a.kind == SCALE_F16) return launch_g<32, SCALE_F16>(a, x16, ex, ew, weights, st);
+  if (a.G == 32 && a.kind == SCALE_F32) return launch_g<32, SCALE_F32>(a, x16, ex, ew, weights, st);
   return hipErrorInvalidValue;
 }
 

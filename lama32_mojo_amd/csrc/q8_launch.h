@@ -70,9 +70,13 @@ constexpr int kArgmaxMaxBlocks = 8192;
 bool gemv_fused_supported(const FusedLinearArgs &f);
 hipError_t launch_gemv_fused(const FusedLinearArgs &a, hipStream_t st);
 // Prefill path, dequant-GEMM on f16 MFMA: x (bf16 or f32) is first written
-// as binary16 rows scaled by a power of two to x16 [s, m] with the factors
-// in rf [s]; then the weights are dequantized to binary16 in registers.
-hipError_t launch_gemm(const LinearArgs &a, uint16_t *x16, float *rf, hipStream_t st);
+// as binary16 rows scaled by a power of two to x16 [s, m] with the
+// exponents in ex [s]; with f32 scales and `weights` set the same launch
+// writes each weight row's scale exponent to ew [n] (a later row chunk of
+// the same call passes weights = false and reuses them); then the weights
+// are dequantized to binary16 in registers.
+hipError_t launch_gemm(const LinearArgs &a, uint16_t *x16, int *ex, int *ew, bool weights,
+                       hipStream_t st);
 // y[i] = sum over z < splits of ws[z * count + i] (split-K partial sums).
 hipError_t launch_splitk_reduce(const float *ws, float *y, int64_t count, int splits,
                                 hipStream_t st);

@@ -521,16 +521,23 @@ __global__ __launch_bounds__(64 * KW) void skinny_x_kernel(const uint8_t *__rest
       for (int v = 0; v < 4; ++v)
         __hip_atomic_store(&part[(16 * tr + 4 * q + v) * ROWS + wid * 16 * NC + 16 * t + c],
                            acc[t][tr][v], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  // every wave's partial stores have completed before the workgroup counts
-  // itself
+  // Publication across workgroups (which may sit on different XCDs, each
+  // with its own L2): every wave waits for its partial stores, the barrier
+  // orders all waves before thread 0, and thread 0 counts the workgroup with
+  // an agent-scope release (its stores and everything before the barrier
+  // reach the agent's coherence point first).  The last workgroup to
+  // arrive takes an agent-scope acquire before it reads the partials, so
+  // the counter it saw at n - 1 orders every other workgroup's stores before
+  // its loads.
   __builtin_amdgcn_s_waitcnt(0);
   __shared__ int last;
   __syncthreads();
   if (threadIdx.x == 0)
-    last = __hip_atomic_fetch_add(&cnt[rb], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+    last = __hip_atomic_fetch_add(&cnt[rb], 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT) ==
            ks_n - 1;
   __syncthreads();
   if (!last) return;
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
   const float *p0 = ws + (int64_t)rb * ks_n * PT;
   const int64_t r0 = (int64_t)rb * ROWS;
   for (int o = threadIdx.x; o < PT; o += 64 * KW) {

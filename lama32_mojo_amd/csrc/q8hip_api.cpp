@@ -438,14 +438,28 @@ void attach_gemm_workspace(q8_ctx *ctx, q8::LinearArgs &la) {
   la.cnt_n = kCountInts;
 }
 
-// Prefill GEMM on f16 MFMA through the context's binary16 activation
-// buffer, in chunks of as many rows as it holds (stream order keeps the
+// Layout of a GEMM activation buffer of `bytes`: the weight-row exponents
+// (n ints) at the end, 256-byte aligned, and before them as many binary16
+// activation rows (2 m bytes each) plus one int exponent per row as fit.
+// Zero rows: the shape does not fit (the C ABI rejects it first).
+int64_t gemm_act_rows(int64_t bytes, int64_t m, int64_t n) {
+  const int64_t tail = (4 * n + 255) / 256 * 256;
+  return bytes > tail ? (bytes - tail) / (2 * m + 4) : 0;
+}
+
+bool gemm_fits(int64_t bytes, int64_t m, int64_t n) {
+  return m < ((int64_t)1 << 40) && n < ((int64_t)1 << 40) && gemm_act_rows(bytes, m, n) > 0;
+}
+
+// Prefill GEMM on f16 MFMA through a binary16 activation buffer of `bytes`
+// at act16, in chunks of as many rows as it holds (stream order keeps the
 // chunks from overlapping).
-hipError_t run_gemm(q8_ctx *ctx, q8::LinearArgs la) {
-  attach_gemm_workspace(ctx, la);
-  const int64_t rows = kAct16Bytes / (la.m * 2 + 4);
-  uint16_t *x16 = static_cast<uint16_t *>(ctx->act16);
-  float *rf = reinterpret_cast<float *>(static_cast<uint8_t *>(ctx->act16) + rows * la.m * 2);
+hipError_t run_gemm_in(q8::LinearArgs la, void *act16, int64_t bytes, hipStream_t st) {
+  const int64_t rows = gemm_act_rows(bytes, la.m, la.n);
+  uint8_t *base = static_cast<uint8_t *>(act16);
+  uint16_t *x16 = reinterpret_cast<uint16_t *>(base);
+  int *ex = reinterpret_cast<int *>(base + rows * la.m * 2);
+  int *ew = reinterpret_cast<int *>(base + bytes - (4 * la.n + 255) / 256 * 256);
   const int64_t xb = la.x_is_bf16 ? 2 : 4;
   const uint8_t *x0 = static_cast<const uint8_t *>(la.x);
   float *y0 = la.y;
@@ -454,10 +468,15 @@ hipError_t run_gemm(q8_ctx *ctx, q8::LinearArgs la) {
     la.s = s - r0 < rows ? s - r0 : rows;
     la.x = x0 + r0 * la.m * xb;
     la.y = y0 + r0 * la.n;
-    hipError_t e = q8::launch_gemm(la, x16, rf, ctx->stream);
+    hipError_t e = q8::launch_gemm(la, x16, ex, ew, r0 == 0, st);
     if (e != hipSuccess) return e;
   }
   return hipSuccess;
+}
+
+hipError_t run_gemm(q8_ctx *ctx, q8::LinearArgs la) {
+  attach_gemm_workspace(ctx, la);
+  return run_gemm_in(la, ctx->act16, kAct16Bytes, ctx->stream);
 }
 
 }  // namespace
@@ -476,6 +495,10 @@ int q8_linear(q8_ctx *ctx, q8_buf *w, uint64_t owt_u16, q8_buf *a, uint64_t ox_f
                 (unsigned long long)oy_f32, (unsigned long long)ny);
   if (nx && ny && overlaps(ox_f32, ox_f32 + nx, oy_f32, oy_f32 + ny))
     return fail(ctx, Q8_ERR_ARG, "q8_linear: x and y overlap");
+  if (s >= kGemmMinRows && !gemm_fits(kAct16Bytes, m, n))
+    return fail(ctx, Q8_ERR_SHAPE, "q8_linear: m=%lld, n=%lld too large for the GEMM's "
+                "activation buffer (%lld bytes)", (long long)m, (long long)n,
+                (long long)kAct16Bytes);
   if (ctx->host_only) return fail(ctx, Q8_ERR_NODEVICE, "q8_linear: host-only context");
   if (s == 0 || n == 0) return ok(ctx);
   if (int rc = set_device(ctx)) return rc;
@@ -521,6 +544,10 @@ int q8_linear_bf16act(q8_ctx *ctx, q8_buf *w, uint64_t owt_u16, q8_buf *x, uint6
                 (unsigned long long)oy_f32, (unsigned long long)ny);
   if (x == y && nx && ny && overlaps(ox_bf16 * 2, (ox_bf16 + nx) * 2, oy_f32 * 4, (oy_f32 + ny) * 4))
     return fail(ctx, Q8_ERR_ARG, "q8_linear_bf16act: x and y overlap");
+  if (!gemm_fits(kAct16Bytes, m, n))
+    return fail(ctx, Q8_ERR_SHAPE, "q8_linear_bf16act: m=%lld, n=%lld too large for the "
+                "GEMM's activation buffer (%lld bytes)", (long long)m, (long long)n,
+                (long long)kAct16Bytes);
   if (ctx->host_only) return fail(ctx, Q8_ERR_NODEVICE, "q8_linear_bf16act: host-only context");
   if (s == 0 || n == 0) return ok(ctx);
   if (int rc = set_device(ctx)) return rc;
@@ -624,6 +651,13 @@ int check_heads(q8_ctx *ctx, int nheads, int nkv, int head_dim, const char *what
 }
 
 int64_t attn_nsplit(int64_t maxlen) { return (maxlen + 63) / 64; }
+
+// The attention kernels address a layer's K or V block through 32-bit
+// buffer offsets: maxlen * nkv * head_dim binary16 values must stay under
+// 2 GiB.
+bool cache_block_ok(int64_t maxlen, int nkv, int head_dim) {
+  return (uint64_t)maxlen * (uint64_t)nkv * (uint64_t)head_dim * 2 < ((uint64_t)1 << 31);
+}
 
 }  // namespace
 
@@ -824,6 +858,9 @@ int q8_rope_kv(q8_ctx *ctx, q8_buf *a, uint64_t oq_f32, uint64_t ok_f32, uint64_
   if (s < 0 || maxlen <= 0 || maxlen > INT32_MAX)
     return fail(ctx, Q8_ERR_SHAPE, "q8_rope_kv: s=%lld, maxlen=%lld", (long long)s,
                 (long long)maxlen);
+  if (!cache_block_ok(maxlen, nkv, head_dim))
+    return fail(ctx, Q8_ERR_SHAPE, "q8_rope_kv: maxlen=%lld (a cache block must stay under "
+                "2 GiB)", (long long)maxlen);
   const uint64_t qn = (uint64_t)s * nheads * head_dim, kn = (uint64_t)s * nkv * head_dim;
   const uint64_t cn = (uint64_t)maxlen * nkv * head_dim;
   if (int rc = check_f32(ctx, a, oq_f32, qn, "q8_rope_kv", "q")) return rc;
@@ -869,6 +906,9 @@ int q8_attention(q8_ctx *ctx, q8_buf *a, uint64_t oq_f32, q8_buf *kv, uint64_t o
   if (s < 0 || s > 65535 || maxlen <= 0 || maxlen > INT32_MAX)
     return fail(ctx, Q8_ERR_SHAPE, "q8_attention: s=%lld, maxlen=%lld", (long long)s,
                 (long long)maxlen);
+  if (!cache_block_ok(maxlen, nkv, head_dim))
+    return fail(ctx, Q8_ERR_SHAPE, "q8_attention: maxlen=%lld (a cache block must stay under "
+                "2 GiB)", (long long)maxlen);
   const uint64_t qn = (uint64_t)s * nheads * head_dim;
   const uint64_t cn = (uint64_t)maxlen * nkv * head_dim;
   const uint64_t sn = q8_attention_scratch_floats(s, nheads, head_dim, maxlen);

@@ -104,18 +104,20 @@ def attention(q: np.ndarray, kc: np.ndarray, vc: np.ndarray, pos0: int, nheads: 
     dot / sqrt(head_dim) (k_scores, k_softmax_rows, k_att_out)."""
     s = q.shape[0]
     grp = nheads // nkv
+    n = pos0 + s                                  # keys the last row sees
+    q = np.asarray(q, dtype=np.float64)
     out = np.zeros((s, nheads * head_dim))
-    for i in range(s):
-        n = pos0 + i + 1
-        for h in range(nheads):
-            g = h // grp
-            qv = q[i, h * head_dim:(h + 1) * head_dim]
-            k = kc[:n, g * head_dim:(g + 1) * head_dim]
-            v = vc[:n, g * head_dim:(g + 1) * head_dim]
-            sc = k @ qv / np.sqrt(head_dim)
-            p = np.exp(sc - sc.max())
-            p /= p.sum()
-            out[i, h * head_dim:(h + 1) * head_dim] = p @ v
+    # key t is visible to row i iff t <= pos0 + i
+    visible = np.arange(n)[None, :] <= (pos0 + np.arange(s))[:, None]
+    for h in range(nheads):
+        g = h // grp
+        k = np.asarray(kc[:n, g * head_dim:(g + 1) * head_dim], dtype=np.float64)
+        v = np.asarray(vc[:n, g * head_dim:(g + 1) * head_dim], dtype=np.float64)
+        sc = q[:, h * head_dim:(h + 1) * head_dim] @ k.T / np.sqrt(head_dim)   # [s, n]
+        sc = np.where(visible, sc, -np.inf)
+        p = np.exp(sc - sc.max(axis=1, keepdims=True))
+        p /= p.sum(axis=1, keepdims=True)
+        out[:, h * head_dim:(h + 1) * head_dim] = p @ v
     return out
 
 

@@ -230,26 +230,28 @@ int q8o_pack_bf16(const uint16_t *w, int64_t n, int64_t m, int G, int kind,
 /* ----------------------------------------------------------------------- */
 
 /* float64 closed form: y[i,j] = sum_g s[j,g] * sum_{k in g} x[i,k] * q[j,k].
- * Every product is exact in float64; this is the parity reference. */
+ * Every product is exact in float64; this is the parity reference.  Each
+ * output is summed on its own in a fixed order, so the OpenMP split over
+ * outputs does not change any result. */
 void q8o_linear_f64(const uint16_t *wpk, const float *x, int64_t s, int64_t m,
                     int64_t n, int G, int kind, double *y)
 {
     int64_t rs = q8o_rowstride_u16(m, G, kind);
     int64_t ng = m / G;
-    for (int64_t i = 0; i < s; ++i) {
+#pragma omp parallel for schedule(static)
+    for (int64_t t = 0; t < s * n; ++t) {
+        const int64_t i = t / n, j = t % n;
         const float *xi = x + i * m;
-        for (int64_t j = 0; j < n; ++j) {
-            const uint16_t *row = wpk + j * rs;
-            const int8_t *q = row_codes(row, m, G, kind);
-            double acc = 0.0;
-            for (int64_t g = 0; g < ng; ++g) {
-                double part = 0.0;
-                for (int k = 0; k < G; ++k)
-                    part += (double)xi[g * G + k] * (double)q[g * G + k];
-                acc += (double)row_scale(row, g, kind) * part;
-            }
-            y[i * n + j] = acc;
+        const uint16_t *row = wpk + j * rs;
+        const int8_t *q = row_codes(row, m, G, kind);
+        double acc = 0.0;
+        for (int64_t g = 0; g < ng; ++g) {
+            double part = 0.0;
+            for (int k = 0; k < G; ++k)
+                part += (double)xi[g * G + k] * (double)q[g * G + k];
+            acc += (double)row_scale(row, g, kind) * part;
         }
+        y[t] = acc;
     }
 }
 

@@ -124,6 +124,9 @@ def main():
     if len(sys.argv) != 2:
         sys.exit("usage: gen_pack_q8_golden.py <reference-root>")
     ref_root = sys.argv[1]
+    # the reference tree is read-only input: importing from it must not
+    # leave compiled bytecode (__pycache__) behind in it
+    sys.dont_write_bytecode = True
     sys.path.insert(0, os.path.join(ref_root, "qwen3_mojo", "scripts"))
     import torch
     from quantize import GROUP, pack_q8  # reference packer (quantize.py:28,31)

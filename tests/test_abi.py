@@ -261,3 +261,52 @@ def test_mm_q8_op_allocates_output_then_validates(hctx):
         q8.mm_q8_op(hctx, w, a, qk, ox, 1, 2048, q8.PAD, 4)
     assert ei.value.code == Q8_ERR_NODEVICE
     assert a.top == q8.PAD + 2048 + 4   # y was allocated, as mm_q8_op does
+
+
+def test_gemm_activation_buffer_limit(hctx):
+    """From 32 rows q8_linear runs the dequant-GEMM through the context's
+    64 MiB binary16 activation buffer, which must hold at least one row
+    (2 m + 4 bytes) plus n weight-row exponents: larger shapes are
+    rejected before any launch (a zero-row chunk would never advance)."""
+    big = 1 << 26
+    w = hctx.alloc(1 << 44)                # host-only: sizes only
+    a = hctx.alloc(1 << 44)
+    L = q8hip.linear
+    # m = 2^24: 2 m + 4 bytes per row no longer fit with the exponents
+    m = 1 << 25
+    c, msg = code_of(L, hctx, w, 0, a, 0, 32 * m, 32, m, 64)
+    assert c == Q8_ERR_SHAPE and "activation buffer" in msg
+    # one row fewer than the GEMM threshold takes the small-batch path: no limit
+    assert code_of(L, hctx, w, 0, a, 0, 31 * m, 31, m, 64)[0] == Q8_ERR_NODEVICE
+    # n weight-row exponents alone fill the buffer
+    c, msg = code_of(L, hctx, w, 0, a, 0, 32 * 64, 32, 64, big // 4)
+    assert c == Q8_ERR_SHAPE and "activation buffer" in msg
+    assert code_of(L, hctx, w, 0, a, 0, 32 * 64, 32, 64, big // 8)[0] == Q8_ERR_NODEVICE
+    B = q8hip.linear_bf16act
+    c, msg = code_of(B, hctx, w, 0, a, 0, a, 1 << 40, 1, m, 64)
+    assert c == Q8_ERR_SHAPE and "activation buffer" in msg
+
+
+@pytest.mark.parametrize("which", ["rope_kv", "attention"])
+def test_kv_cache_block_under_2gib(hctx, which):
+    """The attention kernels address a K or V block with 32-bit buffer
+    offsets: maxlen * nkv * head_dim binary16 values must stay under 2 GiB
+    (the same limit q8_decode_attention enforces)."""
+    nh, nkv, hd = 32, 8, 128
+    a = hctx.alloc(4 * 200000)
+    kv = hctx.alloc(1 << 44)
+    ok_len = (1 << 30) // (nkv * hd) - 1          # 2 GiB - 2 KiB per block
+    bad_len = (1 << 30) // (nkv * hd)             # exactly 2 GiB per block
+    for maxlen, want in ((ok_len, Q8_ERR_NODEVICE), (bad_len, Q8_ERR_SHAPE),
+                         (4 * bad_len, Q8_ERR_SHAPE)):
+        blk = maxlen * nkv * hd
+        if which == "rope_kv":
+            c, msg = code_of(q8hip.rope_kv, hctx, a, 0, 8192, 9216, 10240, kv, 0, blk, maxlen,
+                             1, 0, nh, nkv, hd)
+        else:
+            # 16 query rows: the one-pass kernel, which needs no scratch
+            c, msg = code_of(q8hip.attention, hctx, a, 0, kv, 0, blk, maxlen, 65536, 0, 16, 0,
+                             nh, nkv, hd)
+        assert c == want, (maxlen, msg)
+        if want == Q8_ERR_SHAPE:
+            assert "2 GiB" in msg

@@ -303,11 +303,11 @@ def gpu_model(ctx, spec, tensors, maxlen, max_prefill=8, fuse=True):
     if spec.qk_norm:        # Qwen3-style: plain RoPE, theta 1e6 (as qwen_tiny's oracle)
         cfg = gm.Config(spec.hidden, spec.layers, spec.n_heads, spec.n_kv, spec.head_dim,
                         spec.inter, spec.vocab, spec.eps, 1000000.0, 1.0, 1.0, 4.0, 8192.0,
-                        tied=True, name="tiny-qwen", qk_norm=True, rope="plain")
+                        tied=spec.tied, name="tiny-qwen", qk_norm=True, rope="plain")
     else:
         cfg = gm.Config(spec.hidden, spec.layers, spec.n_heads, spec.n_kv, spec.head_dim,
                         spec.inter, spec.vocab, spec.eps, 500000.0, 32.0, 1.0, 4.0, 8192.0,
-                        tied=True, name="tiny")
+                        tied=spec.tied, name="tiny")
     return gm.Q8Llama(ctx, cfg, maxlen, spec.G, spec.scale, weights=tensors,
                       max_prefill=max_prefill, fuse=fuse)
 
@@ -430,6 +430,37 @@ def test_model_forward_and_greedy_decode(ctx, G, scale):
             ids_ref.append(cur)
         got = [m.forward_argmax([nxt])]
         got += [m.forward_argmax([got[-1]])]
+        got += m.decode_steps(got[-1], 4)
+        assert got == ids_ref, (got, ids_ref)
+    finally:
+        m.close()
+
+
+@pytest.mark.parametrize("G,scale", [(64, "f16"), (32, "f32")])
+def test_model_untied_head(ctx, G, scale):
+    """A separate lm_head (the Llama-3.1-8B and Qwen3-8B layout,
+    llama31_mojo/src/llama_gpu.mojo:142-159): logits within 1e-3 of the
+    float64 model, which reads lm_head.weight, not the embedding table, and
+    the same greedy ids over eager and captured-graph steps."""
+    say("model untied", G, scale)
+    spec, t, inv = tiny_model(G=G, scale=scale, seed=11, tied=False)
+    assert not np.array_equal(t["lm_head.weight"], t["model.embed_tokens.weight"])
+    maxlen = 32
+    prompt = [5, 90, 1, 44, 13]
+    ref = mo.OracleModel(spec, t, inv, maxlen)
+    m = gpu_model(ctx, spec, t, maxlen)
+    try:
+        lg = m.forward(prompt)
+        lr = ref.forward(prompt)
+        assert max_rel_err(lg, lr) <= 1e-3, max_rel_err(lg, lr)
+        nxt = int(np.argmax(lr))
+        assert int(np.argmax(lg)) == nxt
+        ids_ref = []
+        cur = nxt
+        for _ in range(5):
+            cur = int(np.argmax(ref.forward([cur])))
+            ids_ref.append(cur)
+        got = [m.forward_argmax([nxt])]
         got += m.decode_steps(got[-1], 4)
         assert got == ids_ref, (got, ids_ref)
     finally:

@@ -108,16 +108,20 @@ def packed(n, m, seed, std, G, scale):
 
 
 def tiny_model(maxlen=16, G=64, scale="f16", layers=2, seed=0, hidden=512, n_heads=8, n_kv=2,
-               head_dim=64, inter=1024, vocab=97, qk_norm=False):
+               head_dim=64, inter=1024, vocab=97, qk_norm=False, tied=True):
     """A small Llama-style model (packed rows 16-byte aligned, head_dim 64);
-    with qk_norm a Qwen3-style one (per-head q/k norms, plain RoPE)."""
+    with qk_norm a Qwen3-style one (per-head q/k norms, plain RoPE); with
+    tied=False a separate lm_head (Llama-3.1-8B, Qwen3-8B)."""
     spec = mo.ModelSpec(hidden=hidden, layers=layers, n_heads=n_heads, n_kv=n_kv,
                         head_dim=head_dim, inter=inter, vocab=vocab,
-                        eps=1e-6 if qk_norm else 1e-5, G=G, scale=scale, qk_norm=qk_norm)
+                        eps=1e-6 if qk_norm else 1e-5, G=G, scale=scale, qk_norm=qk_norm,
+                        tied=tied)
     rng = np.random.default_rng(seed)
     H, QD, KVD, I = spec.hidden, spec.n_heads * spec.head_dim, spec.n_kv * spec.head_dim, spec.inter
     t = {"model.embed_tokens.weight": packed(spec.vocab, H, seed + 1, 0.5, G, scale),
          "model.norm.weight": f32_to_bf16_bits((1 + 0.1 * rng.standard_normal(H)).astype(np.float32))}
+    if not tied:
+        t["lm_head.weight"] = packed(spec.vocab, H, seed + 2, 1.5 / np.sqrt(H), G, scale)
     k = 10
     for L in range(layers):
         p = f"model.layers.{L}."
