@@ -72,7 +72,11 @@ def build(verbose: bool = True, jobs: int | None = None) -> str:
     with ThreadPoolExecutor(max_workers=jobs) as ex:
         list(ex.map(lambda c: _run(c, verbose), cmds))
     tmp = LIB_PATH + ".tmp"
-    _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *objs], verbose)
+    # export only the C ABI (q8_*): the version script keeps every internal
+    # launcher and helper local to the library
+    vscript = os.path.join(CSRC, "libq8hip.map")
+    _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", f"-Wl,--version-script={vscript}",
+          "-o", tmp, *objs], verbose)
     os.replace(tmp, LIB_PATH)
     return LIB_PATH
 

@@ -32,6 +32,17 @@ def test_header_symbols_exported():
     assert set(names) == set(q8hip.SIGNATURES), set(names) ^ set(q8hip.SIGNATURES)
 
 
+def test_only_the_c_abi_is_exported():
+    """The dynamic symbol table holds the q8_* entry points and no internal
+    launcher or helper (the link's version script)."""
+    import subprocess
+    out = subprocess.run(["nm", "-D", "--defined-only", q8hip.LIB_PATH], capture_output=True,
+                         text=True, check=True).stdout
+    names = [line.split()[-1] for line in out.splitlines() if line.strip()]
+    names = [n for n in names if not n.startswith("q8_")]
+    assert names == [], names[:10]
+
+
 def test_version_and_rowstride():
     lib = q8hip.lib()
     assert lib.q8_version() == 100
