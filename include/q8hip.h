@@ -79,7 +79,8 @@ void *q8_get_stream(q8_ctx *ctx);
 int q8_sync(q8_ctx *ctx);
 
 /* Message of the last failing call on this context ("" if none).  With
- * ctx == NULL: the last error of a failed q8_create on this thread. */
+ * ctx == NULL: the last error of a failed q8_create or q8_linear_noalloc on
+ * this thread. */
 const char *q8_last_error(q8_ctx *ctx);
 
 /* ---- buffers (arenas) --------------------------------------------------- */
@@ -131,6 +132,28 @@ int q8_linear(q8_ctx *ctx, q8_buf *w, uint64_t owt_u16, q8_buf *a,
  * M = 512 bf16-activation prefill case. */
 int q8_linear_bf16act(q8_ctx *ctx, q8_buf *w, uint64_t owt_u16, q8_buf *x,
                       uint64_t ox_bf16, q8_buf *y, uint64_t oy_f32, int64_t s,
+                      int64_t m, int64_t n, int G, int scale_dtype);
+
+/* q8_linear on raw device pointers, without any allocation.  No counterpart
+ * in the reference: it is for callers that cannot call hipMalloc (code under
+ * HIP graph capture, tight serving loops, harnesses that forbid it), who
+ * need no context.  y[s, n] = x[s, m] . deq(W[n, m])^T exactly as q8_linear
+ * computes it (same kernels and split decisions, so the same bits, except
+ * from s = 32 on when the rows do not fit the 16 MiB activation buffer at
+ * once: they then run in chunks, within the same 1e-3 contract), on
+ * hip_stream (NULL: the null stream), which must belong to the current
+ * device.  w points at packed row 0 (rows back to back); x and y are f32
+ * and must not overlap.
+ * Scratch: one fixed array of Q8_NOALLOC_SCRATCH_BYTES per GPU, held until
+ * the process ends (split-K partials, arrival counters, and a 16 MiB
+ * binary16 activation buffer for s >= 32, which takes the rows in chunks).
+ * Limit: from s = 32 on, one activation row (2 m + 4 bytes) plus 4 n bytes
+ * must fit in 16 MiB, else Q8_ERR_SHAPE.  Every call on a GPU shares that
+ * GPU's array: calls that overlap on one GPU (two streams, two threads)
+ * race; calls in one stream's order do not.  Errors: status code, message in
+ * q8_last_error(NULL) on the calling thread. */
+#define Q8_NOALLOC_SCRATCH_BYTES (33816576LL)   /* 16 MiB + 256 KiB + 16 MiB */
+int q8_linear_noalloc(void *hip_stream, const void *w, const float *x, float *y, int64_t s,
                       int64_t m, int64_t n, int G, int scale_dtype);
 
 /* y[i, c] = f32(q[id_i, c]) * f32(scale[id_i, c / G]) for i < s, c < d:

@@ -13,6 +13,7 @@
 #include <cstdint>
 #include <cstdio>
 #include <cstring>
+#include <mutex>
 #include <new>
 #include <string>
 
@@ -58,6 +59,8 @@ struct q8_buf {
 
 namespace {
 
+// Message of the last failing q8_create or q8_linear_noalloc on this thread
+// (calls that have no context to hold it).
 thread_local std::string g_create_err;
 
 int fail(q8_ctx *ctx, int code, const char *fmt, ...) {
@@ -479,6 +482,37 @@ hipError_t run_gemm(q8_ctx *ctx, q8::LinearArgs la) {
   return run_gemm_in(la, ctx->act16, kAct16Bytes, ctx->stream);
 }
 
+// Device memory a W8A32 linear may use besides its inputs and outputs: the
+// split-K partial sums, the small-batch arrival counters (zero between
+// calls) and the GEMM's binary16 activation buffer.
+struct Scratch {
+  float *ws;
+  int64_t ws_floats;
+  int *cnt;
+  int64_t cnt_n;
+  void *act16;
+  int64_t act_bytes;
+};
+
+// The W8A32 linear of q8_linear on resolved pointers: GEMM from
+// kGemmMinRows rows, the few-row and small-batch MFMA kernels from
+// kSkinnyMinRows, the GEMV otherwise (and for unaligned operands).
+hipError_t dispatch_linear(q8::LinearArgs la, const Scratch &sc, hipStream_t st) {
+  la.ws = sc.ws;
+  la.ws_floats = sc.ws_floats;
+  la.cnt = sc.cnt;
+  la.cnt_n = sc.cnt_n;
+  if (la.s >= kGemmMinRows && gemm_aligned(la)) return run_gemm_in(la, sc.act16, sc.act_bytes, st);
+  if (la.s >= kSkinnyMinRows && la.s <= q8::kSkinny4MaxRows && gemm_aligned(la))
+    return q8::launch_skinny4(la, st);
+  if (la.s >= kSkinnyMinRows && gemm_aligned(la)) return q8::launch_skinny(la, st);
+  return q8::launch_gemv(la, st);
+}
+
+Scratch ctx_scratch(q8_ctx *ctx) {
+  return Scratch{ctx->gemm_ws, kGemmWsFloats, ctx->kcount, kCountInts, ctx->act16, kAct16Bytes};
+}
+
 }  // namespace
 
 int q8_linear(q8_ctx *ctx, q8_buf *w, uint64_t owt_u16, q8_buf *a, uint64_t ox_f32,
@@ -513,17 +547,7 @@ int q8_linear(q8_ctx *ctx, q8_buf *w, uint64_t owt_u16, q8_buf *a, uint64_t ox_f
   la.n = n;
   la.G = G;
   la.kind = scale_dtype;
-  hipError_t e;
-  if (s >= kGemmMinRows && gemm_aligned(la)) {
-    e = run_gemm(ctx, la);
-  } else if (s >= kSkinnyMinRows && s <= q8::kSkinny4MaxRows && gemm_aligned(la)) {
-    e = q8::launch_skinny4(la, ctx->stream);
-  } else if (s >= kSkinnyMinRows && gemm_aligned(la)) {
-    attach_gemm_workspace(ctx, la);
-    e = q8::launch_skinny(la, ctx->stream);
-  } else {
-    e = q8::launch_gemv(la, ctx->stream);
-  }
+  hipError_t e = dispatch_linear(la, ctx_scratch(ctx), ctx->stream);
   if (e != hipSuccess) return hip_fail(ctx, e, "q8_linear launch");
   return ok(ctx);
 }
@@ -570,6 +594,123 @@ int q8_linear_bf16act(q8_ctx *ctx, q8_buf *w, uint64_t owt_u16, q8_buf *x, uint6
   }
   if (e != hipSuccess) return hip_fail(ctx, e, "q8_linear_bf16act launch");
   return ok(ctx);
+}
+
+// ---- allocation-free linear -----------------------------------------------------
+//
+// q8_linear_noalloc keeps its scratch in one fixed device array per GPU
+// instead of a context's workspace: 16 MiB of split-K partial sums and 256
+// KiB of arrival counters (the sizes of a context's, so it makes the same
+// split decisions as q8_linear), then the GEMM's 16 MiB binary16
+// activation buffer.  The array's name is a host-side stand-in: host code
+// only ever passes the address hipGetSymbolAddress returns for the current
+// device (noalloc_scratch).
+
+namespace {
+constexpr int64_t kNoAllocWsFloats = kGemmWsFloats;
+constexpr int64_t kNoAllocCountInts = kCountInts;
+constexpr int64_t kNoAllocAct16Bytes = (int64_t)16 << 20;
+constexpr int64_t kNoAllocBytes =
+    kNoAllocWsFloats * 4 + kNoAllocCountInts * 4 + kNoAllocAct16Bytes;
+static_assert(kNoAllocBytes == Q8_NOALLOC_SCRATCH_BYTES, "scratch size differs from the header");
+}  // namespace
+
+static __device__ __align__(256) unsigned char scratch[kNoAllocBytes];
+
+namespace {
+
+__global__ void zero_ints_kernel(int *p, int64_t n) {
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * blockDim.x)
+    p[i] = 0;
+}
+
+constexpr int kNoAllocMaxDevices = 64;
+std::mutex g_noalloc_mu;
+void *g_noalloc_ptr[kNoAllocMaxDevices];   // scratch's device address per device
+
+// Set-up, once per device (the first call on it), with that device current:
+// resolve this device's copy of `scratch` and clear its arrival counters
+// with a fill kernel on the caller's stream (the kernels that use them
+// leave them zero again, so later calls need no clear).
+int noalloc_scratch(int dev, hipStream_t st, Scratch *out) {
+  std::lock_guard<std::mutex> lock(g_noalloc_mu);
+  void *base = g_noalloc_ptr[dev];
+  if (!base) {
+    hipError_t e = hipGetSymbolAddress(&base, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !base)
+      return hip_fail(nullptr, e != hipSuccess ? e : hipErrorInvalidSymbol,
+                      "q8_linear_noalloc: hipGetSymbolAddress(scratch)");
+    int *cnt = reinterpret_cast<int *>(static_cast<uint8_t *>(base) + kNoAllocWsFloats * 4);
+    hipLaunchKernelGGL(zero_ints_kernel, dim3(64), dim3(256), 0, st, cnt, kNoAllocCountInts);
+    e = hipGetLastError();
+    if (e != hipSuccess) return hip_fail(nullptr, e, "q8_linear_noalloc: counter clear");
+    g_noalloc_ptr[dev] = base;
+  }
+  uint8_t *b = static_cast<uint8_t *>(base);
+  out->ws = reinterpret_cast<float *>(b);
+  out->ws_floats = kNoAllocWsFloats;
+  out->cnt = reinterpret_cast<int *>(b + kNoAllocWsFloats * 4);
+  out->cnt_n = kNoAllocCountInts;
+  out->act16 = b + kNoAllocWsFloats * 4 + kNoAllocCountInts * 4;
+  out->act_bytes = kNoAllocAct16Bytes;
+  return Q8_OK;
+}
+
+}  // namespace
+
+int q8_linear_noalloc(void *hip_stream, const void *w, const float *x, float *y, int64_t s,
+                      int64_t m, int64_t n, int G, int scale_dtype) {
+  const char *what = "q8_linear_noalloc";
+  if (int rc = check_layout(nullptr, m, G, scale_dtype, what)) return rc;
+  if (s < 0 || n < 0)
+    return fail(nullptr, Q8_ERR_SHAPE, "%s: s=%lld and n=%lld must be >= 0", what, (long long)s,
+                (long long)n);
+  if (s == 0 || n == 0) return Q8_OK;
+  if (!w || !x || !y) return fail(nullptr, Q8_ERR_ARG, "%s: null weight, x or y pointer", what);
+  const unsigned __int128 xb = (unsigned __int128)s * (uint64_t)m * 4,
+                          yb = (unsigned __int128)s * (uint64_t)n * 4;
+  if (xb >= ((unsigned __int128)1 << 62) || yb >= ((unsigned __int128)1 << 62))
+    return fail(nullptr, Q8_ERR_SHAPE, "%s: s=%lld, m=%lld, n=%lld out of range", what,
+                (long long)s, (long long)m, (long long)n);
+  const uintptr_t x0 = reinterpret_cast<uintptr_t>(x), y0 = reinterpret_cast<uintptr_t>(y);
+  if (overlaps(x0, x0 + (uint64_t)xb, y0, y0 + (uint64_t)yb))
+    return fail(nullptr, Q8_ERR_ARG, "%s: x and y overlap", what);
+  if (s >= kGemmMinRows && !gemm_fits(kNoAllocAct16Bytes, m, n))
+    return fail(nullptr, Q8_ERR_SHAPE, "%s: m=%lld, n=%lld exceed the %lld-byte activation "
+                "buffer of the allocation-free scratch (one row of 2 m + 4 bytes plus 4 n "
+                "bytes must fit)", what, (long long)m, (long long)n,
+                (long long)kNoAllocAct16Bytes);
+  hipStream_t st = static_cast<hipStream_t>(hip_stream);
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return hip_fail(nullptr, e, "q8_linear_noalloc: hipGetDevice");
+  if (dev < 0 || dev >= kNoAllocMaxDevices)
+    return fail(nullptr, Q8_ERR_ARG, "%s: device %d out of range", what, dev);
+  if (st) {
+    int sdev = -1;
+    e = hipStreamGetDevice(st, &sdev);
+    if (e != hipSuccess) return hip_fail(nullptr, e, "q8_linear_noalloc: hipStreamGetDevice");
+    if (sdev != dev)
+      return fail(nullptr, Q8_ERR_ARG, "%s: the stream belongs to device %d, the current "
+                  "device is %d", what, sdev, dev);
+  }
+  Scratch sc;
+  if (int rc = noalloc_scratch(dev, st, &sc)) return rc;
+  q8::LinearArgs la;
+  la.w = static_cast<const uint8_t *>(w);
+  la.row_bytes = rowstride_u16(m, G, scale_dtype) * 2;
+  la.x = x;
+  la.x_is_bf16 = 0;
+  la.y = y;
+  la.s = s;
+  la.m = m;
+  la.n = n;
+  la.G = G;
+  la.kind = scale_dtype;
+  e = dispatch_linear(la, sc, st);
+  if (e != hipSuccess) return hip_fail(nullptr, e, "q8_linear_noalloc launch");
+  return Q8_OK;
 }
 
 int q8_embed_gather(q8_ctx *ctx, q8_buf *w, uint64_t oemb_u16, q8_buf *ids, uint64_t oids_i32,

@@ -68,6 +68,7 @@ SIGNATURES = {
     "q8_quantize_pack": (_I, [_P, _P, _U64, _I, _I64, _I64, _P, _U64, _I, _I]),
     "q8_linear": (_I, [_P, _P, _U64, _P, _U64, _U64, _I64, _I64, _I64, _I, _I]),
     "q8_linear_bf16act": (_I, [_P, _P, _U64, _P, _U64, _P, _U64, _I64, _I64, _I64, _I, _I]),
+    "q8_linear_noalloc": (_I, [_P, _P, _P, _P, _I64, _I64, _I64, _I, _I]),
     "q8_embed_gather": (_I, [_P, _P, _U64, _P, _U64, _P, _U64, _I64, _I64, _I64, _I, _I]),
     "q8_linear_fused": (_I, [_P, _P, _U64, _P, _U64, _U64, _I64, _I64, _I, _I, _I, _U64,
                             ctypes.c_float, _I, _U64]),
@@ -324,6 +325,23 @@ def linear_bf16act(ctx: Context, w: Buffer, owt_u16: int, x: Buffer, ox_bf16: in
     ctx.check(ctx._lib.q8_linear_bf16act(ctx.h, w.h, int(owt_u16), x.h, int(ox_bf16), y.h,
                                          int(oy_f32), int(s), int(m), int(n), int(G),
                                          scale_code(scale)))
+
+
+NOALLOC_SCRATCH_BYTES = 33816576
+
+
+def linear_noalloc(hip_stream: int | None, w_ptr: int, x_ptr: int, y_ptr: int, s: int, m: int,
+                   n: int, G: int = 64, scale="f16") -> None:
+    """q8_linear on raw device pointers with no allocation (scratch in the
+    library's fixed per-GPU array): q8_linear_noalloc.  Raises Q8Error with
+    the calling thread's message on failure."""
+    L = lib()
+    rc = L.q8_linear_noalloc(hip_stream or None, ctypes.c_void_p(w_ptr), ctypes.c_void_p(x_ptr),
+                             ctypes.c_void_p(y_ptr), int(s), int(m), int(n), int(G),
+                             scale_code(scale))
+    if rc != Q8_OK:
+        msg = L.q8_last_error(None)
+        raise Q8Error(rc, msg.decode() if isinstance(msg, bytes) else str(msg))
 
 
 def embed_gather(ctx: Context, w: Buffer, oemb_u16: int, ids: Buffer, oids_i32: int, a: Buffer,
