@@ -1,57 +1,69 @@
 #!/usr/bin/env python3
 """Benchmark of the Q8 (INT8 group-quantized, W8A32) path on one MI355X.
 
-Default workload -- Llama-3.2-1B decode step, batch 1, at a KV context of
-1024 tokens: the whole token step of the reference's Q8 model
+Default run (`--workload all`, what the driver runs): one JSON line.
+
+Headline -- Llama-3.2-1B decode step, batch 1, at a KV context of 1024
+tokens: the whole token step of the reference's Q8 model
 (qwen3_mojo/src/qwen_q8.mojo:127-162 with run_layer_q8,
 src/llama_q8.mojo:144-230) on libq8hip -- embedding gather, 16 layers of
 [rmsnorm + fused q|k|v GEMV 2048->3072, RoPE + fp16 KV append + attention
 (context splits, then their merge), o GEMV 2048->2048 + residual, rmsnorm +
 fused gate|up GEMV 2048->16384 + swiglu, down GEMV 8192->2048 + residual],
-final rmsnorm + tied lm_head GEMV 2048->128256, argmax: six launches per
-layer, the norms, swiglu and residual adds folded into the GEMVs.  Weights
-are random bf16 ~N(0, 0.02) per tensor, packed on the GPU by
-q8_quantize_pack into one weight arena (G=64, f16 scales: the reference
-layout); norms ~1; the 1024-token KV context is random fp16.
+final rmsnorm + tied lm_head GEMV 2048->128256, argmax.  Weights are
+random bf16 ~N(0, 0.02) per tensor, packed on the GPU by q8_quantize_pack
+into one weight arena (G=64, f16 scales: the reference layout); norms ~1;
+the 1024-token KV context is random fp16.  A step is one token: one replay
+of a HIP graph that reads the token id and the position from device memory
+and writes the argmax id and the next position back.  `value` is the
+step's streaming throughput in GB/s: packed weight bytes (1.274 GB) plus
+the KV bytes read at the step's context length, divided by the time per
+token (HIP events on the library's stream around K replays);
+config.tok_s is tokens per second.
 
-A step is one token: one replay of a HIP graph that reads the token id and
-the position from device memory and writes the argmax id and the next
-position back.  `value` is the step's streaming throughput in GB/s: packed
-weight bytes (1.274 GB) plus the KV bytes read at the step's context length,
-divided by the time per token (HIP events on the library's stream around K
-replays); config.tok_s is tokens per second.
+`roofline` is for the step's dominant kernel by GPU time, the fused gate|up
+GEMV (rmsnorm prologue, 2048 -> 16384, swiglu epilogue; 16 launches per
+step): its algorithmic bytes per launch (packed rows + x + norm weights +
+the 8192 outputs) over its average launch duration, from HIP events on the
+library's stream around replays of a graph of the 16 layers' gate|up
+launches (554 MB of weights in turn, more than the 256 MB Infinity Cache).
+`roofline_lm_head` is the same figure for the lm_head GEMV, the largest
+single launch.  `roofline.traffic` is the kernel's HBM bytes per launch from
+rocprofv3 FETCH_SIZE and WRITE_SIZE passes over --workload gateup-pmc, each
+scaled by what the counter reads for a copy kernel of known size; the
+figures are read from profiles/gateup_gemv_pmc.md.
 
-`roofline` is for the lm_head GEMV (the largest launch, 128256 x 2048):
-its algorithmic bytes per launch divided by its average launch duration,
-timed with HIP events around back-to-back launches that alternate between
-two copies of the table (542 MB, more than the 256 MB Infinity Cache).
+`configs` holds the other configurations, each measured in the same run:
+  linear_8192x2048   one Q8 linear, x f32 [1, 2048], 64 rotated weight
+                     copies (>= 1.1 GB), both layouts
+  prefill_1b_m512    Llama-3.2-1B prefill linears, M = 512 bf16 activations,
+                     16 layers x 7 projections (q|k|v and gate|up as one GEMM
+                     each over their adjacent rows), per shape and aggregate
+  qwen3_8b_decode    Qwen3-8B decode linears (36 layers + lm_head), batch 1 /
+                     4 / 16, group 32 f32 scales
+  llama31_8b_e2e     Llama-3.1-8B: prefill of 2048 random ids (seed 3), then
+                     256 greedy decode steps (one HIP graph per token)
+  qwen3_06b_decode   the reference's own Q8 model (Qwen3-0.6B, q/k head
+                     norms, tied head 1024 -> 151936) at KV context 128
 
 `cpu_baseline` runs the oracle's group-major fp32 restatement of k_mm_q8
-(oracle/q8_oracle.c, OpenMP) over the same packed weights on the host cores.
+(oracle/q8_oracle.c, OpenMP) over the same packed weights on all host
+cores; its `legs` add the same on one core and numpy's BLAS x @ W.T over
+the dequantized weights (the form of scripts/gen_oracle.py:74-93).
 
-Other workloads (--workload):
+Other workloads (--workload) run one of these alone:
+  decode   the headline only (with its roofline and CPU legs)
   decode-linears  only the 65 Q8 GEMVs of the Llama-3.2-1B step, one graph
-  linear   one Q8 linear 8192x2048, x f32 [1, 2048], weights rotated over
-           >= 64 copies (>= 1.1 GB) so no launch reads a cached matrix
-  prefill  Llama-3.2-1B prefill linears, M = 512 bf16 activations, all 16
-           layers x 7 projections (q|k|v and gate|up as one GEMM each over
-           their adjacent rows) on the f16-MFMA dequant-GEMM (TFLOP/s), group 32
-  qwen8b   Qwen3-8B decode linears, --batch 1 / 4 / 16, group 32
-  e2e-8b   Llama-3.1-8B end to end: prefill of 2048 random ids (seed 3),
-           then 256 greedy decode steps (one HIP graph per token); value is
-           decode tok/s, config holds the prefill time
-  qwen3-06b  the reference's own Q8 model, Qwen3-0.6B (q/k head norms, tied
-           lm_head 1024 -> 151936), decode step at KV context 128; value is
-           tok/s, vs_baseline against the reference's published 29 tok/s
-           (Apple M4, QUANTIZATION.md:28)
-  lmhead-pmc  the launches the HBM-traffic counter passes read: 3 copies of
-           1 GiB by torch's copy kernel (the calibration of known size), then
-           8 lm_head GEMVs 128256x2048 alternating over two tables
-
-`roofline.traffic` (default workload) is the lm_head GEMV's HBM bytes per
-launch measured by rocprofv3 FETCH_SIZE and WRITE_SIZE passes over
---workload lmhead-pmc, each scaled by the copy kernel's known bytes / its
-counter reading; the figures are read from profiles/lm_head_gemv_pmc.md.
+  linear   the single linear (--layout picks one layout)
+  prefill  the 1B prefill GEMMs
+  qwen8b   Qwen3-8B decode linears, --batch 1 / 4 / 16
+  e2e-8b   Llama-3.1-8B end to end
+  qwen3-06b  Qwen3-0.6B decode; value is tok/s, vs_baseline against the
+           reference's published 29 tok/s (Apple M4, QUANTIZATION.md:28)
+  lmhead-pmc / gateup-pmc  the launches the HBM-traffic counter passes read:
+           3 copies of 1 GiB by torch's copy kernel (the calibration of
+           known size), then 8 lm_head GEMVs 128256x2048 alternating over
+           two tables / 32 fused gate|up GEMVs over the 16 layers
 """
 
 from __future__ import annotations
@@ -82,15 +94,16 @@ def parse():
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=50)
     p.add_argument("--warmup", type=int, default=5)
-    p.add_argument("--workload", default="decode",
-                   choices=["decode", "decode-linears", "linear", "prefill", "qwen8b",
-                            "e2e-8b", "lmhead-pmc", "qwen3-06b"])
+    p.add_argument("--workload", default="all",
+                   choices=["all", "decode", "decode-linears", "linear", "prefill", "qwen8b",
+                            "e2e-8b", "lmhead-pmc", "gateup-pmc", "qwen3-06b"])
     p.add_argument("--layout", default=None, choices=["g64f16", "g32f32"],
                    help="packed layout (default: g64f16; g32f32 for --workload linear)")
     p.add_argument("--batch", type=int, default=1)
     p.add_argument("--no-graph", action="store_true", help="launch eagerly, no HIP graph")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
-    p.add_argument("--cpu-seconds", type=float, default=10.0)
+    p.add_argument("--cpu-seconds", type=float, default=8.0,
+                   help="seconds per CPU-baseline leg")
     return p.parse_args()
 
 
@@ -118,8 +131,11 @@ class Bench:
         from lama32_mojo_amd import q8hip
         self.q8hip = q8hip
         self.args, self.ctx, self.torch = args, ctx, torch
-        self.G, self.scale, self.sb = layout(args.layout)
+        self.set_layout(args.layout)
         self.stream = torch.cuda.ExternalStream(ctx.stream)
+
+    def set_layout(self, name):
+        self.G, self.scale, self.sb = layout(name)
 
     # ---- weights --------------------------------------------------------------
     def pack_arena(self, shapes, seeds):
@@ -207,37 +223,54 @@ def decode_shapes(cfg):
     return shapes, seeds
 
 
+def decode_linears(B: Bench, cfg, batches, head_copy=False):
+    """The decode step's Q8 linears (fused q|k|v, o, fused gate|up, down per
+    layer, then the lm_head) as one captured graph per batch size; returns
+    ({batch: record}, (w, offs, shapes)) with the packed arena still alive."""
+    q8hip, ctx = B.q8hip, B.ctx
+    G, scale, sb = B.G, B.scale, B.sb
+    shapes, seeds = decode_shapes(cfg)
+    head = len(shapes) - 1
+    extra = ([shapes[head]], [seeds[head] + 1]) if head_copy else ([], [])
+    w, offs = B.pack_arena(shapes + extra[0], seeds + extra[1])
+    smax = max(batches)
+    aoffs, top = [], 32
+    for n, m in shapes:
+        aoffs.append((top, top + smax * m))
+        top += smax * m + smax * n
+    xa = B.activations(top, 1)
+    a = q8hip.Buffer.wrap(ctx, xa.data_ptr(), 4 * top)
+    out = {}
+    for s in batches:
+        step_bytes = sum(linear_bytes(s, m, n, G, sb) for n, m in shapes)
+        launches = [(lambda i=i, s=s: q8hip.linear(ctx, w, offs[i], a, aoffs[i][0], aoffs[i][1],
+                                                    s, shapes[i][1], shapes[i][0], G, scale))
+                    for i in range(len(shapes))]
+        graph = B.capture(launches)
+        step = B.run_graph_or_eager(graph, launches)
+        ms, wall = B.time_steps(step, B.args.steps, B.args.warmup)
+        if graph is not None:
+            graph.destroy()
+        gbs = step_bytes / (ms * 1e-3) / 1e9
+        out[s] = {"batch": s, "ms_per_step": round(ms, 4), "gbs": round(gbs, 1),
+                  "frac_hbm": round(gbs / HBM_PEAK_GBS, 4), "bytes_per_step": step_bytes,
+                  "graph": graph is not None, "wall_s": round(wall, 3)}
+    B.keep = (xa, a)
+    return out, (w, offs, shapes)
+
+
 def run_decode(B: Bench, cfg):
     args, q8hip, ctx = B.args, B.q8hip, B.ctx
     G, scale, sb = B.G, B.scale, B.sb
     s = args.batch
-    shapes, seeds = decode_shapes(cfg)
+    recs, (w, offs, shapes) = decode_linears(B, cfg, [s], head_copy=True)
+    rec = recs[s]
     head = len(shapes) - 1
     n_h, m_h = shapes[head]
-    # lm_head twice (second copy only for the roofline timing loop)
-    w, offs = B.pack_arena(shapes + [shapes[head]], seeds + [seeds[head] + 1])
-    aoffs, top = [], 32
-    for n, m in shapes:
-        aoffs.append((top, top + s * m))
-        top += s * m + s * n
-    xa = B.activations(top, 1)
-    a = q8hip.Buffer.wrap(ctx, xa.data_ptr(), 4 * top)
-    step_bytes = sum(linear_bytes(s, m, n, G, sb) for n, m in shapes)
-
-    def launcher(i, woff=None):
-        n, m = shapes[i]
-        ox, oy = aoffs[i]
-        wo = offs[i] if woff is None else woff
-        return lambda: q8hip.linear(ctx, w, wo, a, ox, oy, s, m, n, G, scale)
-
-    launches = [launcher(i) for i in range(len(shapes))]
-    graph = B.capture(launches)
-    step = B.run_graph_or_eager(graph, launches)
-    ms, wall = B.time_steps(step, args.steps, args.warmup)
-    value = step_bytes / (ms * 1e-3) / 1e9
-
-    # roofline kernel: lm_head GEMV, back-to-back over two copies
-    heads = [launcher(head), launcher(head, offs[head + 1])]
+    _, a = B.keep
+    oxh = 32
+    heads = [(lambda o=o: q8hip.linear(ctx, w, o, a, oxh, oxh + s * m_h, s, m_h, n_h, G, scale))
+             for o in (offs[head], offs[head + 1])]
     kk = max(args.steps, 20)
     head_ms, _ = B.time_steps(lambda: [h() for h in heads], kk // 2, 2)
     head_ms /= 2
@@ -250,18 +283,15 @@ def run_decode(B: Bench, cfg):
         for i in list(range(4)) + [head]:
             n, m = shapes[i]
             rs = q8hip.rowstride_u16(m, G, scale)
-            pk = w.download((n, rs), np.uint16, 2 * offs[i])
-            packs.append((pk, s, m))
+            packs.append((w.download((n, rs), np.uint16, 2 * offs[i]), s, m))
         cpu = cpu_baseline(packs, G, scale, args.cpu_seconds,
                            "(layer-0 q|k|v, o, gate|up, down + lm_head)")
-    if graph is not None:
-        graph.destroy()
     w.free()
     return {
         "metric": f"Q8 GEMV GB/s (% of HBM peak); decode tok/s batch {s}, {cfg['name']} Q8",
-        "value": round(value, 1),
+        "value": rec["gbs"],
         "unit": "GB/s",
-        "ms_per_step": round(ms, 4),
+        "ms_per_step": rec["ms_per_step"],
         "higher_is_better": True,
         "dtype": "int8xf32",
         "data": "synthetic (random-init N(0,0.02) bf16 weights packed on GPU; x ~ N(0,1))",
@@ -269,13 +299,13 @@ def run_decode(B: Bench, cfg):
                                f"({len(shapes)} GEMVs, fused qkv / gate|up, lm_head "
                                f"{n_h}x{m_h})",
                    "layout": f"G={G} {scale} scales", "batch": s,
-                   "bytes_per_step": step_bytes, "graph": graph is not None,
-                   "pct_hbm_peak": round(100 * value / HBM_PEAK_GBS, 1),
-                   "linears_only_steps_per_s": round(1000.0 / ms, 1),
-                   "wall_s": round(wall, 3)},
+                   "bytes_per_step": rec["bytes_per_step"], "graph": rec["graph"],
+                   "pct_hbm_peak": round(100 * rec["frac_hbm"], 1),
+                   "linears_only_steps_per_s": round(1000.0 / rec["ms_per_step"], 1),
+                   "wall_s": rec["wall_s"]},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
-                     "traffic": measured_traffic(G, sb),
+                     "traffic": None,
                      "kernel": f"lm_head GEMV {n_h}x{m_h}: {head_bytes} B/launch, "
                                f"{head_ms * 1e3:.2f} us avg over {kk} launches"},
         "cpu_baseline": cpu,
@@ -286,13 +316,13 @@ def run_decode(B: Bench, cfg):
 # full decode step (Llama-3.2-1B model on the layer kernels, captured graph)
 # ---------------------------------------------------------------------------
 
-def measured_traffic(G: int, sb: int):
-    """The lm_head GEMV's HBM bytes per launch from the committed counter
-    passes (profiles/lm_head_gemv_pmc.md), for the layout they measured."""
+def measured_traffic(profile: str, G: int, sb: int):
+    """HBM bytes per launch from the committed counter passes (a profiles/
+    summary), for the layout they measured (G=64, f16 scales)."""
     if (G, sb) != (64, 2):
         return None
     try:
-        with open(os.path.join(ROOT, "profiles", "lm_head_gemv_pmc.md")) as f:
+        with open(os.path.join(ROOT, "profiles", profile)) as f:
             for line in f:
                 if line.strip().startswith("- traffic_bytes_per_launch:"):
                     return int(line.split(":", 1)[1])
@@ -301,7 +331,78 @@ def measured_traffic(G: int, sb: int):
     return None
 
 
-def run_decode_model(B: Bench, ctxlen: int = 1024, cfg=None, tok_metric: bool = False):
+def fused_gateup_bytes(H, I, G, sb):
+    """Algorithmic bytes of one fused gate|up launch: 2I packed rows of H,
+    x (H f32), the bf16 norm weights (H) and the I swiglu outputs."""
+    return 2 * I * (H + (H // G) * sb) + 4 * H + 2 * H + 4 * I
+
+
+def gateup_launches(B: Bench, m):
+    """Closures for the fused gate|up GEMV of every layer of model m (norm +
+    gate|up + swiglu, as in the step), over a separate input / output."""
+    q8hip, ctx = B.q8hip, B.ctx
+    cfg = m.cfg
+    H, I = cfg.hidden, cfg.inter
+    xa = B.activations(32 + H + I, 9)
+    a = q8hip.Buffer.wrap(ctx, xa.data_ptr(), 4 * (32 + H + I))
+    B.keep_gu = (xa, a)
+    return [(lambda lo=lo: q8hip.linear_fused(ctx, m.w.buf, lo.gate, a, 32, 32 + H, H, 2 * I,
+                                              m.G, m.scale, pre=q8hip.PRE_RMSNORM,
+                                              onorm_u16=lo.post_norm, eps=cfg.eps,
+                                              post=q8hip.POST_SWIGLU))
+            for lo in m.lo]
+
+
+def gateup_roofline(B: Bench, m):
+    """The dominant kernel of the decode step: HIP events around replays of
+    a graph of every layer's fused gate|up launch (the step's own launch
+    setting; 16 different weight matrices in turn)."""
+    cfg = m.cfg
+    launches = gateup_launches(B, m)
+    B.ctx.graph_begin()
+    for f in launches:
+        f()
+    g = B.ctx.graph_end()
+    reps = max(B.args.steps, 20)
+    ms, _ = B.time_steps(lambda: g.launch(), reps, 3)
+    g.destroy()
+    per = ms / len(launches)
+    nbytes = fused_gateup_bytes(cfg.hidden, cfg.inter, B.G, B.sb)
+    achieved = nbytes / (per * 1e-3) / 1e9
+    return {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
+            "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "traffic": measured_traffic("gateup_gemv_pmc.md", B.G, B.sb),
+            "kernel": f"fused rmsnorm + gate|up GEMV {2 * cfg.inter}x{cfg.hidden} + swiglu "
+                      f"(the step's dominant kernel): {nbytes} B/launch, {per * 1e3:.2f} us avg "
+                      f"over {reps} x {len(launches)} launches (graph replays)"}
+
+
+def lm_head_roofline(B: Bench, cfg):
+    """The lm_head GEMV back-to-back over two copies of the table (the 256
+    MB Infinity Cache cannot serve a repeat)."""
+    q8hip, ctx = B.q8hip, B.ctx
+    G, scale, sb = B.G, B.scale, B.sb
+    n_h, m_h = cfg.vocab, cfg.hidden
+    w2, offs2 = B.pack_arena([(n_h, m_h), (n_h, m_h)], [5, 6])
+    xa = B.activations(32 + m_h + n_h, 1)
+    a = q8hip.Buffer.wrap(ctx, xa.data_ptr(), 4 * (32 + m_h + n_h))
+    heads = [(lambda o=o: q8hip.linear(ctx, w2, o, a, 32, 32 + m_h, 1, m_h, n_h, G, scale))
+             for o in offs2]
+    kk = max(B.args.steps, 20)
+    head_ms, _ = B.time_steps(lambda: [h() for h in heads], kk // 2, 2)
+    head_ms /= 2
+    head_bytes = linear_bytes(1, m_h, n_h, G, sb)
+    achieved = head_bytes / (head_ms * 1e-3) / 1e9
+    w2.free()
+    return {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
+            "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "traffic": measured_traffic("lm_head_gemv_pmc.md", G, sb),
+            "kernel": f"lm_head GEMV {n_h}x{m_h}: {head_bytes} B/launch, "
+                      f"{head_ms * 1e3:.2f} us avg over {kk} launches"}
+
+
+def run_decode_model(B: Bench, ctxlen: int = 1024, cfg=None, tok_metric: bool = False,
+                     rooflines: bool = True, cpu: bool = True):
     from lama32_mojo_amd import model as gm
 
     args, q8hip, ctx, torch = B.args, B.q8hip, B.ctx, B.torch
@@ -335,33 +436,23 @@ def run_decode_model(B: Bench, ctxlen: int = 1024, cfg=None, tok_metric: bool = 
     value = step_bytes / (ms * 1e-3) / 1e9
     tok_s = 1000.0 / ms
 
-    # roofline kernel: the lm_head GEMV (tied embed table), back-to-back over
-    # two copies so the 256 MB MALL cannot serve it
-    n_h, m_h = cfg.vocab, cfg.hidden
-    w2, offs2 = B.pack_arena([(n_h, m_h), (n_h, m_h)], [5, 6])
-    xa = B.activations(32 + m_h + n_h, 1)
-    a = q8hip.Buffer.wrap(ctx, xa.data_ptr(), 4 * (32 + m_h + n_h))
-    heads = [(lambda o=o: q8hip.linear(ctx, w2, o, a, 32, 32 + m_h, 1, m_h, n_h, G, scale))
-             for o in offs2]
-    kk = max(K, 20)
-    head_ms, _ = B.time_steps(lambda: [h() for h in heads], kk // 2, 2)
-    head_ms /= 2
-    head_bytes = linear_bytes(1, m_h, n_h, G, sb)
-    achieved = head_bytes / (head_ms * 1e-3) / 1e9
-    w2.free()
-
-    cpu = None
-    if not args.no_cpu:
+    roof = gateup_roofline(B, m) if rooflines else None
+    cpu_res = None
+    if cpu and not args.no_cpu:
         lo = m.lo[0]
         H, QD, KVD, I = cfg.hidden, cfg.q_dim(), cfg.kv_dim(), cfg.inter
         packs = []
         for off, n, mm in [(lo.q, QD + 2 * KVD, H), (lo.o, H, QD), (lo.gate, 2 * I, H),
-                           (lo.down, H, I), (m.w.o("model.embed_tokens.weight"), n_h, m_h)]:
+                           (lo.down, H, I), (m.w.o(m._head_name()), cfg.vocab, H)]:
             rs = q8hip.rowstride_u16(mm, G, scale)
             packs.append((m.w.buf.download((n, rs), np.uint16, 2 * off), 1, mm))
-        cpu = cpu_baseline(packs, G, scale, args.cpu_seconds,
-                           "(layer-0 q|k|v, o, gate|up, down + lm_head)")
     m.close()
+    torch.cuda.empty_cache()
+    head_roof = lm_head_roofline(B, cfg) if rooflines else None
+    if cpu and not args.no_cpu:
+        cpu_res = cpu_baseline(packs, G, scale, args.cpu_seconds,
+                               "(layer-0 q|k|v, o, gate|up, down + lm_head)")
+        del packs
     if tok_metric:
         # the reference's published Q8 figure: Qwen3-0.6B decode, batch 1,
         # 22-29 tok/s on an Apple M4 GPU (QUANTIZATION.md:28)
@@ -370,7 +461,7 @@ def run_decode_model(B: Bench, ctxlen: int = 1024, cfg=None, tok_metric: bool = 
     else:
         head = {"metric": f"Q8 GEMV GB/s (% of HBM peak); decode tok/s batch 1, {cfg.name} Q8",
                 "value": round(value, 1), "unit": "GB/s"}
-    return {
+    out = {
         **head,
         "ms_per_step": round(ms, 4),
         "higher_is_better": True,
@@ -383,19 +474,18 @@ def run_decode_model(B: Bench, ctxlen: int = 1024, cfg=None, tok_metric: bool = 
                                + ("q/k head norms + " if cfg.qk_norm else "")
                                + "RoPE + fp16 KV append + attention, merge, o GEMV "
                                "+ residual, rmsnorm + fused gate|up GEMV + swiglu, down GEMV "
-                               f"+ residual), final norm + lm_head GEMV {n_h}x{m_h}, argmax; "
-                               "one HIP graph per token",
+                               f"+ residual), final norm + lm_head GEMV {cfg.vocab}x"
+                               f"{cfg.hidden}, argmax; one HIP graph per token",
                    "layout": f"G={G} {scale} scales", "batch": 1, "tok_s": round(tok_s, 1),
                    "weight_bytes_per_token": weight_bytes, "kv_bytes_per_token": kv_bytes,
                    "pct_hbm_peak": round(100 * value / HBM_PEAK_GBS, 1),
                    "graph": True, "wall_s": round(wall, 3)},
-        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
-                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
-                     "traffic": measured_traffic(G, sb),
-                     "kernel": f"lm_head GEMV {n_h}x{m_h}: {head_bytes} B/launch, "
-                               f"{head_ms * 1e3:.2f} us avg over {kk} launches"},
-        "cpu_baseline": cpu,
+        "cpu_baseline": cpu_res,
     }
+    if rooflines:
+        out["roofline"] = roof
+        out["roofline_lm_head"] = head_roof
+    return out
 
 
 def run_lmhead_pmc(B: Bench):
@@ -426,7 +516,37 @@ def run_lmhead_pmc(B: Bench):
                                             "lm_head_bytes": linear_bytes(1, m_h, n_h, G, sb)}}
 
 
-def run_e2e_8b(B: Bench, prompt: int = 2048, gen: int = 256):
+def run_gateup_pmc(B: Bench):
+    """The launches the gate|up counter passes read: the calibration copies,
+    then every layer's fused gate|up GEMV twice (Llama-3.2-1B, G=64 f16)."""
+    from lama32_mojo_amd import model as gm
+
+    torch = B.torch
+    nbytes = 1 << 30
+    src = torch.empty(nbytes // 4, dtype=torch.float32, device="cuda").normal_()
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    del src, dst
+    cfg = gm.LLAMA_32_1B
+    m = gm.Q8Llama(B.ctx, cfg, 64, B.G, B.scale, seed=7)
+    launches = gateup_launches(B, m)
+    for _ in range(2):
+        for f in launches:
+            f()
+    B.ctx.sync()
+    m.close()
+    nb = fused_gateup_bytes(cfg.hidden, cfg.inter, B.G, B.sb)
+    return {"metric": "counter-pass launches (no timing)", "value": 0, "unit": "none",
+            "ms_per_step": 0.0, "higher_is_better": True, "dtype": "int8xf32",
+            "data": "synthetic", "config": {"workload": "3 x 1 GiB copy, 32 x fused gate|up "
+                                                        f"GEMV {2 * cfg.inter}x{cfg.hidden}",
+                                            "copy_bytes": nbytes, "gateup_bytes": nb}}
+
+
+def run_e2e_8b(B: Bench, prompt: int = 2048, gen: int = 256, rooflines: bool = True):
     """Llama-3.1-8B: prefill `prompt` random ids, then `gen` greedy steps."""
     from lama32_mojo_amd import model as gm
 
@@ -456,19 +576,10 @@ def run_e2e_8b(B: Bench, prompt: int = 2048, gen: int = 256):
     lin_flops = 2.0 * prompt * L * H * (QD + 2 * KVD + I * 3) + 2.0 * prompt * L * QD * H
     weight_bytes = 2 * (m.w.top - 32)
 
-    # roofline kernel: the untied lm_head GEMV 128256 x 4096 over two copies
-    n_h, m_h = cfg.vocab, cfg.hidden
-    w2, offs2 = B.pack_arena([(n_h, m_h), (n_h, m_h)], [5, 6])
-    xa = B.activations(32 + m_h + n_h, 1)
-    a = q8hip.Buffer.wrap(ctx, xa.data_ptr(), 4 * (32 + m_h + n_h))
-    heads = [(lambda o=o: q8hip.linear(ctx, w2, o, a, 32, 32 + m_h, 1, m_h, n_h, G, scale))
-             for o in offs2]
-    head_ms, _ = B.time_steps(lambda: [h() for h in heads], 10, 2)
-    head_ms /= 2
-    head_bytes = linear_bytes(1, m_h, n_h, G, sb)
-    achieved = head_bytes / (head_ms * 1e-3) / 1e9
-    w2.free()
     m.close()
+    torch.cuda.empty_cache()
+    # roofline kernel: the untied lm_head GEMV 128256 x 4096 over two copies
+    roof = lm_head_roofline(B, cfg) if rooflines else None
     return {
         "metric": f"decode tok/s batch 1 after a {prompt}-token prefill, {cfg.name} Q8",
         "value": round(tok_s, 1),
@@ -488,11 +599,7 @@ def run_e2e_8b(B: Bench, prompt: int = 2048, gen: int = 256):
                    "decode_ms_per_token": round(ms, 4),
                    "decode_weight_gbs": round(weight_bytes / (ms * 1e-3) / 1e9, 1),
                    "e2e_ms": round(prefill_ms + gen * ms, 1), "wall_s": round(wall, 3)},
-        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
-                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
-                     "traffic": None,
-                     "kernel": f"lm_head GEMV {n_h}x{m_h}: {head_bytes} B/launch, "
-                               f"{head_ms * 1e3:.2f} us avg over 10 launches"},
+        "roofline": roof,
         "cpu_baseline": None,
     }
 
@@ -501,7 +608,7 @@ def run_e2e_8b(B: Bench, prompt: int = 2048, gen: int = 256):
 # single linear (8192 x 2048, rotated copies)
 # ---------------------------------------------------------------------------
 
-def run_linear(B: Bench):
+def run_linear(B: Bench, cpu: bool = True):
     args, q8hip, ctx = B.args, B.q8hip, B.ctx
     G, scale, sb = B.G, B.scale, B.sb
     n, m, s = 8192, 2048, args.batch
@@ -517,11 +624,11 @@ def run_linear(B: Bench):
     ms, wall = B.time_steps(step, max(args.steps // 4, 5), args.warmup)
     per_launch_ms = ms / copies
     value = one / (per_launch_ms * 1e-3) / 1e9
-    cpu = None
-    if not args.no_cpu:
+    cpu_res = None
+    if cpu and not args.no_cpu:
         rs = q8hip.rowstride_u16(m, G, scale)
         pk = w.download((n, rs), np.uint16, 2 * offs[0])
-        cpu = cpu_baseline([(pk, s, m)], G, scale, args.cpu_seconds, f"{n}x{m} linear")
+        cpu_res = cpu_baseline([(pk, s, m)], G, scale, args.cpu_seconds, f"{n}x{m} linear")
     if graph is not None:
         graph.destroy()
     w.free()
@@ -538,7 +645,7 @@ def run_linear(B: Bench):
         "roofline": {"bound": "hbm", "achieved": round(value, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(value / HBM_PEAK_GBS, 4), "traffic": None,
                      "kernel": f"GEMV {n}x{m}: {one} B/launch, {per_launch_ms * 1e3:.2f} us avg"},
-        "cpu_baseline": cpu,
+        "cpu_baseline": cpu_res,
     }
 
 
@@ -581,15 +688,29 @@ def run_prefill(B: Bench, cfg=LLAMA_1B, M=512):
     step = B.run_graph_or_eager(graph, launches)
     ms, wall = B.time_steps(step, max(args.steps // 5, 5), args.warmup)
     tflops = flops / (ms * 1e-3) / 1e12
-    # roofline kernel: the gate|up GEMM 512 x 16384 x 2048 (largest per-layer
-    # shape), timed per call with its binary16 pre-pass included
-    gi = 2
-    kk = max(args.steps, 20)
-    gms, _ = B.time_steps(lambda: launches[gi](), kk, 3)
-    gflop = 2 * M * gemms[gi][1] * gemms[gi][2]
-    g_tflops = gflop / (gms * 1e-3) / 1e12
     if graph is not None:
         graph.destroy()
+    # per shape: one graph of that GEMM over the 16 layers' weights, each
+    # call with its binary16 pre-pass (and reduce launch, if split)
+    names = ["q|k|v", "o", "gate|up", "down"]
+    per_shape = {}
+    for j, name in enumerate(names):
+        sub = launches[j::4]
+        g = B.capture(sub)
+        run = B.run_graph_or_eager(g, sub)
+        sms, _ = B.time_steps(run, max(args.steps // 2, 5), 2)
+        if g is not None:
+            g.destroy()
+        per = sms / len(sub)
+        fl = 2 * M * gemms[j][1] * gemms[j][2]
+        per_shape[name] = {"shape": f"{M}x{gemms[j][1]}x{gemms[j][2]}",
+                           "us_per_call": round(per * 1e3, 2),
+                           "tflops": round(fl / (per * 1e-3) / 1e12, 1),
+                           "frac_mfma": round(fl / (per * 1e-3) / 1e12 / BF16_PEAK_TFLOPS, 4)}
+    gi = 2
+    gflop = 2 * M * gemms[gi][1] * gemms[gi][2]
+    gms = per_shape["gate|up"]["us_per_call"] * 1e-3
+    g_tflops = gflop / (gms * 1e-3) / 1e12
     w.free()
     return {
         "metric": "Q8 prefill GEMM TFLOP/s (% of dense bf16 MFMA peak), Llama-3.2-1B M=512",
@@ -600,43 +721,166 @@ def run_prefill(B: Bench, cfg=LLAMA_1B, M=512):
                                "(q|k|v and gate|up stacked)",
                    "layout": f"G={G} {scale} scales", "flops_per_step": flops,
                    "pct_mfma_peak": round(100 * tflops / BF16_PEAK_TFLOPS, 2),
+                   "per_shape": per_shape,
                    "graph": graph is not None, "wall_s": round(wall, 3)},
         "roofline": {"bound": "mfma", "achieved": round(g_tflops, 2), "peak": BF16_PEAK_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(g_tflops / BF16_PEAK_TFLOPS, 4),
                      "traffic": None,
                      "kernel": f"GEMM {M}x{gemms[gi][1]}x{gemms[gi][2]} (+ binary16 pre-pass): "
-                               f"{gflop} flop/launch, {gms * 1e3:.2f} us avg"},
+                               f"{gflop} flop/launch, {gms * 1e3:.2f} us avg over the 16 "
+                               "layers' calls (graph replays)"},
         "cpu_baseline": None,
     }
 
 
 def cpu_baseline(packs, G, scale, budget_s, label):
-    """The oracle's group-major fp32 restatement of k_mm_q8 over host copies
-    of the packed weights, on the host cores (OpenMP)."""
-    from oracle.q8_oracle import c_oracle
+    """Q8 linears over host copies of the packed weights on the host cores,
+    three legs of about budget_s seconds each:
+      port, all cores  the oracle's group-major fp32 restatement of k_mm_q8
+                       (oracle/q8_oracle.c, OpenMP over output rows);
+      port, one core   the same with one thread;
+      numpy BLAS       x @ W.T in fp32 over the dequantized weights (the form
+                       of scripts/gen_oracle.py:74-93; the dequantization runs
+                       once, before the timed loop).
+    Rates count the Q8 algorithmic bytes of each linear, so the legs compare
+    as time per linear.  The first leg is the reported baseline."""
+    # pin the OpenMP threads next to each other before the oracle's runtime
+    # starts (it reads the variable once, when it is loaded)
+    os.environ.setdefault("OMP_PROC_BIND", "close")
+    from oracle.q8_oracle import c_oracle, unpack_q8_np
     cor = c_oracle()
-    threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+    sb = 2 if scale == "f16" else 4
     rng = np.random.default_rng(5)
     xs = {}
+    for pk, s, m in packs:
+        if (s, m) not in xs:
+            xs[(s, m)] = rng.standard_normal((s, m), dtype=np.float32)
+
+    def timed(run_one):
+        t0 = time.perf_counter()
+        done, reps = 0, 0
+        while True:
+            for pk, s, m in packs:
+                run_one(pk, s, m)
+                done += linear_bytes(s, m, pk.shape[0], G, sb)
+            reps += 1
+            el = time.perf_counter() - t0
+            if el >= budget_s:
+                return done / el / 1e9, reps, el
+
+    all_threads = cor.threads()
+    legs = []
+    for threads in (all_threads, 1):
+        cor.set_threads(threads)
+        gbs, reps, el = timed(lambda pk, s, m: cor.linear_f32(pk, xs[(s, m)], G, scale))
+        legs.append({"leg": f"port, {threads} thread{'s' if threads > 1 else ''}",
+                     "value": round(gbs, 2), "unit": "GB/s", "cores": threads,
+                     "sample": f"{reps} x {label} in {el:.1f} s"})
+    cor.set_threads(all_threads)
+    blas = "numpy BLAS"
+    try:
+        from threadpoolctl import threadpool_info
+        info = [d for d in threadpool_info() if d.get("user_api") == "blas"]
+        if info:
+            blas = f"{info[0].get('internal_api')} {info[0].get('version')}"
+            blas_threads = int(info[0].get("num_threads"))
+        else:
+            blas_threads = all_threads
+    except Exception:
+        blas_threads = all_threads
+    deq = {}
+    for i, (pk, s, m) in enumerate(packs):
+        codes, sc = unpack_q8_np(pk, m, G, scale)
+        deq[i] = (codes.astype(np.float32).reshape(pk.shape[0], m // G, G)
+                  * sc.astype(np.float32)[:, :, None]).reshape(pk.shape[0], m)
+        del codes, sc
+    ids = {id(pk): i for i, (pk, _, _) in enumerate(packs)}
+    gbs, reps, el = timed(lambda pk, s, m: xs[(s, m)] @ deq[ids[id(pk)]].T)
+    legs.append({"leg": f"numpy {blas}, {blas_threads} threads", "value": round(gbs, 2),
+                 "unit": "GB/s", "cores": blas_threads,
+                 "sample": f"{reps} x {label} as x @ dequant(W).T in {el:.1f} s"})
+    del deq
+    try:
+        affinity = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        affinity = None
+    first = legs[0]
+    return {"value": first["value"], "unit": "GB/s", "cores": first["cores"], "kind": "port",
+            "sample": f"{first['sample']}; oracle/q8_oracle.c q8o_linear_f32 (group-major fp32 "
+                      f"restatement of k_mm_q8), {cpu_model()}",
+            "legs": legs,
+            "host": {"cpu": cpu_model(), "nproc": os.cpu_count(), "affinity_cpus": affinity,
+                     "OMP_NUM_THREADS": os.environ.get("OMP_NUM_THREADS"),
+                     "OMP_PROC_BIND": os.environ.get("OMP_PROC_BIND"),
+                     "blas": blas, "blas_threads": blas_threads}}
+
+
+def run_all(B: Bench):
+    """The headline decode step plus every other configuration's record."""
+    from lama32_mojo_amd import model as gm
+
+    torch = B.torch
     t0 = time.perf_counter()
-    done_bytes = 0
-    reps = 0
-    sb = 2 if scale == "f16" else 4
-    while True:
-        for pk, s, m in packs:
-            if (s, m) not in xs:
-                xs[(s, m)] = rng.standard_normal((s, m), dtype=np.float32)
-            cor.linear_f32(pk, xs[(s, m)], G, scale)
-            done_bytes += linear_bytes(s, m, pk.shape[0], G, sb)
-        reps += 1
-        el = time.perf_counter() - t0
-        if el >= budget_s:
-            break
-    return {"value": round(done_bytes / el / 1e9, 2), "unit": "GB/s", "cores": threads,
-            "kind": "port",
-            "sample": f"{reps} x {label} on {threads} threads in {el:.1f} s; "
-                      f"oracle/q8_oracle.c q8o_linear_f32 (group-major fp32 restatement "
-                      f"of k_mm_q8), {cpu_model()}"}
+    B.set_layout("g64f16")
+    res = run_decode_model(B)
+    configs = {}
+
+    def note(name, rec, t):
+        rec["bench_s"] = round(time.perf_counter() - t, 1)
+        configs[name] = rec
+        torch.cuda.empty_cache()
+        print(f"[bench] {name} done in {rec['bench_s']} s", file=sys.stderr, flush=True)
+
+    t = time.perf_counter()
+    lin = {}
+    for lay in ("g32f32", "g64f16"):
+        B.set_layout(lay)
+        r = run_linear(B, cpu=False)
+        lin[lay] = {"gbs": r["value"], "us_per_launch": round(r["ms_per_step"] * 1e3, 3),
+                    "frac_hbm": r["roofline"]["frac"],
+                    "bytes_per_launch": r["config"]["bytes_per_launch"]}
+    note("linear_8192x2048", {"workload": "single Q8 linear 8192x2048, x f32 [1, 2048], 64 "
+                                          "rotated weight copies, one graph", **lin}, t)
+
+    t = time.perf_counter()
+    B.set_layout("g32f32")
+    r = run_prefill(B)
+    note("prefill_1b_m512", {"workload": r["config"]["workload"], "layout": r["config"]["layout"],
+                             "tflops": r["value"], "ms_per_step": r["ms_per_step"],
+                             "frac_mfma": round(r["value"] / BF16_PEAK_TFLOPS, 4),
+                             "per_shape": r["config"]["per_shape"]}, t)
+
+    t = time.perf_counter()
+    recs, (w, _, shapes) = decode_linears(B, QWEN3_8B, [1, 4, 16])
+    w.free()
+    B.keep = None
+    note("qwen3_8b_decode", {"workload": f"Qwen3-8B decode linears: 36 layers x (fused q|k|v "
+                                         "4096->6144, o 4096->4096, fused gate|up 4096->24576, "
+                                         "down 12288->4096) + lm_head 4096->151936, one graph",
+                             "layout": "G=32 f32 scales",
+                             "batches": {str(k): v for k, v in recs.items()}}, t)
+
+    t = time.perf_counter()
+    B.set_layout("g64f16")
+    r = run_e2e_8b(B, rooflines=False)
+    c = r["config"]
+    note("llama31_8b_e2e", {"workload": c["workload"], "layout": c["layout"],
+                            "prefill_ms": c["prefill_ms"],
+                            "prefill_linear_tflops": c["prefill_linear_tflops"],
+                            "decode_tok_s": r["value"],
+                            "decode_ms_per_token": c["decode_ms_per_token"],
+                            "decode_weight_gbs": c["decode_weight_gbs"], "e2e_ms": c["e2e_ms"]},
+         t)
+
+    t = time.perf_counter()
+    r = run_decode_model(B, ctxlen=128, cfg=gm.QWEN3_06B, tok_metric=True, rooflines=False,
+                         cpu=False)
+    note("qwen3_06b_decode", {"workload": r["config"]["workload"], "tok_s": r["value"],
+                              "ms_per_token": r["ms_per_step"],
+                              "vs_reference_m4_29_tok_s": r["vs_baseline"]}, t)
+    res["configs"] = configs
+    res["config"]["bench_total_s"] = round(time.perf_counter() - t0, 1)
+    return res
 
 
 def main():
@@ -648,15 +892,20 @@ def main():
     if args.layout is None:
         # the reference layout for the Llama-3.2-1B decode step; group 32
         # with f32 scales where the workload is defined with it
-        args.layout = ("g64f16" if args.workload in ("decode", "decode-linears", "e2e-8b",
-                                                     "lmhead-pmc", "qwen3-06b")
+        args.layout = ("g64f16" if args.workload in ("all", "decode", "decode-linears",
+                                                     "e2e-8b", "lmhead-pmc", "gateup-pmc",
+                                                     "qwen3-06b")
                        else "g32f32")
     import torch
     from lama32_mojo_amd import q8hip
     ctx = q8hip.Context(0)
     B = Bench(args, ctx, torch)
-    if args.workload == "decode":
+    if args.workload == "all":
+        res = run_all(B)
+    elif args.workload == "decode":
         res = run_decode_model(B)
+    elif args.workload == "gateup-pmc":
+        res = run_gateup_pmc(B)
     elif args.workload == "decode-linears":
         res = run_decode(B, LLAMA_1B)
     elif args.workload == "qwen3-06b":
@@ -679,7 +928,7 @@ def main():
     out.setdefault("vs_baseline", None)
     order = ["metric", "value", "unit", "n_gpus", "steps", "warmup", "ms_per_step",
              "higher_is_better", "scaling", "vs_baseline", "dtype", "data", "config",
-             "roofline", "cpu_baseline"]
+             "roofline", "roofline_lm_head", "cpu_baseline", "configs"]
     print(json.dumps({k: out[k] for k in order if k in out}), flush=True)
     ctx.close()
 

@@ -300,6 +300,17 @@ void q8o_linear_f32(const uint16_t *wpk, const float *x, int64_t s, int64_t m,
     }
 }
 
+/* OpenMP threads for the parallel loops above (the CPU baseline runs the
+ * fp32 restatement on all host cores and on one). */
+#ifdef _OPENMP
+#include <omp.h>
+void q8o_set_threads(int n) { omp_set_num_threads(n > 0 ? n : 1); }
+int q8o_get_threads(void) { return omp_get_max_threads(); }
+#else
+void q8o_set_threads(int n) { (void)n; }
+int q8o_get_threads(void) { return 1; }
+#endif
+
 /* ----------------------------------------------------------------------- */
 /* Embedding gather (src/llama_q8.mojo:96-109)                              */
 /* ----------------------------------------------------------------------- */

@@ -176,7 +176,18 @@ class COracle:
         lib.q8o_f32_to_f16_array.restype = None
         lib.q8o_f16_to_f32_array.argtypes = [P, I64, P]
         lib.q8o_f16_to_f32_array.restype = None
+        lib.q8o_set_threads.argtypes = [I]
+        lib.q8o_set_threads.restype = None
+        lib.q8o_get_threads.argtypes = []
+        lib.q8o_get_threads.restype = I
         self.lib = lib
+
+    def set_threads(self, n: int) -> None:
+        """OpenMP threads of the parallel loops (linear_f32, linear_f64)."""
+        self.lib.q8o_set_threads(int(n))
+
+    def threads(self) -> int:
+        return int(self.lib.q8o_get_threads())
 
     @staticmethod
     def _p(a: np.ndarray):
