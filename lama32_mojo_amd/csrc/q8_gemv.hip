@@ -79,29 +79,86 @@ __global__ __launch_bounds__(256) void gemv_kernel(
   };
 
   // A wave loads up to NPF steps (1 KiB per row each) of its R rows at once,
-  // then computes: a tile with m / SPLITK <= 4096 waits on memory once.  The
-  // first tile's first loads do not depend on x and are issued before x is
-  // staged.
+  // then computes; NPF covers the wave's whole K range up to 4 steps, so a
+  // tile with m / SPLITK <= 4096 waits on memory once.  Steps past the range
+  // reload the current step instead of sitting in a branch, so the loads
+  // are unconditional and the compiler can wait on each group alone.
   u32x4 q[NPF][R];
   float sc[NPF][R];
   auto load_chunk = [&](const uint8_t *const *rowp, int64_t kc) {
 #pragma unroll
     for (int p = 0; p < NPF; ++p) {
-      const int64_t k = kc + 1024 * p;
-      if (k < k_hi) {
+      const int64_t k = kc + 1024 * p < k_hi ? kc + 1024 * p : kc;
 #pragma unroll
-        for (int r = 0; r < R; ++r)
-          q[p][r] = __builtin_nontemporal_load(
-              reinterpret_cast<const u32x4 *>(rowp[r] + scale_bytes + k));
+      for (int r = 0; r < R; ++r)
+        q[p][r] = __builtin_nontemporal_load(
+            reinterpret_cast<const u32x4 *>(rowp[r] + scale_bytes + k));
 #pragma unroll
-        for (int r = 0; r < R; ++r) sc[p][r] = load_scale<KIND>(rowp[r], k / G);
-      }
+      for (int r = 0; r < R; ++r) sc[p][r] = load_scale<KIND>(rowp[r], k / G);
     }
   };
   const uint8_t *rowp[R];
 #pragma unroll
   for (int r = 0; r < R; ++r) rowp[r] = w + row_of(r0, r) * row_bytes;
-  if (r0 < nout) load_chunk(rowp, k_first);
+
+  // Load order at the start: loads return in issue order, so x goes first
+  // (its first staging batch, or with x read from L2 and one activation row
+  // this lane's x slices of the first NPF <= 2 steps, held in registers),
+  // then every weight step of the first tile.  Staging x then waits for x
+  // alone while the weights are still arriving.
+  constexpr int XB = 4;                          // staging batch: 16-byte loads per thread
+  constexpr bool XREG = !XLDS && S == 1 && NPF <= 2;
+  f32x4 xv[XB], uv[XB];
+  uint2 wb[XB];
+  f32x4 xr[XREG ? NPF : 1][4];
+  const int64_t tot = S * m;                     // multiple of 4 (m % 32 == 0)
+  auto load_x = [&](int64_t i0) {
+#pragma unroll
+    for (int u = 0; u < XB; ++u) {
+      const int64_t i = i0 + 4 * 256 * u;
+      if (i < tot) {
+        xv[u] = *reinterpret_cast<const f32x4 *>(x + i);
+        if constexpr (PRE == PRE_SWIGLU) uv[u] = *reinterpret_cast<const f32x4 *>(x + m + i);
+        if constexpr (PRE == PRE_RMSNORM) wb[u] = *reinterpret_cast<const uint2 *>(wn + i);
+      }
+    }
+  };
+  if constexpr (XLDS) load_x(4 * threadIdx.x);
+  if constexpr (XREG) {
+#pragma unroll
+    for (int p = 0; p < NPF; ++p) {
+      const int64_t k = k_first + 1024 * p < k_hi ? k_first + 1024 * p : k_first;
+      const f32x4 *xv4 = reinterpret_cast<const f32x4 *>(x + k);
+#pragma unroll
+      for (int c = 0; c < 4; ++c) xr[p][c] = xv4[c];
+    }
+  }
+  load_chunk(rowp, k_first);
+  // POST_RESIDUAL: the first tile's residual values, loaded after the
+  // weights (the store at the end would otherwise wait on one more round
+  // trip).  Without a K split lane 0 stores the wave's outputs, so every
+  // lane holds them all; with one, thread t < R S stores output (t / S,
+  // t % S).  Indices past the outputs are clamped (their stores are
+  // skipped).  A residual that is y itself is read before this kernel
+  // writes any of it.
+  constexpr int RR = POST == POST_RESIDUAL ? (SPLITK > 1 ? 1 : RO * S) : 1;
+  float resv[RR] = {};
+  const int64_t r0_first = r0;
+  if constexpr (POST == POST_RESIDUAL) {
+    if constexpr (SPLITK > 1) {
+      const int t = threadIdx.x < R * S ? threadIdx.x : 0;
+      const int64_t o = r0 + t / S < nout ? r0 + t / S : nout - 1;
+      resv[0] = res[(t % S) * n + o];
+    } else {
+#pragma unroll
+      for (int r = 0; r < RO; ++r)
+#pragma unroll
+        for (int b = 0; b < S; ++b) {
+          const int64_t o = r0 + r < nout ? r0 + r : nout - 1;
+          resv[r * S + b] = res[b * n + o];
+        }
+    }
+  }
 
   // PRE_RMSNORM: x is staged as bf16(wn) * x and every output is scaled by
   // 1 / sqrt(mean(x^2) + eps) at the end (W (wn x inv) = inv W (wn x)); the
@@ -109,23 +166,11 @@ __global__ __launch_bounds__(256) void gemv_kernel(
   float inv = 1.0f;
   const float *xp = x;
   if constexpr (XLDS) {
-    const int64_t tot = S * m;   // multiple of 4 (m % 32 == 0)
     float ss = 0.0f;
     // batches of XB independent 16-byte loads per thread, then the LDS
     // stores (a load-store-load chain would wait on L2 once per step)
-    constexpr int XB = 4;
     for (int64_t i0 = 4 * threadIdx.x; i0 < tot; i0 += 4 * 256 * XB) {
-      f32x4 xv[XB], uv[XB];
-      uint2 wb[XB];
-#pragma unroll
-      for (int u = 0; u < XB; ++u) {
-        const int64_t i = i0 + 4 * 256 * u;
-        if (i < tot) {
-          xv[u] = *reinterpret_cast<const f32x4 *>(x + i);
-          if constexpr (PRE == PRE_SWIGLU) uv[u] = *reinterpret_cast<const f32x4 *>(x + m + i);
-          if constexpr (PRE == PRE_RMSNORM) wb[u] = *reinterpret_cast<const uint2 *>(wn + i);
-        }
-      }
+      if (i0 != 4 * threadIdx.x) load_x(i0);     // the first batch is in flight already
 #pragma unroll
       for (int u = 0; u < XB; ++u) {
         const int64_t i = i0 + 4 * 256 * u;
@@ -163,7 +208,8 @@ __global__ __launch_bounds__(256) void gemv_kernel(
   }
 
   // one finished output (value v of tile slot r) -> memory
-  auto store = [&](int64_t t0, int r, int b, float v, float v_up) {
+  // (rv: the prefetched residual when t0 is the first tile)
+  auto store = [&](int64_t t0, int r, int b, float v, float v_up, float rv) {
     const int64_t o = t0 + r;
     if (o >= nout) return;
     if constexpr (POST == POST_SWIGLU) {
@@ -171,7 +217,7 @@ __global__ __launch_bounds__(256) void gemv_kernel(
       y[o] = (g / (1.0f + expf(-g))) * u;
     } else {
       v = inv * v;
-      if constexpr (POST == POST_RESIDUAL) v = res[b * n + o] + v;
+      if constexpr (POST == POST_RESIDUAL) v = (t0 == r0_first ? rv : res[b * n + o]) + v;
       y[b * n + o] = v;
     }
   };
@@ -201,8 +247,19 @@ __global__ __launch_bounds__(256) void gemv_kernel(
         if (k < k_hi) {
 #pragma unroll
           for (int b = 0; b < S; ++b) {
-            const f32x4 *xv4 = reinterpret_cast<const f32x4 *>(xp + b * m + k);
-            f32x4 xa = xv4[0], xb = xv4[1], xc = xv4[2], xd = xv4[3];
+            f32x4 xa, xb, xc, xd;
+            if (XREG && kc == k_first) {
+              xa = xr[XREG ? p : 0][0];
+              xb = xr[XREG ? p : 0][1];
+              xc = xr[XREG ? p : 0][2];
+              xd = xr[XREG ? p : 0][3];
+            } else {
+              const f32x4 *xv4 = reinterpret_cast<const f32x4 *>(xp + b * m + k);
+              xa = xv4[0];
+              xb = xv4[1];
+              xc = xv4[2];
+              xd = xv4[3];
+            }
 #pragma unroll
             for (int r = 0; r < R; ++r)
               acc[r][b] =
@@ -223,7 +280,8 @@ __global__ __launch_bounds__(256) void gemv_kernel(
         for (int r = 0; r < RO; ++r)
 #pragma unroll
           for (int b = 0; b < S; ++b)
-            store(r0, r, b, v[r][b], POST == POST_SWIGLU ? v[(r + RO) % R][b] : 0.0f);
+            store(r0, r, b, v[r][b], POST == POST_SWIGLU ? v[(r + RO) % R][b] : 0.0f,
+                  resv[POST == POST_RESIDUAL ? r * S + b : 0]);
         if constexpr (POST == POST_ARGMAX) {
           // rows in increasing order, strict >: the lowest row among equal
           // values; NaN never wins
@@ -251,7 +309,7 @@ __global__ __launch_bounds__(256) void gemv_kernel(
         float v = part[0][r][b];
 #pragma unroll
         for (int u = 1; u < SPLITK; ++u) v += part[u][r][b];
-        store(r0, r, b, v, 0.0f);
+        store(r0, r, b, v, 0.0f, resv[0]);
       }
       __syncthreads();
     }
@@ -316,14 +374,20 @@ int grid_for(int64_t tiles, int64_t cap) {
   return (int)(tiles < cap ? (tiles > 0 ? tiles : 1) : cap);
 }
 
-// NPF: K steps in flight per wave (registers against occupancy: one step
-// for waves of 2 or more rows -- measured no slower than two on the decode
-// shapes, with more waves per SIMD -- and four for 1-row waves)
+// NPF: K steps in flight per wave.  Batches of 2-4 rows (the unaligned
+// fallback) keep one step for waves of 2+ rows (registers against
+// occupancy).  One activation row puts the wave's whole K range in flight,
+// up to 4 steps (2 or 4, by the range): every wave waits on memory once, so
+// the weights stream at full rate from the start instead of in two waves of
+// requests (gate|up 2048 -> 16384: first step's data in 3.4 us per wave,
+// then the second step's round trip).
 template <int R, int S> constexpr int npf_for() { return R * S >= 4 ? 1 : 4; }
 
-template <int G, int KIND, int S, int R, int SPLITK, int NPF = npf_for<R, S>()>
-hipError_t launch_fast(const LinearArgs &a, const float *x, float *y, int64_t cap,
-                       hipStream_t st) {
+inline bool two_steps(int64_t m, int splitk) { return m / splitk <= 2048; }
+
+template <int G, int KIND, int S, int R, int SPLITK, int NPF>
+hipError_t launch_fast_t(const LinearArgs &a, const float *x, float *y, int64_t cap,
+                         hipStream_t st) {
   const int64_t rows_per_group = SPLITK > 1 ? R : kWaves * R;
   const int64_t tiles = (a.n + rows_per_group - 1) / rows_per_group;
   dim3 grid(grid_for(tiles, cap)), block(256);
@@ -340,6 +404,17 @@ hipError_t launch_fast(const LinearArgs &a, const float *x, float *y, int64_t ca
   return hipGetLastError();
 }
 
+template <int G, int KIND, int S, int R, int SPLITK>
+hipError_t launch_fast(const LinearArgs &a, const float *x, float *y, int64_t cap,
+                       hipStream_t st) {
+  if constexpr (S == 1) {
+    if (two_steps(a.m, SPLITK)) return launch_fast_t<G, KIND, S, R, SPLITK, 2>(a, x, y, cap, st);
+    return launch_fast_t<G, KIND, S, R, SPLITK, 4>(a, x, y, cap, st);
+  } else {
+    return launch_fast_t<G, KIND, S, R, SPLITK, npf_for<R, S>()>(a, x, y, cap, st);
+  }
+}
+
 // Shape classes (tuned on MI355X, decode shapes of Llama-3.2-1B / Qwen3-8B):
 //   long rows (m > 4096):         K split over the 4 waves, 4 rows per workgroup
 //   vocabulary heads (n >= 64K):  2 rows per wave, up to 8192 workgroups
@@ -348,7 +423,7 @@ hipError_t launch_fast(const LinearArgs &a, const float *x, float *y, int64_t ca
 template <int G, int KIND, int S>
 hipError_t launch_rows(const LinearArgs &a, const float *x, float *y, hipStream_t st) {
   if (a.m > 4096 && a.m % 64 == 0) return launch_fast<G, KIND, S, 4, 4>(a, x, y, 1024, st);
-  if (a.n >= 65536) return launch_fast<G, KIND, S, 2, 1, 1>(a, x, y, 8192, st);
+  if (a.n >= 65536) return launch_fast<G, KIND, S, 2, 1>(a, x, y, 8192, st);
   if (a.n >= 8192) return launch_fast<G, KIND, S, 4, 1>(a, x, y, 1024, st);
   // one row, 4096 .. 8191 outputs: 2 rows per wave (Qwen3-8B o and q|k|v)
   if (S == 1 && a.n >= 4096) return launch_fast<G, KIND, S, 2, 1>(a, x, y, 2048, st);
@@ -390,8 +465,8 @@ hipError_t launch_g(const LinearArgs &a, hipStream_t st) {
   return hipSuccess;
 }
 
-template <int G, int KIND, int R, int SPLITK, int PRE, int POST, int NPF = npf_for<R, 1>()>
-hipError_t launch_fused_t(const FusedLinearArgs &f, int64_t cap, hipStream_t st) {
+template <int G, int KIND, int R, int SPLITK, int PRE, int POST, int NPF>
+hipError_t launch_fused_npf(const FusedLinearArgs &f, int64_t cap, hipStream_t st) {
   const LinearArgs &a = f.lin;
   constexpr int RO = POST == POST_SWIGLU ? R / 2 : R;
   const int64_t nout = POST == POST_SWIGLU ? a.n / 2 : a.n;
@@ -416,6 +491,12 @@ hipError_t launch_fused_t(const FusedLinearArgs &f, int64_t cap, hipStream_t st)
   return hipGetLastError();
 }
 
+template <int G, int KIND, int R, int SPLITK, int PRE, int POST>
+hipError_t launch_fused_t(const FusedLinearArgs &f, int64_t cap, hipStream_t st) {
+  if (two_steps(f.lin.m, SPLITK)) return launch_fused_npf<G, KIND, R, SPLITK, PRE, POST, 2>(f, cap, st);
+  return launch_fused_npf<G, KIND, R, SPLITK, PRE, POST, 4>(f, cap, st);
+}
+
 // Shape classes as launch_rows; the swiglu epilogue keeps whole rows per
 // wave (gate and up rows of one output in the same wave).
 template <int G, int KIND, int PRE, int POST>
@@ -426,11 +507,11 @@ hipError_t launch_fused_rows(const FusedLinearArgs &f, hipStream_t st) {
     return launch_fused_t<G, KIND, 2, 1, PRE, POST>(f, 4096, st);
   } else if constexpr (POST == POST_ARGMAX) {
     // whole rows per wave; the grid stays within kArgmaxMaxBlocks partials
-    if (a.n >= 65536) return launch_fused_t<G, KIND, 2, 1, PRE, POST, 1>(f, 8192, st);
+    if (a.n >= 65536) return launch_fused_t<G, KIND, 2, 1, PRE, POST>(f, 8192, st);
     return launch_fused_t<G, KIND, 1, 1, PRE, POST>(f, 4096, st);
   } else {
     if (a.m > 4096 && a.m % 64 == 0) return launch_fused_t<G, KIND, 4, 4, PRE, POST>(f, 1024, st);
-    if (a.n >= 65536) return launch_fused_t<G, KIND, 2, 1, PRE, POST, 1>(f, 8192, st);
+    if (a.n >= 65536) return launch_fused_t<G, KIND, 2, 1, PRE, POST>(f, 8192, st);
     if (a.n >= 8192) return launch_fused_t<G, KIND, 4, 1, PRE, POST>(f, 1024, st);
     // 2 rows per wave from 4096 rows (Llama-3.1-8B q|k|v and o: step
     // 2.308 -> 2.238 ms)
