@@ -85,10 +85,14 @@ __global__ __launch_bounds__(256) void gemv_kernel(
   // are unconditional and the compiler can wait on each group alone.
   u32x4 q[NPF][R];
   float sc[NPF][R];
+  // (kc itself lies past the range only for lanes beyond a row shorter than
+  // 1024 codes: those reload the range's first slice, k_lo, which every row
+  // has)
   auto load_chunk = [&](const uint8_t *const *rowp, int64_t kc) {
+    const int64_t base = kc < k_hi ? kc : k_lo;
 #pragma unroll
     for (int p = 0; p < NPF; ++p) {
-      const int64_t k = kc + 1024 * p < k_hi ? kc + 1024 * p : kc;
+      const int64_t k = kc + 1024 * p < k_hi ? kc + 1024 * p : base;
 #pragma unroll
       for (int r = 0; r < R; ++r)
         q[p][r] = __builtin_nontemporal_load(
@@ -125,9 +129,10 @@ __global__ __launch_bounds__(256) void gemv_kernel(
   };
   if constexpr (XLDS) load_x(4 * threadIdx.x);
   if constexpr (XREG) {
+    const int64_t base = k_first < k_hi ? k_first : k_lo;
 #pragma unroll
     for (int p = 0; p < NPF; ++p) {
-      const int64_t k = k_first + 1024 * p < k_hi ? k_first + 1024 * p : k_first;
+      const int64_t k = k_first + 1024 * p < k_hi ? k_first + 1024 * p : base;
       const f32x4 *xv4 = reinterpret_cast<const f32x4 *>(x + k);
 #pragma unroll
       for (int c = 0; c < 4; ++c) xr[p][c] = xv4[c];
@@ -391,7 +396,11 @@ hipError_t launch_fast_t(const LinearArgs &a, const float *x, float *y, int64_t 
   const int64_t rows_per_group = SPLITK > 1 ? R : kWaves * R;
   const int64_t tiles = (a.n + rows_per_group - 1) / rows_per_group;
   dim3 grid(grid_for(tiles, cap)), block(256);
-  if (S * a.m <= kLdsStageFloats) {
+  // x staged in LDS for rows up to the stage limit, except when each lane's
+  // x slices fit in registers (one activation row, a wave K range of at
+  // most 2 steps): those are loaded before the weights and need no stage or
+  // barrier (the 8192 x 2048 linear: 6.40 -> 5.82 us)
+  if (S * a.m <= kLdsStageFloats && !(S == 1 && NPF <= 2)) {
     size_t lds = (size_t)S * a.m * sizeof(float);
     hipLaunchKernelGGL((gemv_kernel<G, KIND, S, R, SPLITK, true, PRE_NONE, POST_STORE, NPF>), grid,
                        block, lds, st, a.w, a.row_bytes, a.n, x, a.m, y, nullptr, 0.0f, nullptr,
@@ -474,17 +483,21 @@ hipError_t launch_fused_npf(const FusedLinearArgs &f, int64_t cap, hipStream_t s
   const int64_t tiles = (nout + rows_per_group - 1) / rows_per_group;
   dim3 grid(grid_for(tiles, cap)), block(256);
   const float *x = reinterpret_cast<const float *>(a.x);
-  // x read from L2 by every wave past the stage limit, and for short rows
-  // (m <= 2048), where the stage and its barrier cost more than they save
-  // (Qwen3-0.6B o projection: step 0.741 -> 0.737 ms)
+  // x read from L2 by every wave past the stage limit, and held in
+  // registers (loaded before the weights) when a wave's K range is at most
+  // 2 steps: the stage and its barrier cost more than they save (Qwen3-0.6B
+  // o projection: step 0.741 -> 0.737 ms).  The fused prologues keep the
+  // LDS stage: whole rows in every wave's registers (m <= 2048) made the
+  // 1B gate|up 8.57 -> 11.0 us (registers past one round of workgroups,
+  // and x and the norm weights fetched per wave instead of per workgroup).
+  if (f.grid_out) *f.grid_out = (int)grid.x;
   if constexpr (PRE == PRE_NONE) {
-    if (a.m > kLdsStageFloats || a.m <= 2048) {
+    if (a.m > kLdsStageFloats || NPF <= 2) {
       hipLaunchKernelGGL((gemv_kernel<G, KIND, 1, R, SPLITK, false, PRE, POST, NPF>), grid, block,
                          0, st, a.w, a.row_bytes, a.n, x, a.m, a.y, f.wn, f.eps, f.res, f.part);
       return hipGetLastError();
     }
   }
-  if (f.grid_out) *f.grid_out = (int)grid.x;
   hipLaunchKernelGGL((gemv_kernel<G, KIND, 1, R, SPLITK, true, PRE, POST, NPF>), grid, block,
                      (size_t)a.m * sizeof(float), st, a.w, a.row_bytes, a.n, x, a.m, a.y, f.wn,
                      f.eps, f.res, f.part);
