@@ -392,6 +392,10 @@ void gemm_kernel(const uint8_t *__restrict__ w, int64_t row_bytes,
           s2[t][g] = k0 + g * G < m ? f16x2{hs, hs} : zero2;
         }
       }
+      // The slot's MFMA work runs at raised wave priority: of the SIMD's two
+      // waves the one in its MFMA phase issues first, the other stages and
+      // dequantizes meanwhile.
+      __builtin_amdgcn_s_setprio(1);
       // A fragments of k-step ks + 1 are read while k-step ks runs
       f16x8 af[2][TM];
 #pragma unroll
@@ -418,6 +422,7 @@ void gemm_kernel(const uint8_t *__restrict__ w, int64_t row_bytes,
           for (int t = 0; t < TN; ++t)
             acc[ii][t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[ks & 1][ii], bq[t], acc[ii][t], 0, 0, 0);
       }
+      __builtin_amdgcn_s_setprio(0);
     }
     // stage the tiles of iteration it + 1, then load those of it + 2
     store_scales(rs, (it + 1) & 1);
