@@ -400,7 +400,8 @@ hipError_t launch_fast_t(const LinearArgs &a, const float *x, float *y, int64_t 
   // x slices fit in registers (one activation row, a wave K range of at
   // most 2 steps): those are loaded before the weights and need no stage or
   // barrier (the 8192 x 2048 linear: 6.40 -> 5.82 us)
-  if (S * a.m <= kLdsStageFloats && !(S == 1 && NPF <= 2)) {
+  const bool xreg = S == 1 && NPF <= 2 && a.m / SPLITK <= 1024 * NPF;
+  if (S * a.m <= kLdsStageFloats && !xreg) {
     size_t lds = (size_t)S * a.m * sizeof(float);
     hipLaunchKernelGGL((gemv_kernel<G, KIND, S, R, SPLITK, true, PRE_NONE, POST_STORE, NPF>), grid,
                        block, lds, st, a.w, a.row_bytes, a.n, x, a.m, y, nullptr, 0.0f, nullptr,
@@ -432,7 +433,11 @@ hipError_t launch_fast(const LinearArgs &a, const float *x, float *y, int64_t ca
 template <int G, int KIND, int S>
 hipError_t launch_rows(const LinearArgs &a, const float *x, float *y, hipStream_t st) {
   if (a.m > 4096 && a.m % 64 == 0) return launch_fast<G, KIND, S, 4, 4>(a, x, y, 1024, st);
-  if (a.n >= 65536) return launch_fast<G, KIND, S, 2, 1>(a, x, y, 8192, st);
+  // vocabulary heads: one K step in flight per wave (more waves per CU; the
+  // 8192 workgroups walk about two row tiles each, so occupancy, not one
+  // round of loads, covers the latency: 2 steps made the 1B lm_head 42 ->
+  // 47 us)
+  if (a.n >= 65536) return launch_fast_t<G, KIND, S, 2, 1, 1>(a, x, y, 8192, st);
   if (a.n >= 8192) return launch_fast<G, KIND, S, 4, 1>(a, x, y, 1024, st);
   // one row, 4096 .. 8191 outputs: 2 rows per wave (Qwen3-8B o and q|k|v)
   if (S == 1 && a.n >= 4096) return launch_fast<G, KIND, S, 2, 1>(a, x, y, 2048, st);
@@ -492,7 +497,7 @@ hipError_t launch_fused_npf(const FusedLinearArgs &f, int64_t cap, hipStream_t s
   // and x and the norm weights fetched per wave instead of per workgroup).
   if (f.grid_out) *f.grid_out = (int)grid.x;
   if constexpr (PRE == PRE_NONE) {
-    if (a.m > kLdsStageFloats || NPF <= 2) {
+    if (a.m > kLdsStageFloats || (NPF <= 2 && a.m / SPLITK <= 1024 * NPF)) {
       hipLaunchKernelGGL((gemv_kernel<G, KIND, 1, R, SPLITK, false, PRE, POST, NPF>), grid, block,
                          0, st, a.w, a.row_bytes, a.n, x, a.m, a.y, f.wn, f.eps, f.res, f.part);
       return hipGetLastError();
@@ -516,15 +521,17 @@ template <int G, int KIND, int PRE, int POST>
 hipError_t launch_fused_rows(const FusedLinearArgs &f, hipStream_t st) {
   const LinearArgs &a = f.lin;
   if constexpr (POST == POST_SWIGLU) {
-    if (a.n >= 8192) return launch_fused_t<G, KIND, 4, 1, PRE, POST>(f, 1024, st);
+    // one gate and one up row per wave (the 1B gate|up: step 0.5309 ->
+    // 0.5276 ms against 2 + 2 rows per wave, with every K step in flight)
+    if (a.n >= 8192) return launch_fused_t<G, KIND, 2, 1, PRE, POST>(f, 2048, st);
     return launch_fused_t<G, KIND, 2, 1, PRE, POST>(f, 4096, st);
   } else if constexpr (POST == POST_ARGMAX) {
     // whole rows per wave; the grid stays within kArgmaxMaxBlocks partials
-    if (a.n >= 65536) return launch_fused_t<G, KIND, 2, 1, PRE, POST>(f, 8192, st);
+    if (a.n >= 65536) return launch_fused_npf<G, KIND, 2, 1, PRE, POST, 1>(f, 8192, st);
     return launch_fused_t<G, KIND, 1, 1, PRE, POST>(f, 4096, st);
   } else {
     if (a.m > 4096 && a.m % 64 == 0) return launch_fused_t<G, KIND, 4, 4, PRE, POST>(f, 1024, st);
-    if (a.n >= 65536) return launch_fused_t<G, KIND, 2, 1, PRE, POST>(f, 8192, st);
+    if (a.n >= 65536) return launch_fused_npf<G, KIND, 2, 1, PRE, POST, 1>(f, 8192, st);
     if (a.n >= 8192) return launch_fused_t<G, KIND, 4, 1, PRE, POST>(f, 1024, st);
     // 2 rows per wave from 4096 rows (Llama-3.1-8B q|k|v and o: step
     // 2.308 -> 2.238 ms)
