@@ -1,6 +1,7 @@
 """Build libq8hip.so (the gfx950 Q8 kernels + C ABI) in-tree with hipcc.
 
     python -m lama32_mojo_amd.build          # -> lama32_mojo_amd/libq8hip.so
+    python -m lama32_mojo_amd.build --incremental   # only out-of-date objects
 
 Every source under csrc/ is compiled for gfx950 only, with
   * packed fp32 instructions disabled (-target-feature -packed-fp32-ops),
@@ -59,16 +60,29 @@ def _run(cmd, verbose):
         print(out, flush=True)
 
 
-def build(verbose: bool = True, jobs: int | None = None) -> str:
-    """Compile every csrc/ source and link libq8hip.so; returns its path."""
+def _stale(src: str, obj: str) -> bool:
+    """An object older than its source or any header it may include."""
+    if not os.path.exists(obj):
+        return True
+    deps = [src] + [os.path.join(CSRC, f) for f in os.listdir(CSRC) if f.endswith(".h")]
+    deps.append(os.path.join(os.path.dirname(HERE), "include", "q8hip.h"))
+    t = os.path.getmtime(obj)
+    return any(os.path.getmtime(d) > t for d in deps if os.path.exists(d))
+
+
+def build(verbose: bool = True, jobs: int | None = None, incremental: bool = False) -> str:
+    """Compile every csrc/ source and link libq8hip.so; returns its path.
+    incremental=True recompiles only sources whose object is out of date."""
     os.makedirs(BUILD_DIR, exist_ok=True)
     srcs = sources()
     objs = [os.path.join(BUILD_DIR, os.path.basename(s) + ".o") for s in srcs]
     cmds = []
     for s, o in zip(srcs, objs):
+        if incremental and not _stale(s, o):
+            continue
         lang = ["-x", "hip"] if s.endswith(".cpp") else []
         cmds.append([HIPCC, *COMMON_FLAGS, *lang, "-c", s, "-o", o])
-    jobs = jobs or min(len(cmds), max(1, min(8, os.cpu_count() or 1)))
+    jobs = jobs or min(max(len(cmds), 1), max(1, min(8, os.cpu_count() or 1)))
     with ThreadPoolExecutor(max_workers=jobs) as ex:
         list(ex.map(lambda c: _run(c, verbose), cmds))
     tmp = LIB_PATH + ".tmp"
@@ -82,4 +96,4 @@ def build(verbose: bool = True, jobs: int | None = None) -> str:
 
 
 if __name__ == "__main__":
-    build(verbose="-q" not in sys.argv)
+    build(verbose="-q" not in sys.argv, incremental="--incremental" in sys.argv)

@@ -7,16 +7,19 @@
 // The kernel is HBM-bound: every weight byte is read exactly once.  Layout
 // and mapping:
 //   * a wavefront owns R whole rows at a time (or, for rows longer than 4096
-//     codes, one K quarter of R rows shared by the workgroup's 4 waves); lane
-//     l owns the 16-byte code slices k = 16 l + 1024 i, so each load
+//     codes, one K quarter of R rows shared by a group of 4 waves); lane l
+//     owns the 16-byte code slices k = 16 l + 1024 i, so each load
 //     instruction is one 1 KiB fully coalesced run per row
 //     (global_load_dwordx4, non-temporal);
-//   * the R rows' loads are issued together, so a wave keeps R KiB in flight
-//     per step and many waves per CU cover HBM latency;
+//   * a wave issues a whole chunk of NPF steps of its R rows at once, so it
+//     keeps NPF R KiB in flight and waits for each step's loads alone: the
+//     dot products of the chunk's early steps overlap the later steps'
+//     arrival (the loop over a chunk has no branch, see compute_chunk);
 //   * the lane's 16 codes lie inside one quantization group (16 | G), so one
 //     scale per row per step is applied after the unscaled 16-term dot;
 //   * x (S rows of m f32) is staged once per workgroup in LDS and read with
-//     ds_read_b128;
+//     ds_read_b128, or held in registers (a wave K range of at most 2
+//     steps); either way its loads are issued before the weights;
 //   * each (row, batch) partial is reduced across the wave with DPP row
 //     moves plus readlane; lane 0 stores.
 // Rows are distributed over a grid sized to fill all 256 CUs; workgroups
@@ -37,34 +40,42 @@ constexpr int kLdsFloats = 16384;       // fused prologues stage x in LDS up to 
 constexpr int kLdsStageFloats = 8192;
 
 template <int G, int KIND, int S, int R, int SPLITK, bool XLDS, int PRE = PRE_NONE,
-          int POST = POST_STORE, int NPF = 1>
-__global__ __launch_bounds__(256) void gemv_kernel(
+          int POST = POST_STORE, int NPF = 1, int NW = kWaves>
+__global__ __launch_bounds__(64 * NW) void gemv_kernel(
     const uint8_t *__restrict__ w, int64_t row_bytes, int64_t n,
     const float *__restrict__ x, int64_t m, float *y, const uint16_t *__restrict__ wn,
     float eps, const float *res, float *__restrict__ amax) {
   extern __shared__ float xs[];
-  __shared__ float part[SPLITK > 1 ? SPLITK : 1][R][S];
+  __shared__ float part[SPLITK > 1 ? NW : 1][R][S];
   __shared__ float red[4];
+  static_assert(NW == kWaves || (SPLITK > 1 && NW % SPLITK == 0 && PRE != PRE_RMSNORM),
+                "workgroups of more than 4 waves are K-split row groups (no rmsnorm prologue)");
   static_assert(PRE == PRE_NONE || (XLDS && S == 1), "fused prologues stage one x row in LDS");
   static_assert(POST != POST_SWIGLU || (SPLITK == 1 && R % 2 == 0 && S == 1),
                 "the swiglu epilogue pairs gate and up rows within a wave");
   static_assert(POST != POST_ARGMAX || (SPLITK == 1 && S == 1),
                 "the argmax epilogue keeps whole rows per wave");
   constexpr int SB = ScaleTraits<KIND>::bytes;
+  constexpr int NT = 64 * NW;                   // threads
   const int lane = threadIdx.x & 63;
-  const int wid = threadIdx.x >> 6;
+  // wave-uniform by construction, so row pointers and K ranges live in
+  // scalar registers
+  const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int64_t scale_bytes = (m / G) * SB;
   // SPLITK == 1: each wave owns R rows over the whole K range.
-  // SPLITK == 4: the 4 waves of a workgroup share R rows, wave w owning the
-  // K range [w m/4, (w+1) m/4); partial sums meet in LDS.
+  // SPLITK == 4: each group of 4 waves of a workgroup (NW / 4 groups, one
+  // after another) shares R rows, wave w of a group owning the K range
+  // [w m/4, (w+1) m/4); partial sums meet in LDS.
   // POST_SWIGLU: a wave's R rows are R/2 gate rows j.. and the matching up
   // rows n/2 + j..; it stores the R/2 outputs silu(gate) * up.
   constexpr int RO = POST == POST_SWIGLU ? R / 2 : R;   // outputs per wave tile
   const int64_t nout = POST == POST_SWIGLU ? n / 2 : n;
-  const int64_t rows_per_group = SPLITK > 1 ? RO : (int64_t)kWaves * RO;
+  constexpr int RG = SPLITK > 1 ? NW / SPLITK : 1;   // row groups of a K split
+  const int rgw = SPLITK > 1 ? wid / SPLITK : 0;      // this wave's row group
+  const int64_t rows_per_group = SPLITK > 1 ? (int64_t)RG * RO : (int64_t)NW * RO;
   const int64_t stride_rows = (int64_t)gridDim.x * rows_per_group;
-  int64_t r0 = (int64_t)blockIdx.x * rows_per_group + (SPLITK > 1 ? 0 : wid * RO);
-  const int64_t k_lo = SPLITK > 1 ? wid * (m / SPLITK) : 0;
+  int64_t r0 = (int64_t)blockIdx.x * rows_per_group + (SPLITK > 1 ? rgw * RO : wid * RO);
+  const int64_t k_lo = SPLITK > 1 ? (wid % SPLITK) * (m / SPLITK) : 0;
   const int64_t k_hi = SPLITK > 1 ? k_lo + m / SPLITK : m;
   const int64_t k_first = k_lo + 16 * lane;
   // weight row of slot r for output tile r0 (clamped: tail slots recompute
@@ -100,6 +111,7 @@ __global__ __launch_bounds__(256) void gemv_kernel(
 #pragma unroll
       for (int r = 0; r < R; ++r) sc[p][r] = load_scale<KIND>(rowp[r], k / G);
     }
+    __builtin_amdgcn_sched_barrier(0);
   };
   const uint8_t *rowp[R];
 #pragma unroll
@@ -119,7 +131,7 @@ __global__ __launch_bounds__(256) void gemv_kernel(
   auto load_x = [&](int64_t i0) {
 #pragma unroll
     for (int u = 0; u < XB; ++u) {
-      const int64_t i = i0 + 4 * 256 * u;
+      const int64_t i = i0 + 4 * NT * u;
       if (i < tot) {
         xv[u] = *reinterpret_cast<const f32x4 *>(x + i);
         if constexpr (PRE == PRE_SWIGLU) uv[u] = *reinterpret_cast<const f32x4 *>(x + m + i);
@@ -148,11 +160,12 @@ __global__ __launch_bounds__(256) void gemv_kernel(
   // writes any of it.
   constexpr int RR = POST == POST_RESIDUAL ? (SPLITK > 1 ? 1 : RO * S) : 1;
   float resv[RR] = {};
-  const int64_t r0_first = r0;
   if constexpr (POST == POST_RESIDUAL) {
     if constexpr (SPLITK > 1) {
-      const int t = threadIdx.x < R * S ? threadIdx.x : 0;
-      const int64_t o = r0 + t / S < nout ? r0 + t / S : nout - 1;
+      // thread t < RG R S: row group t / (R S), row (t / S) % R, batch t % S
+      const int t = threadIdx.x < RG * R * S ? threadIdx.x : 0;
+      const int64_t tr = r0 - rgw * RO + (t / (R * S)) * RO + (t / S) % R;
+      const int64_t o = tr < nout ? tr : nout - 1;
       resv[0] = res[(t % S) * n + o];
     } else {
 #pragma unroll
@@ -164,6 +177,10 @@ __global__ __launch_bounds__(256) void gemv_kernel(
         }
     }
   }
+  // Every load above stays ahead of the first use: without this the
+  // scheduler sinks weight loads of later steps below the dot products of
+  // earlier ones, and fewer bytes are in flight while the first arrive.
+  __builtin_amdgcn_sched_barrier(0);
 
   // PRE_RMSNORM: x is staged as bf16(wn) * x and every output is scaled by
   // 1 / sqrt(mean(x^2) + eps) at the end (W (wn x inv) = inv W (wn x)); the
@@ -174,11 +191,11 @@ __global__ __launch_bounds__(256) void gemv_kernel(
     float ss = 0.0f;
     // batches of XB independent 16-byte loads per thread, then the LDS
     // stores (a load-store-load chain would wait on L2 once per step)
-    for (int64_t i0 = 4 * threadIdx.x; i0 < tot; i0 += 4 * 256 * XB) {
+    for (int64_t i0 = 4 * threadIdx.x; i0 < tot; i0 += 4 * NT * XB) {
       if (i0 != 4 * threadIdx.x) load_x(i0);     // the first batch is in flight already
 #pragma unroll
       for (int u = 0; u < XB; ++u) {
-        const int64_t i = i0 + 4 * 256 * u;
+        const int64_t i = i0 + 4 * NT * u;
         if (i >= tot) continue;
         f32x4 o = xv[u];
         if constexpr (PRE == PRE_SWIGLU) {
@@ -213,8 +230,8 @@ __global__ __launch_bounds__(256) void gemv_kernel(
   }
 
   // one finished output (value v of tile slot r) -> memory
-  // (rv: the prefetched residual when t0 is the first tile)
-  auto store = [&](int64_t t0, int r, int b, float v, float v_up, float rv) {
+  // (rv: the prefetched residual, used for the first tile)
+  auto store = [&](int64_t t0, int r, int b, float v, float v_up, float rv, bool first_tile) {
     const int64_t o = t0 + r;
     if (o >= nout) return;
     if constexpr (POST == POST_SWIGLU) {
@@ -222,58 +239,57 @@ __global__ __launch_bounds__(256) void gemv_kernel(
       y[o] = (g / (1.0f + expf(-g))) * u;
     } else {
       v = inv * v;
-      if constexpr (POST == POST_RESIDUAL) v = (t0 == r0_first ? rv : res[b * n + o]) + v;
+      if constexpr (POST == POST_RESIDUAL) v = (first_tile ? rv : res[b * n + o]) + v;
       y[b * n + o] = v;
     }
   };
 
   float best_v = -INFINITY;              // POST_ARGMAX: lane 0's best row so far
   int best_i = INT32_MAX;
-  bool first = true;
-  for (; r0 < nout; r0 += stride_rows) {
-    float acc[R][S];
-#pragma unroll
-    for (int r = 0; r < R; ++r)
-#pragma unroll
-      for (int b = 0; b < S; ++b) acc[r][b] = 0.0f;
-    if (!first) {
-#pragma unroll
-      for (int r = 0; r < R; ++r) rowp[r] = w + row_of(r0, r) * row_bytes;
-    }
 
-    for (int64_t kc = k_first; kc < k_hi; kc += 1024 * NPF) {
-      if (first)
-        first = false;                   // loaded before x was staged
-      else
-        load_chunk(rowp, kc);
+  // The dot products of one chunk of NPF steps starting at the
+  // wave-uniform kw (each lane adds its own offset), from the loads in q
+  // and sc.  No step sits in a branch: a lane whose step lies past the
+  // range reads a valid x slice and keeps its sum (a select), so the
+  // compiler waits for each step's loads alone and the dot products of
+  // early steps overlap the loads still in flight (a branch here made
+  // every wave wait for all of its loads, and with x read from L2 inside
+  // it, for one more round trip per step).
+  const int64_t kx_safe = k_first < k_hi ? k_first : k_lo;
+  auto compute_chunk = [&](int64_t kw, float (&acc)[R][S]) {
+    const int64_t kc = kw + 16 * lane;
 #pragma unroll
-      for (int p = 0; p < NPF; ++p) {
-        const int64_t k = kc + 1024 * p;
-        if (k < k_hi) {
+    for (int p = 0; p < NPF; ++p) {
+      const int64_t k = kc + 1024 * p;
+      const bool live = k < k_hi;
+      const int64_t kx = live ? k : kx_safe;
 #pragma unroll
-          for (int b = 0; b < S; ++b) {
-            f32x4 xa, xb, xc, xd;
-            if (XREG && kc == k_first) {
-              xa = xr[XREG ? p : 0][0];
-              xb = xr[XREG ? p : 0][1];
-              xc = xr[XREG ? p : 0][2];
-              xd = xr[XREG ? p : 0][3];
-            } else {
-              const f32x4 *xv4 = reinterpret_cast<const f32x4 *>(xp + b * m + k);
-              xa = xv4[0];
-              xb = xv4[1];
-              xc = xv4[2];
-              xd = xv4[3];
-            }
+      for (int b = 0; b < S; ++b) {
+        f32x4 xa, xb, xc, xd;
+        if (XREG && kw == k_lo) {
+          xa = xr[XREG ? p : 0][0];
+          xb = xr[XREG ? p : 0][1];
+          xc = xr[XREG ? p : 0][2];
+          xd = xr[XREG ? p : 0][3];
+        } else {
+          const f32x4 *xv4 = reinterpret_cast<const f32x4 *>(xp + b * m + kx);
+          xa = xv4[0];
+          xb = xv4[1];
+          xc = xv4[2];
+          xd = xv4[3];
+        }
 #pragma unroll
-            for (int r = 0; r < R; ++r)
-              acc[r][b] =
-                  __builtin_fmaf(sc[p][r], dot16(q[p][r], xa, xb, xc, xd), acc[r][b]);
-          }
+        for (int r = 0; r < R; ++r) {
+          const float t = __builtin_fmaf(sc[p][r], dot16(q[p][r], xa, xb, xc, xd), acc[r][b]);
+          acc[r][b] = live ? t : acc[r][b];
         }
       }
     }
+  };
 
+  // A finished tile: wave sums, the K split's partials met in LDS, the
+  // epilogue.
+  auto finish_tile = [&](int64_t t0, const float (&acc)[R][S], bool first_tile) {
     if constexpr (SPLITK == 1) {
       float v[R][S];
 #pragma unroll
@@ -285,17 +301,17 @@ __global__ __launch_bounds__(256) void gemv_kernel(
         for (int r = 0; r < RO; ++r)
 #pragma unroll
           for (int b = 0; b < S; ++b)
-            store(r0, r, b, v[r][b], POST == POST_SWIGLU ? v[(r + RO) % R][b] : 0.0f,
-                  resv[POST == POST_RESIDUAL ? r * S + b : 0]);
+            store(t0, r, b, v[r][b], POST == POST_SWIGLU ? v[(r + RO) % R][b] : 0.0f,
+                  resv[POST == POST_RESIDUAL ? r * S + b : 0], first_tile);
         if constexpr (POST == POST_ARGMAX) {
           // rows in increasing order, strict >: the lowest row among equal
           // values; NaN never wins
 #pragma unroll
           for (int r = 0; r < R; ++r) {
             const float yv = inv * v[r][0];
-            if (r0 + r < n && yv > best_v) {
+            if (t0 + r < n && yv > best_v) {
               best_v = yv;
-              best_i = (int)(r0 + r);
+              best_i = (int)(t0 + r);
             }
           }
         }
@@ -309,15 +325,48 @@ __global__ __launch_bounds__(256) void gemv_kernel(
           if (lane == 0) part[wid][r][b] = v;
         }
       __syncthreads();
-      if (threadIdx.x < R * S) {
-        const int r = threadIdx.x / S, b = threadIdx.x % S;
-        float v = part[0][r][b];
+      if (threadIdx.x < RG * R * S) {
+        const int g = threadIdx.x / (R * S), r = (threadIdx.x / S) % R, b = threadIdx.x % S;
+        float v = part[g * SPLITK][r][b];
 #pragma unroll
-        for (int u = 1; u < SPLITK; ++u) v += part[u][r][b];
-        store(r0, r, b, v, 0.0f, resv[0]);
+        for (int u = 1; u < SPLITK; ++u) v += part[g * SPLITK + u][r][b];
+        store(t0 - rgw * RO + g * RO, r, b, v, 0.0f, resv[0], first_tile);
       }
       __syncthreads();
     }
+  };
+
+  // The first tile's first chunk was loaded before x was staged; it is
+  // consumed in straight-line code, with no branch between those loads and
+  // their use (a wave whose first tile lies past the outputs computes on
+  // the clamped rows it loaded and stores nothing), and every wave reaches
+  // the barriers of finish_tile.
+  {
+    float acc[R][S];
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+      for (int b = 0; b < S; ++b) acc[r][b] = 0.0f;
+    compute_chunk(k_lo, acc);
+    for (int64_t kw = k_lo + 1024 * NPF; kw < k_hi; kw += 1024 * NPF) {
+      load_chunk(rowp, kw + 16 * lane);
+      compute_chunk(kw, acc);
+    }
+    finish_tile(r0, acc, true);
+  }
+  for (r0 += stride_rows; r0 < nout; r0 += stride_rows) {
+#pragma unroll
+    for (int r = 0; r < R; ++r) rowp[r] = w + row_of(r0, r) * row_bytes;
+    float acc[R][S];
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+      for (int b = 0; b < S; ++b) acc[r][b] = 0.0f;
+    for (int64_t kw = k_lo; kw < k_hi; kw += 1024 * NPF) {
+      load_chunk(rowp, kw + 16 * lane);
+      compute_chunk(kw, acc);
+    }
+    finish_tile(r0, acc, false);
   }
   if constexpr (POST == POST_ARGMAX) {
     __shared__ float bv[kWaves];
@@ -390,23 +439,24 @@ template <int R, int S> constexpr int npf_for() { return R * S >= 4 ? 1 : 4; }
 
 inline bool two_steps(int64_t m, int splitk) { return m / splitk <= 2048; }
 
-template <int G, int KIND, int S, int R, int SPLITK, int NPF>
+template <int G, int KIND, int S, int R, int SPLITK, int NPF, int NW = kWaves>
 hipError_t launch_fast_t(const LinearArgs &a, const float *x, float *y, int64_t cap,
                          hipStream_t st) {
-  const int64_t rows_per_group = SPLITK > 1 ? R : kWaves * R;
+  const int64_t rows_per_group = SPLITK > 1 ? (int64_t)(NW / SPLITK) * R : (int64_t)NW * R;
   const int64_t tiles = (a.n + rows_per_group - 1) / rows_per_group;
-  dim3 grid(grid_for(tiles, cap)), block(256);
-  // x staged in LDS for rows up to the stage limit, except when each lane's
-  // x slices fit in registers (one activation row, a wave K range of at
-  // most 2 steps): those are loaded before the weights and need no stage or
-  // barrier (the 8192 x 2048 linear: 6.40 -> 5.82 us)
-  const bool xreg = S == 1 && NPF <= 2 && a.m / SPLITK <= 1024 * NPF;
-  if (S * a.m <= kLdsStageFloats && !xreg) {
+  dim3 grid(grid_for(tiles, cap)), block(64 * NW);
+  // x staged in LDS for rows up to the stage limit (and always in the
+  // workgroups of K-split row groups), except when each lane's x slices fit
+  // in registers (one activation row, a wave K range of at most 2 steps):
+  // those are loaded before the weights and need no stage or barrier (the
+  // 8192 x 2048 linear: 6.40 -> 5.82 us)
+  const bool xreg = NW == kWaves && S == 1 && NPF <= 2 && a.m / SPLITK <= 1024 * NPF;
+  if ((NW > kWaves || S * a.m <= kLdsStageFloats) && !xreg) {
     size_t lds = (size_t)S * a.m * sizeof(float);
-    hipLaunchKernelGGL((gemv_kernel<G, KIND, S, R, SPLITK, true, PRE_NONE, POST_STORE, NPF>), grid,
-                       block, lds, st, a.w, a.row_bytes, a.n, x, a.m, y, nullptr, 0.0f, nullptr,
-                       nullptr);
-  } else {
+    hipLaunchKernelGGL((gemv_kernel<G, KIND, S, R, SPLITK, true, PRE_NONE, POST_STORE, NPF, NW>),
+                       grid, block, lds, st, a.w, a.row_bytes, a.n, x, a.m, y, nullptr, 0.0f,
+                       nullptr, nullptr);
+  } else if constexpr (NW == kWaves) {
     hipLaunchKernelGGL((gemv_kernel<G, KIND, S, R, SPLITK, false, PRE_NONE, POST_STORE, NPF>),
                        grid, block, 0, st, a.w, a.row_bytes, a.n, x, a.m, y, nullptr, 0.0f,
                        nullptr, nullptr);
@@ -425,6 +475,22 @@ hipError_t launch_fast(const LinearArgs &a, const float *x, float *y, int64_t ca
   }
 }
 
+// Long rows at one activation row and at least 4096 outputs: the K split
+// over 4 waves, in workgroups of 4 row groups (16 waves, 16 rows, one
+// workgroup per CU at 4096 rows) that stage x once in LDS with one batch of
+// loads issued ahead of the weights, so x is read from LDS independently of
+// the weights' arrival and fetched once per 16 rows instead of once per 4
+// from L2.  Each wave streams its K range in chunks of 2 steps: the second
+// chunk's loads go out while the first chunk's dot products run (the
+// Llama-3.1-8B down projection 14336 -> 4096: 16.0 us with 4 rows per
+// workgroup and x from L2, 17.2 with 16 waves and 4-step chunks, 13.5 with
+// 2-step chunks; Qwen3-8B 12288 -> 4096 14.8 -> 13.3 us).  Fewer outputs
+// keep the 4-wave workgroups (with 8 waves the 1B down projection ran 6.0
+// against 5.9 us).  The stage holds m floats.
+inline bool long_row_groups(const LinearArgs &a) {
+  return a.s == 1 && a.m <= kLdsFloats && a.n >= 4096;
+}
+
 // Shape classes (tuned on MI355X, decode shapes of Llama-3.2-1B / Qwen3-8B):
 //   long rows (m > 4096):         K split over the 4 waves, 4 rows per workgroup
 //   vocabulary heads (n >= 64K):  2 rows per wave, up to 8192 workgroups
@@ -432,7 +498,12 @@ hipError_t launch_fast(const LinearArgs &a, const float *x, float *y, int64_t ca
 //   small:                        1 row per wave
 template <int G, int KIND, int S>
 hipError_t launch_rows(const LinearArgs &a, const float *x, float *y, hipStream_t st) {
-  if (a.m > 4096 && a.m % 64 == 0) return launch_fast<G, KIND, S, 4, 4>(a, x, y, 1024, st);
+  if (a.m > 4096 && a.m % 64 == 0) {
+    if constexpr (S == 1) {
+      if (long_row_groups(a)) return launch_fast_t<G, KIND, S, 4, 4, 2, 16>(a, x, y, 256, st);
+    }
+    return launch_fast<G, KIND, S, 4, 4>(a, x, y, 1024, st);
+  }
   // vocabulary heads: one K step in flight per wave (more waves per CU; the
   // 8192 workgroups walk about two row tiles each, so occupancy, not one
   // round of loads, covers the latency: 2 steps made the 1B lm_head 42 ->
@@ -479,14 +550,14 @@ hipError_t launch_g(const LinearArgs &a, hipStream_t st) {
   return hipSuccess;
 }
 
-template <int G, int KIND, int R, int SPLITK, int PRE, int POST, int NPF>
+template <int G, int KIND, int R, int SPLITK, int PRE, int POST, int NPF, int NW = kWaves>
 hipError_t launch_fused_npf(const FusedLinearArgs &f, int64_t cap, hipStream_t st) {
   const LinearArgs &a = f.lin;
   constexpr int RO = POST == POST_SWIGLU ? R / 2 : R;
   const int64_t nout = POST == POST_SWIGLU ? a.n / 2 : a.n;
-  const int64_t rows_per_group = SPLITK > 1 ? RO : kWaves * RO;
+  const int64_t rows_per_group = SPLITK > 1 ? (int64_t)(NW / SPLITK) * RO : (int64_t)NW * RO;
   const int64_t tiles = (nout + rows_per_group - 1) / rows_per_group;
-  dim3 grid(grid_for(tiles, cap)), block(256);
+  dim3 grid(grid_for(tiles, cap)), block(64 * NW);
   const float *x = reinterpret_cast<const float *>(a.x);
   // x read from L2 by every wave past the stage limit, and held in
   // registers (loaded before the weights) when a wave's K range is at most
@@ -496,14 +567,14 @@ hipError_t launch_fused_npf(const FusedLinearArgs &f, int64_t cap, hipStream_t s
   // 1B gate|up 8.57 -> 11.0 us (registers past one round of workgroups,
   // and x and the norm weights fetched per wave instead of per workgroup).
   if (f.grid_out) *f.grid_out = (int)grid.x;
-  if constexpr (PRE == PRE_NONE) {
+  if constexpr (PRE == PRE_NONE && NW == kWaves) {
     if (a.m > kLdsStageFloats || (NPF <= 2 && a.m / SPLITK <= 1024 * NPF)) {
       hipLaunchKernelGGL((gemv_kernel<G, KIND, 1, R, SPLITK, false, PRE, POST, NPF>), grid, block,
                          0, st, a.w, a.row_bytes, a.n, x, a.m, a.y, f.wn, f.eps, f.res, f.part);
       return hipGetLastError();
     }
   }
-  hipLaunchKernelGGL((gemv_kernel<G, KIND, 1, R, SPLITK, true, PRE, POST, NPF>), grid, block,
+  hipLaunchKernelGGL((gemv_kernel<G, KIND, 1, R, SPLITK, true, PRE, POST, NPF, NW>), grid, block,
                      (size_t)a.m * sizeof(float), st, a.w, a.row_bytes, a.n, x, a.m, a.y, f.wn,
                      f.eps, f.res, f.part);
   return hipGetLastError();
@@ -530,7 +601,14 @@ hipError_t launch_fused_rows(const FusedLinearArgs &f, hipStream_t st) {
     if (a.n >= 65536) return launch_fused_npf<G, KIND, 2, 1, PRE, POST, 1>(f, 8192, st);
     return launch_fused_t<G, KIND, 1, 1, PRE, POST>(f, 4096, st);
   } else {
-    if (a.m > 4096 && a.m % 64 == 0) return launch_fused_t<G, KIND, 4, 4, PRE, POST>(f, 1024, st);
+    if (a.m > 4096 && a.m % 64 == 0) {
+      // (a swiglu prologue stages [gate | up]: its registers do not fit the
+      // 16-wave workgroups, and the decode step never uses it on long rows)
+      if constexpr (PRE == PRE_NONE) {
+        if (long_row_groups(a)) return launch_fused_npf<G, KIND, 4, 4, PRE, POST, 2, 16>(f, 256, st);
+      }
+      return launch_fused_t<G, KIND, 4, 4, PRE, POST>(f, 1024, st);
+    }
     if (a.n >= 65536) return launch_fused_npf<G, KIND, 2, 1, PRE, POST, 1>(f, 8192, st);
     if (a.n >= 8192) return launch_fused_t<G, KIND, 4, 1, PRE, POST>(f, 1024, st);
     // 2 rows per wave from 4096 rows (Llama-3.1-8B q|k|v and o: step

@@ -170,6 +170,36 @@ def test_fused_gemv_8b_shapes_against_float64(ctx, cor, G, scale, m, n, pre, pos
     P.free()
 
 
+# (m, n): rows longer than 4096 codes at one activation row take the K split
+# in workgroups of 16 waves (n >= 4096, 16 rows each, at most 256
+# workgroups looping over the rest) or 8 waves (n >= 2048, 8 rows each) with
+# x staged in LDS; ragged n leaves a partial last tile, and 8896 rows make
+# every workgroup walk two or three tiles.
+LONG_ROWS_RAGGED = [(8192, 4100), (8192, 2050), (5120, 8896), (12288, 2056)]
+
+
+@pytest.mark.parametrize("G,scale", LAYOUTS)
+@pytest.mark.parametrize("m,n", LONG_ROWS_RAGGED)
+def test_long_rows_ragged_against_float64(ctx, cor, G, scale, m, n):
+    """q8_linear and q8_linear_fused (residual in place) on the long-row
+    K-split workgroups, ragged and multi-tile, within 1e-5 of float64."""
+    say("long rows", G, scale, m, n)
+    P = Packed(ctx, n, m, G, scale, seed=m + 3 * n)
+    x = synth_x(1, m, seed=5)
+    y = run_linear(ctx, P, x)
+    ref = cor.linear_f64(P.pk, x, G, scale)
+    assert max_rel_err(y, ref) <= 1e-5
+    res = np.random.default_rng(n).standard_normal(n).astype(np.float32)
+    a = ctx.alloc(4 * (m + n))
+    a.upload(x)
+    a.upload(res, 4 * m)
+    q8hip.linear_fused(ctx, P.w, 0, a, 0, m, m, n, G, scale, post=q8hip.POST_RESIDUAL, ores_f32=m)
+    got = a.download((n,), np.float32, 4 * m)
+    a.free()
+    assert max_rel_err(got, res.astype(np.float64) + ref[0]) <= 1e-5
+    P.free()
+
+
 @pytest.mark.parametrize("G,scale", LAYOUTS)
 def test_head_argmax_untied_8b_head(ctx, cor, G, scale):
     """q8_head_argmax over the untied Llama-3.1-8B head (4096 -> 128256):
