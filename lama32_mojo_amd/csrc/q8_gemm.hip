@@ -1,5 +1,5 @@
 // q8_gemm.hip -- prefill-path Q8 GEMM on gfx950 f16 MFMA, weights
-// dequantized in registers.
+// dequantized once per workgroup into LDS.
 //
 // y[i, j] = sum_k x[i, k] * (q[j, k] * scale[j, k / G])
 // (k_mm_q8's product, src/llama_q8.mojo:73-84) as a dequant-GEMM on
@@ -11,11 +11,11 @@
 //      f32 scales the same launch gives every weight row j an exponent f_j
 //      that puts its largest scale in [2^7, 2^8) (binary16 scales need none:
 //      f_j = 0);
-//   2. gemm_kernel: each lane turns its column's int8 codes into binary16
-//      weights q * s 2^-f_j in registers and feeds them to the MFMA as the B
-//      operand; the activations come through LDS as the A operand; the f32
-//      accumulators need no per-group rescale, and each output is scaled
-//      once by 2^(e_i + f_j).
+//   2. gemm_kernel: producer waves turn int8 codes into binary16 weights
+//      q * s 2^-f_j and stage them, with the binary16 activations, in LDS;
+//      consumer waves run the MFMAs on both (A = activations, B = weights);
+//      the f32 accumulators need no per-group rescale, and each output is
+//      scaled once by 2^(e_i + f_j).
 // Rounding: the binary16 weight carries one rounding of q * s (two with f32
 // scales: s 2^-f_j is rounded to binary16 first), i.e. a relative error
 // below 2^-11 each; products and sums are f32.  Without the row exponent
@@ -24,26 +24,11 @@
 // groups 2^21 times smaller than their row's largest group do, and their
 // share of any output is that much smaller.
 //
-// Cost model (per SIMD: 512 MFMA MACs or 16 VALU lanes per clock).  A weight
-// costs 1.75 VALU operations (one xor per 4 codes, then per 2 codes a v_perm
-// that builds binary16 1024 + (q + 128), a packed subtract of 1152 and a
-// packed multiply by the scale) and is used by BM rows; the activations
-// cost no VALU work in the loop.  At BM = 128 the VALU needs ~0.44 clocks
-// per MFMA clock.
-//
-// Work decomposition (one workgroup of 8 waves per BM x BN output tile,
-// BN = 128 * TN): the waves form 4 column groups of 32 * TN outputs x 2
-// K-parities; wave (p, h) owns TN column tiles of 32 and all BM rows and
-// takes the second 64-code slot of each 128-code iteration when h = 1; the
-// two parities meet in LDS at the end.  Per iteration the workgroup stages
-// three tiles through registers into double-buffered LDS, each loaded with
-// whole 128-byte lines: activations (BM x 128 binary16), codes (BN rows x
-// 128 bytes, 16-byte chunks XOR-swizzled by row) and, every other
-// iteration, the scales of the next two.  A lane then reads its column's
-// codes and scales from LDS and dequantizes them in registers as the MFMA
-// B operand; the MFMA K order inside a slot is permuted so each lane's
-// codes come in two 16-byte chunks and no k-step straddles a quantization
-// group (the A fragments read from LDS use the same permutation).
+// Cost per weight (dequantized once per workgroup, used by BM rows): 1.75
+// VALU operations (one xor per 4 codes, then per 2 codes a v_perm that
+// builds binary16 1024 + (q + 128), a packed subtract of 1152 and a packed
+// multiply by the scale) and one 2-byte LDS write, read back by 4 consumer
+// waves.
 #include "q8_device.h"
 #include "q8_launch.h"
 
@@ -53,9 +38,6 @@ namespace {
 typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 
-constexpr int KT = 128;        // k per iteration = two 64-code slots
-constexpr int kWaves = 8;      // waves per workgroup: 8 (two K parities) or 4
-constexpr int LDA = KT + 8;    // halves per LDS row (16-byte pad)
 
 // ---- 1. activation rows to binary16 ----------------------------------------
 // Exponent f that puts a weight row's largest f32 scale mx in [2^7, 2^8):
@@ -211,132 +193,161 @@ __device__ __forceinline__ f16x8 dequant8(uint32_t d0, uint32_t d1, f16x2 s2) {
   return f16x8{a.x, a.y, b.x, b.y, c.x, c.y, d.x, d.y};
 }
 
-template <int G, int KIND, int BM, int TN, int NW>
-__global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(NW / 4, NW / 4)))
+// One workgroup per BM x BN output tile (BM = 32 TM, BN = 128 TN), its 12
+// waves split by role, three per SIMD:
+//   * waves 0-3 (consumers) only read MFMA fragments from LDS and issue the
+//     MFMAs, each over all BM rows and its own 32 TN columns (TM x TN
+//     accumulator tiles of 32 x 32);
+//   * waves 4-11 (producers) stream the tiles of later iterations
+//     (activations and codes PD iterations ahead, in registers), dequantize
+//     each weight once into binary16 q * s 2^-f_j and write both tiles into
+//     a double-buffered LDS stage.
+// So the dequantizing VALU work runs beside the matrix core instead of in
+// the MFMA waves' instruction stream; one barrier per iteration hands the
+// stages over.  Tiles hold KS = 64 codes of K; LDS rows are padded by 16
+// bytes (the 16-byte fragment reads of 8 neighbouring rows fall on
+// different banks).
+//
+// Measured on the 1B / 8B prefill shapes against one 8-wave role-free form
+// (every wave staging, dequantizing its own columns in registers and
+// issuing MFMAs, two K parities): 512x16384x2048 63.2 -> 55.4 us,
+// 2048x14336x4096 342 -> 307 us, 2048x4096x14336 309 -> 276 us.  Alone,
+// the consumers reach 1.45 PFLOP/s on 2048x14336x4096 and the producers
+// take 225 us: the producers set the pace (their loads, dequantizing VALU
+// and LDS writes run in lockstep phases between the barriers; LDS takes
+// about 385 GB/s of 16-byte reads and 174 GB/s of 16-byte writes per CU
+// here), and 4 producer waves instead of 8, or 3-4 register stages instead
+// of 2, were slower or equal.
+constexpr int KS = 64;             // k per iteration
+constexpr int LDS_ROW = KS + 8;    // halves per LDS row
+constexpr int kProducerWaves = 8;
+constexpr int kStages = 2;         // register stages of the producers
+
+template <int G, int KIND, int TM, int TN, int NPW = kProducerWaves, int PD = kStages>
+__global__ __launch_bounds__(64 * (4 + NPW)) __attribute__((amdgpu_waves_per_eu(1 + NPW / 4, 1 + NPW / 4)))
 void gemm_kernel(const uint8_t *__restrict__ w, int64_t row_bytes,
-                   const uint16_t *__restrict__ x16, const int *__restrict__ ex,
-                   const int *__restrict__ ew, float *__restrict__ y, int64_t s, int64_t m,
-                   int64_t n, int nit, float *__restrict__ ws) {
-  // blockIdx.z selects a K range of nit iterations (split-K): with
-  // gridDim.z == 1 y is written directly, otherwise split z writes its
-  // partial sums to ws[z] and splitk_reduce_kernel adds them up.
-  constexpr int NT = 64 * NW;                 // threads
-  constexpr int NP = NW / 4;                  // K parities among the waves (1 or 2)
+                    const uint16_t *__restrict__ x16, const int *__restrict__ ex,
+                    const int *__restrict__ ew, float *__restrict__ y, int64_t s, int64_t m,
+                    int64_t n, int nit, float *__restrict__ ws) {
+  constexpr int BM = 32 * TM, BN = 128 * TN;
   constexpr int SB = ScaleTraits<KIND>::bytes;
-  constexpr int TM = BM / 32;                 // 32-row MFMA tiles per wave
-  constexpr int BN = 128 * TN;
-  constexpr int AU = BM * KT / 8 / NT;        // 8-half A chunks per thread
-  constexpr int NG = 64 / G;                  // groups per 64-code slot
-  constexpr int SPB = (KT / G) * SB;          // scale bytes of a row per iteration
-  constexpr int SDW = BN * SPB / 4;           // ... as dwords per block
-  constexpr int SU = (SDW + NT - 1) / NT;     // ... per thread
-  constexpr int CU = BN * KT / 16 / NT;       // 16-byte code chunks per thread
-  __shared__ __attribute__((aligned(16))) uint16_t As[2][BM * LDA];
-  __shared__ __attribute__((aligned(16))) uint8_t Bs[2][BN * KT];    // codes, swizzled rows
-  __shared__ __attribute__((aligned(16))) uint8_t Ss[2][BN * SPB];   // scales
+  constexpr int NPT = 64 * NPW;                  // producer threads
+  constexpr int NT = 256 + NPT;                  // threads
+  constexpr int AC = BM * (KS / 8) / NPT;        // 8-half activation chunks per producer
+  constexpr int BC = BN * (KS / 16) / NPT;       // 16-code weight chunks per producer
+  static_assert(AC >= 1 && BC >= 1, "tile too small for the producer waves");
+  __shared__ __attribute__((aligned(16))) _Float16 As[2][BM * LDS_ROW];
+  __shared__ __attribute__((aligned(16))) _Float16 Bs[2][BN * LDS_ROW];
   __shared__ int exs[BM];
+  __shared__ int ews[BN];
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int p = wid & 3, h0 = wid >> 2;
-  const int lr = lane & 31, lh = lane >> 5;
   const int64_t n0 = (int64_t)blockIdx.x * BN, m0 = (int64_t)blockIdx.y * BM;
-  // This split covers codes [kbase, kbase + nit * KT); iteration it covers
-  // the 128 codes from kbase + KT it: with 8 waves parity h0 takes the
-  // 64-code slot at 64 h0, with 4 waves each wave takes both slots.
-  const int64_t kbase = (int64_t)blockIdx.z * nit * KT;
-
-  // Weights: this block's (at most) BN packed rows; a row past n lies past
-  // the resource (its loads read zeros).
-  const int64_t nrows = n - n0 < BN ? n - n0 : BN;
-  const rsrc_t wr = make_rsrc(w + n0 * row_bytes, (uint32_t)(nrows * row_bytes));
-  // Code tiles: BN rows x 128 codes per iteration, 8 threads per 128-byte
-  // row (coalesced), staged through registers.  The 16-byte chunk c of row
-  // r sits at LDS chunk c ^ ((r >> 1) & 7): the 16 rows one ds_read_b128
-  // pass reads then fall on 16 different bank groups.
-  auto load_codes = [&](u32x4 *dst, int it) {
-#pragma unroll
-    for (int u = 0; u < CU; ++u) {
-      const int c = tid + NT * u, r = c >> 3;
-      dst[u] = bload16(wr, (uint32_t)(r * row_bytes + (m / G) * SB + kbase + KT * it + 16 * (c & 7)));
-    }
-  };
-  auto store_codes = [&](const u32x4 *src, int buf) {
-#pragma unroll
-    for (int u = 0; u < CU; ++u) {
-      const int c = tid + NT * u, r = c >> 3;
-      *reinterpret_cast<u32x4 *>(&Bs[buf][r * KT + 16 * ((c & 7) ^ ((r >> 1) & 7))]) = src[u];
-    }
-  };
-  // Scale tiles: BN rows x SPB bytes per iteration, as dwords (thread t
-  // takes dwords t, t + NT, ... of the [BN][SPB / 4] tile; a thread past the
-  // tile loads a duplicate it does not store, so no load sits in a branch).
-  auto load_scales = [&](uint32_t *dst, int it) {
-#pragma unroll
-    for (int u = 0; u < SU; ++u) {
-      const int i = (tid + NT * u) % SDW;
-      dst[u] = __builtin_amdgcn_raw_buffer_load_b32(
-          wr, (uint32_t)((i / (SPB / 4)) * row_bytes + (kbase + KT * it) / G * SB +
-                         4 * (i % (SPB / 4))), 0, 0);
-    }
-  };
-  auto store_scales = [&](const uint32_t *src, int buf) {
-#pragma unroll
-    for (int u = 0; u < SU; ++u) {
-      const int i = tid + NT * u;
-      if (i < SDW) *reinterpret_cast<uint32_t *>(&Ss[buf][4 * i]) = src[u];
-    }
-  };
-  // This lane's column within the block for tile t
-  auto bcol = [&](int t) { return p * 32 * TN + 32 * t + lr; };
-  // k-step ks of lane half lh reads codes (offsets within the slot)
-  //   G=64: [32 lh + 8 ks, +8)                      (chunks at 32 lh, 32 lh + 16)
-  //   G=32: [32 (ks / 2) + 16 lh + 8 (ks % 2), +8)   (chunks at 16 lh, 32 + 16 lh)
-  // so for G = 32 k-steps 0..1 are the slot's first group and 2..3 its second.
-  const int chunk0 = G == 64 ? 32 * lh : 16 * lh;
-  const int chunk1 = G == 64 ? 32 * lh + 16 : 32 + 16 * lh;
-
-  // Activations (binary16 rows from act16_kernel): this block's (at most)
-  // BM rows, 128 k per iteration; chunk u of a thread is row c / 16, k
-  // 8 (c % 16) .. +8 (c = tid + NT u).  A row past s lies past the
-  // resource, a column past m is sent past it explicitly.
+  const int64_t kbase = (int64_t)blockIdx.z * nit * KS;   // this split's first code
   const int64_t arows = s - m0 < BM ? s - m0 : BM;
-  const rsrc_t xr = make_rsrc(x16 + m0 * m, (uint32_t)(arows * m * 2));
-  const int64_t mk = m - kbase;
-  uint32_t vx[AU];
-  int akc[AU];
+  const int64_t nrows = n - n0 < BN ? n - n0 : BN;
+
+  for (int t = tid; t < BM; t += NT) exs[t] = t < arows ? ex[m0 + t] : 0;
+  for (int t = tid; t < BN; t += NT) ews[t] = KIND == SCALE_F32 && t < nrows ? ew[n0 + t] : 0;
+  __syncthreads();
+
+  if (wid >= 4) {
+    // ---- producers ----
+    const int pt = tid - 256;
+    const rsrc_t wr = make_rsrc(w + n0 * row_bytes, (uint32_t)(nrows * row_bytes));
+    const rsrc_t xr = make_rsrc(x16 + m0 * m, (uint32_t)(arows * m * 2));
+    // activation chunk u: row c / 8, halves 8 (c % 8) .. +8 of the tile's
+    // 64 (c = pt + 256 u; 8 threads read one 128-byte row run); weight chunk
+    // u: row c / 4, codes 16 (c % 4) .. +16 (4 threads per 64-byte run).  A
+    // 16-code chunk never leaves its quantization group (16 | G).
+    uint32_t aoff[AC], boff[BC], soff[BC];
+    int arow[AC], akq[AC], brow[BC], bkc[BC];
 #pragma unroll
-  for (int u = 0; u < AU; ++u) {
-    const int c = tid + NT * u;
-    akc[u] = (c % (KT / 8)) * 8;
-    vx[u] = (uint32_t)(((c / (KT / 8)) * m + kbase + akc[u]) * 2);
+    for (int u = 0; u < AC; ++u) {
+      const int c = pt + NPT * u;
+      arow[u] = c >> 3;
+      akq[u] = c & 7;
+      aoff[u] = (uint32_t)((arow[u] * m + kbase + 8 * akq[u]) * 2);
+    }
+#pragma unroll
+    for (int u = 0; u < BC; ++u) {
+      const int c = pt + NPT * u;
+      brow[u] = c >> 2;
+      bkc[u] = c & 3;
+      boff[u] = (uint32_t)(brow[u] * row_bytes + (m / G) * SB + kbase + 16 * bkc[u]);
+      soff[u] = (uint32_t)(brow[u] * row_bytes + ((kbase + 16 * bkc[u]) / G) * SB);
+    }
+    struct Stage {
+      u32x4 a[AC], b[BC];
+      uint32_t sc[BC];
+    };
+    // Loads of iteration it are unconditional: activations past m read
+    // zeros, codes past the row read bytes whose scale is forced to 0 below,
+    // and iterations past the split's range are never stored.
+    auto load = [&](Stage &S, int it) {
+#pragma unroll
+      for (int u = 0; u < AC; ++u) {
+        const bool in = kbase + KS * it + 8 * akq[u] < m;
+        S.a[u] = bload16(xr, in ? aoff[u] + (uint32_t)(KS * it * 2) : kOutOfRange);
+      }
+#pragma unroll
+      for (int u = 0; u < BC; ++u) S.b[u] = bload16(wr, boff[u] + (uint32_t)(KS * it));
+#pragma unroll
+      for (int u = 0; u < BC; ++u) {
+        const uint32_t o = soff[u] + (uint32_t)((KS * it / G) * SB);
+        if constexpr (KIND == SCALE_F16)
+          S.sc[u] = bload2(wr, o);
+        else
+          S.sc[u] = __builtin_amdgcn_raw_buffer_load_b32(wr, o, 0, 0);
+      }
+    };
+    auto store = [&](const Stage &S, int it, int buf) {
+#pragma unroll
+      for (int u = 0; u < AC; ++u)
+        *reinterpret_cast<u32x4 *>(&As[buf][arow[u] * LDS_ROW + 8 * akq[u]]) = S.a[u];
+#pragma unroll
+      for (int u = 0; u < BC; ++u) {
+        _Float16 hs;
+        if constexpr (KIND == SCALE_F16)
+          hs = __builtin_bit_cast(_Float16, (uint16_t)S.sc[u]);
+        else
+          hs = (_Float16)__builtin_ldexpf(__builtin_bit_cast(float, S.sc[u]), -ews[brow[u]]);
+        const _Float16 h0 = (_Float16)0.0f;
+        hs = kbase + KS * it + 16 * bkc[u] < m ? hs : h0;
+        const f16x2 s2 = {hs, hs};
+        _Float16 *dst = &Bs[buf][brow[u] * LDS_ROW + 16 * bkc[u]];
+        *reinterpret_cast<f16x8 *>(dst) = dequant8(S.b[u].x, S.b[u].y, s2);
+        *reinterpret_cast<f16x8 *>(dst + 8) = dequant8(S.b[u].z, S.b[u].w, s2);
+      }
+    };
+    // PD register stages: stage u % PD holds iteration u, loaded PD
+    // iterations before its store
+    Stage S[PD];
+#pragma unroll
+    for (int u = 0; u < PD; ++u) load(S[u], u);
+    store(S[0], 0, 0);
+    load(S[0], PD);
+    __syncthreads();
+    // iteration it: the consumers read LDS stage it & 1; write stage
+    // (it + 1) & 1 (read last in iteration it - 1) from registers, which then
+    // load iteration it + 1 + PD
+    for (int it0 = 0; it0 < nit; it0 += PD) {
+#pragma unroll
+      for (int u = 0; u < PD; ++u) {
+        const int it = it0 + u;
+        if (it >= nit) break;
+        if (it + 1 < nit) store(S[(u + 1) % PD], it + 1, (it + 1) & 1);
+        load(S[(u + 1) % PD], it + 1 + PD);
+        __syncthreads();
+      }
+    }
+    return;
   }
-  auto load_a = [&](u32x4 *dst, int it) {
-#pragma unroll
-    for (int u = 0; u < AU; ++u) {
-      const uint32_t off = KT * it + akc[u] < mk ? vx[u] + KT * it * 2 : kOutOfRange;
-      dst[u] = bload16(xr, off);
-    }
-  };
-  auto store_a = [&](const u32x4 *src, int buf) {
-#pragma unroll
-    for (int u = 0; u < AU; ++u) {
-      const int row = (tid + NT * u) / (KT / 8);
-      *reinterpret_cast<u32x4 *>(&As[buf][row * LDA + akc[u]]) = src[u];
-    }
-  };
-  // activation column of k-step ks (same permutation as the codes)
-  auto acol = [&](int h, int ks) {
-    return 64 * h + (G == 64 ? 32 * lh + 8 * ks : 32 * (ks >> 1) + 16 * lh + 8 * (ks & 1));
-  };
 
-  if (tid < BM) exs[tid] = tid < arows ? ex[m0 + tid] : 0;
-  // this lane's weight-row exponents (f32 scales) per column tile
-  int ewc[TN];
-#pragma unroll
-  for (int t = 0; t < TN; ++t)
-    ewc[t] = KIND == SCALE_F32 && n0 + bcol(t) < n ? ew[n0 + bcol(t)] : 0;
-
+  // ---- consumers ----
+  const int lr = lane & 31, lh = lane >> 5;
+  const int cb = wid * 32 * TN;                  // this wave's first column in the tile
   f32x16 acc[TM][TN];
 #pragma unroll
   for (int i = 0; i < TM; ++i)
@@ -344,126 +355,44 @@ void gemm_kernel(const uint8_t *__restrict__ w, int64_t row_bytes,
     for (int t = 0; t < TN; ++t)
 #pragma unroll
       for (int v = 0; v < 16; ++v) acc[i][t][v] = 0.0f;
-
-  // Every iteration stages the tiles of the next one; loads past the split's
-  // K range read zeros or bytes that are never used, so none of them sits in
-  // a branch (a load in a branch makes the wave wait for all its loads).
-  u32x4 ra[AU], rc[CU];
-  uint32_t rs[SU];
-  load_scales(rs, 0);
-  load_codes(rc, 0);
-  load_a(ra, 0);
-  store_scales(rs, 0);
-  store_codes(rc, 0);
-  store_a(ra, 0);
-  load_scales(rs, 1);
-  load_codes(rc, 1);
-  load_a(ra, 1);
   __syncthreads();
-
-  const f16x2 zero2 = {(_Float16)0.0f, (_Float16)0.0f};
   for (int it = 0; it < nit; ++it) {
-    const uint8_t *bt = Bs[it & 1];
-    const uint8_t *st = Ss[it & 1];
-    const uint16_t *at = As[it & 1];
+    const _Float16 *at = As[it & 1];
+    const _Float16 *bt = Bs[it & 1];
 #pragma unroll
-    for (int hh = 0; hh < 2 / NP; ++hh) {
-      const int h = h0 + hh;
-      // the slot's codes and scales for each column tile; a slot (or its
-      // second G=32 group) past the row end meets zero activations and its
-      // scales (whatever bytes were read) are forced to 0
-      const int64_t k0 = kbase + KT * it + 64 * h;
-      u32x4 cq[TN][2];
-      f16x2 s2[TN][NG];
+    for (int ks = 0; ks < KS / 16; ++ks) {
+      // v_mfma_f32_32x32x16_f16 operands: lane (lr, lh) holds row / column lr,
+      // k = 16 ks + 8 lh .. +8 of this tile, for both A and B
+      f16x8 af[TM], bf[TN];
 #pragma unroll
-      for (int t = 0; t < TN; ++t) {
-        const int r = bcol(t);
-        const int sw = (r >> 1) & 7;
-        cq[t][0] = *reinterpret_cast<const u32x4 *>(bt + r * KT + 16 * ((4 * h + (chunk0 >> 4)) ^ sw));
-        cq[t][1] = *reinterpret_cast<const u32x4 *>(bt + r * KT + 16 * ((4 * h + (chunk1 >> 4)) ^ sw));
-        const uint8_t *sp = st + r * SPB + h * NG * SB;
+      for (int i = 0; i < TM; ++i)
+        af[i] = *reinterpret_cast<const f16x8 *>(&at[(i * 32 + lr) * LDS_ROW + 16 * ks + 8 * lh]);
 #pragma unroll
-        for (int g = 0; g < NG; ++g) {
-          _Float16 hs;
-          if constexpr (KIND == SCALE_F16)
-            hs = *reinterpret_cast<const _Float16 *>(sp + 2 * g);
-          else
-            hs = (_Float16)__builtin_ldexpf(*reinterpret_cast<const float *>(sp + 4 * g), -ewc[t]);
-          s2[t][g] = k0 + g * G < m ? f16x2{hs, hs} : zero2;
-        }
-      }
-      // The slot's MFMA work runs at raised wave priority: of the SIMD's two
-      // waves the one in its MFMA phase issues first, the other stages and
-      // dequantizes meanwhile.
-      __builtin_amdgcn_s_setprio(1);
-      // A fragments of k-step ks + 1 are read while k-step ks runs
-      f16x8 af[2][TM];
+      for (int t = 0; t < TN; ++t)
+        bf[t] = *reinterpret_cast<const f16x8 *>(&bt[(cb + t * 32 + lr) * LDS_ROW + 16 * ks + 8 * lh]);
 #pragma unroll
-      for (int ii = 0; ii < TM; ++ii)
-        af[0][ii] = *reinterpret_cast<const f16x8 *>(&at[(ii * 32 + lr) * LDA + acol(h, 0)]);
+      for (int i = 0; i < TM; ++i)
 #pragma unroll
-      for (int ks = 0; ks < 4; ++ks) {
-        if (ks < 3) {
-#pragma unroll
-          for (int ii = 0; ii < TM; ++ii)
-            af[(ks + 1) & 1][ii] =
-                *reinterpret_cast<const f16x8 *>(&at[(ii * 32 + lr) * LDA + acol(h, ks + 1)]);
-        }
-        const int g = G == 64 ? 0 : ks >> 1;
-        f16x8 bq[TN];
-#pragma unroll
-        for (int t = 0; t < TN; ++t) {
-          const u32x4 &c = cq[t][ks >> 1];
-          bq[t] = (ks & 1) ? dequant8(c.z, c.w, s2[t][g]) : dequant8(c.x, c.y, s2[t][g]);
-        }
-#pragma unroll
-        for (int ii = 0; ii < TM; ++ii)
-#pragma unroll
-          for (int t = 0; t < TN; ++t)
-            acc[ii][t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[ks & 1][ii], bq[t], acc[ii][t], 0, 0, 0);
-      }
-      __builtin_amdgcn_s_setprio(0);
+        for (int t = 0; t < TN; ++t)
+          acc[i][t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bf[t], acc[i][t], 0, 0, 0);
     }
-    // stage the tiles of iteration it + 1, then load those of it + 2
-    store_scales(rs, (it + 1) & 1);
-    store_codes(rc, (it + 1) & 1);
-    store_a(ra, (it + 1) & 1);
     __syncthreads();
-    load_scales(rs, it + 2);
-    load_codes(rc, it + 2);
-    load_a(ra, it + 2);
   }
-
-  // With two K parities, each column tile's parities meet in LDS (reusing
-  // As), one column tile at a time; each output is scaled by 2^(e_i + f_j).
-  float *red = reinterpret_cast<float *>(&As[0][0]);   // 4 * TM * 16 * 64 floats
-  static_assert(4 * TM * 16 * 64 * 4 <= (int)sizeof(As), "reduction buffer too small");
+  // D layout of v_mfma_f32_32x32x16: lane -> column lane % 32, element v ->
+  // row 8 (v / 4) + 4 (lane / 32) + v % 4; each output scaled by 2^(e_i + f_j)
   const int rows_left = (int)(s - m0 - lh * 4);
 #pragma unroll
   for (int t = 0; t < TN; ++t) {
-    if constexpr (NP == 2) {
-      __syncthreads();
-      if (h0 == 1) {
-#pragma unroll
-        for (int i = 0; i < TM; ++i)
-#pragma unroll
-          for (int v = 0; v < 16; ++v) red[((p * TM + i) * 16 + v) * 64 + lane] = acc[i][t][v];
-      }
-      __syncthreads();
-    }
-    const int64_t col = n0 + bcol(t);
-    if (h0 == 0 && col < n) {
-      // D layout of v_mfma_f32_32x32x16: lane -> column lane % 32,
-      // element v -> row 8 (v / 4) + 4 (lane / 32) + v % 4.
+    const int jc = cb + t * 32 + lr;
+    const int64_t col = n0 + jc;
+    if (col < n) {
       float *out = (gridDim.z == 1 ? y : ws + (int64_t)blockIdx.z * s * n) + (m0 + lh * 4) * n + col;
 #pragma unroll
       for (int i = 0; i < TM; ++i)
 #pragma unroll
         for (int v = 0; v < 16; ++v) {
           const int r = i * 32 + (v >> 2) * 8 + (v & 3);
-          float o = acc[i][t][v];
-          if constexpr (NP == 2) o += red[((p * TM + i) * 16 + v) * 64 + lane];
-          if (r < rows_left) out[(int64_t)r * n] = __builtin_ldexpf(o, exs[r + lh * 4] + ewc[t]);
+          if (r < rows_left) out[(int64_t)r * n] = __builtin_ldexpf(acc[i][t][v], exs[r + lh * 4] + ews[jc]);
         }
     }
   }
@@ -488,24 +417,24 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float *__restr
   }
 }
 
-template <int G, int KIND, int BM, int TN, int NW>
+template <int G, int KIND, int TM, int TN>
 hipError_t launch_t(const LinearArgs &a, const uint16_t *x16, const int *ex, const int *ew,
-                    hipStream_t st) {
-  constexpr int BN = 128 * TN;
-  const int64_t nit_all = (a.m + KT - 1) / KT;
+                       hipStream_t st) {
+  constexpr int BM = 32 * TM, BN = 128 * TN;
+  const int64_t nit_all = (a.m + KS - 1) / KS;
   const int64_t gx = (a.n + BN - 1) / BN, gy = (a.s + BM - 1) / BM;
-  // Split K when the output tiles alone leave CUs idle (256 CUs, one 8-wave
-  // workgroup each); every split keeps at least 4 iterations.
+  // Split K when the output tiles alone leave CUs idle (256 CUs, one
+  // workgroup each); every split keeps at least 8 iterations.
   int64_t splits = 1;
   if (a.ws) {
-    while (gx * gy * splits * 2 <= 256 && (nit_all + 2 * splits - 1) / (2 * splits) >= 4 &&
+    while (gx * gy * splits * 2 <= 256 && (nit_all + 2 * splits - 1) / (2 * splits) >= 8 &&
            2 * splits * a.s * a.n <= a.ws_floats)
       splits *= 2;
   }
   int64_t nit = (nit_all + splits - 1) / splits;
-  dim3 grid((unsigned)gx, (unsigned)gy, (unsigned)splits), block(64 * NW);
-  hipLaunchKernelGGL((gemm_kernel<G, KIND, BM, TN, NW>), grid, block, 0, st, a.w, a.row_bytes, x16,
-                     ex, ew, a.y, a.s, a.m, a.n, (int)nit, a.ws);
+  dim3 grid((unsigned)gx, (unsigned)gy, (unsigned)splits), block(64 * (4 + kProducerWaves));
+  hipLaunchKernelGGL((gemm_kernel<G, KIND, TM, TN>), grid, block, 0, st, a.w, a.row_bytes,
+                     x16, ex, ew, a.y, a.s, a.m, a.n, (int)nit, a.ws);
   if (splits > 1) return launch_splitk_reduce(a.ws, a.y, a.s * a.n, (int)splits, st);
   return hipGetLastError();
 }
@@ -520,14 +449,14 @@ hipError_t launch_g(const LinearArgs &a, uint16_t *x16, int *ex, int *ew, bool w
     launch_act16<false, G>(a, x16, ex, ew, nw, st);
   else
     launch_act16<true, G>(a, x16, ex, ew, nw, st);
-  // 128-row tiles once the rows fill them; two column tiles per wave when
-  // the 256-column tiles still give every CU a workgroup.
+  // 128-row tiles once the rows fill them; two column tiles per consumer
+  // wave when the 256-column tiles still give every CU a workgroup.
   if (a.s > 64) {
     const int64_t tiles256 = (a.n + 255) / 256 * ((a.s + 127) / 128);
-    if (tiles256 >= 256) return launch_t<G, KIND, 128, 2, kWaves>(a, x16, ex, ew, st);
-    return launch_t<G, KIND, 128, 1, kWaves>(a, x16, ex, ew, st);
+    if (tiles256 >= 256) return launch_t<G, KIND, 4, 2>(a, x16, ex, ew, st);
+    return launch_t<G, KIND, 4, 1>(a, x16, ex, ew, st);
   }
-  return launch_t<G, KIND, 64, 1, kWaves>(a, x16, ex, ew, st);
+  return launch_t<G, KIND, 2, 1>(a, x16, ex, ew, st);
 }
 
 }  // namespace
