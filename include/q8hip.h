@@ -145,14 +145,14 @@ int q8_linear_bf16act(q8_ctx *ctx, q8_buf *w, uint64_t owt_u16, q8_buf *x,
  * device.  w points at packed row 0 (rows back to back); x and y are f32
  * and must not overlap.
  * Scratch: one fixed array of Q8_NOALLOC_SCRATCH_BYTES per GPU, held until
- * the process ends (split-K partials, arrival counters, and a 16 MiB
- * binary16 activation buffer for s >= 32, which takes the rows in chunks).
+ * the process ends (16 MiB of split-K partials and a 16 MiB binary16
+ * activation buffer for s >= 32, which takes the rows in chunks).
  * Limit: from s = 32 on, one activation row (2 m + 4 bytes) plus 4 n bytes
  * must fit in 16 MiB, else Q8_ERR_SHAPE.  Every call on a GPU shares that
  * GPU's array: calls that overlap on one GPU (two streams, two threads)
  * race; calls in one stream's order do not.  Errors: status code, message in
  * q8_last_error(NULL) on the calling thread. */
-#define Q8_NOALLOC_SCRATCH_BYTES (33816576LL)   /* 16 MiB + 256 KiB + 16 MiB */
+#define Q8_NOALLOC_SCRATCH_BYTES (33554432LL)   /* 16 MiB + 16 MiB */
 int q8_linear_noalloc(void *hip_stream, const void *w, const float *x, float *y, int64_t s,
                       int64_t m, int64_t n, int G, int scale_dtype);
 

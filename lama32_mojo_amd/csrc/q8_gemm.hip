@@ -399,6 +399,8 @@ void gemm_kernel(const uint8_t *__restrict__ w, int64_t row_bytes,
 }
 
 // y[i] = sum over splits z (in order) of ws[z][i]; four outputs per thread.
+// The loads of up to 8 splits are issued before their adds, so a thread
+// waits for one memory round trip per 8 splits rather than one per split.
 __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float *__restrict__ ws,
                                                             float *__restrict__ y, int64_t count,
                                                             int splits) {
@@ -406,7 +408,24 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float *__restr
   if (i >= count) return;
   if (i + 4 <= count && (count & 3) == 0) {
     f32x4 v = *reinterpret_cast<const f32x4 *>(ws + i);
-    for (int z = 1; z < splits; ++z) v += *reinterpret_cast<const f32x4 *>(ws + z * count + i);
+    int z = 1;
+    for (; z + 8 <= splits; z += 8) {
+      f32x4 t[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) t[u] = *reinterpret_cast<const f32x4 *>(ws + (z + u) * count + i);
+#pragma unroll
+      for (int u = 0; u < 8; ++u) v += t[u];
+    }
+    // the last splits mod 8: unconditional loads (an index past the last
+    // split rereads it) so they too are issued together
+    f32x4 t[7];
+#pragma unroll
+    for (int u = 0; u < 7; ++u) {
+      const int zz = z + u < splits ? z + u : splits - 1;
+      t[u] = *reinterpret_cast<const f32x4 *>(ws + zz * count + i);
+    }
+#pragma unroll
+    for (int u = 0; u < 7; ++u) v = z + u < splits ? v + t[u] : v;
     *reinterpret_cast<f32x4 *>(y + i) = v;
   } else {
     for (int64_t e = i; e < i + 4 && e < count; ++e) {

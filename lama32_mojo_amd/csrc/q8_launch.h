@@ -33,10 +33,6 @@ struct LinearArgs {
   // partial sums.
   float *ws = nullptr;
   int64_t ws_floats = 0;
-  // Arrival counters for K splits across workgroups (small-batch kernels):
-  // cnt_n ints, zero between calls.
-  int *cnt = nullptr;
-  int64_t cnt_n = 0;
 };
 // Decode path (s small, f32 x): VALU GEMV.
 hipError_t launch_gemv(const LinearArgs &a, hipStream_t st);

@@ -43,17 +43,6 @@ namespace {
 template <int G, int KIND> struct SkinnyScale {
   static constexpr int bytes = (64 / G) * ScaleTraits<KIND>::bytes;
   uint32_t wd[bytes >= 4 ? bytes / 4 : 1];
-  __device__ __forceinline__ void load(rsrc_t r, uint32_t off) {
-    if constexpr (bytes == 8) {
-      const u32x2 v = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, 0));
-      wd[0] = v.x;
-      wd[1] = v.y;
-    } else if constexpr (bytes == 4) {
-      wd[0] = __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0);
-    } else {
-      wd[0] = __builtin_amdgcn_raw_buffer_load_b16(r, off, 0, 0);
-    }
-  }
   __device__ __forceinline__ float get(int gi) const {
     if constexpr (G == 64 && KIND == SCALE_F16) return f16_bits_to_f32((uint16_t)wd[0]);
     else if constexpr (G == 64) return __builtin_bit_cast(float, wd[0]);
@@ -308,27 +297,30 @@ __global__ __launch_bounds__(64 * KW) void skinny_kernel(const uint8_t *__restri
 // in k-step ks lane (c, q) takes codes and x at k = 32 ks + 8 q .. +8 of
 // weight row c and batch row c.  A k-step lies in one scale group; its
 // partial is folded into the output with the lane's scale (G = 64: every
-// two k-steps).  Rows are padded in LDS (x by 8 bf16, codes by 16 bytes) so
-// the ds_read passes are conflict-free.  No K ranges meet: each wave's
-// accumulators are its outputs.
+// two k-steps).  Rows are padded in LDS (x by 16 bf16, codes by 16 bytes)
+// and the codes are kept in k-step pair order, so every ds_read is a
+// conflict-free 16-byte access.  No K ranges meet: each wave's accumulators
+// are its outputs.
 constexpr int kXSlab = 256;                // codes of a row per slab
-constexpr int kXbRow = kXSlab + 8;         // LDS bf16 per staged x row
+constexpr int kXbRow = kXSlab + 16;        // LDS bf16 per staged x row
 constexpr int kCbRow = kXSlab + 16;        // LDS bytes per staged code row
+constexpr int kXStages = 2;                // slabs held in registers per wave
+// waves per SIMD the register allocation must allow: three 4-wave
+// workgroups per CU (their LDS, 53 KiB each, fits three times)
+template <int KW> constexpr int kXWavesPerSimd = KW == 4 ? 3 : 1;
 
-// Narrow matrices split K over KS workgroups per row block (slabs
-// [k spk, (k + 1) spk) for workgroup k): each writes its partial tile to ws
-// with device-scope stores, waits for them and counts itself in cnt[row
-// block]; the last to arrive adds the KS partials in order 0 .. KS-1 (so
-// the result does not depend on arrival order), stores y and resets the
-// counter.  No workgroup waits for another.
-template <int G, int KIND, int TR, int NC, int KW>
-__global__ __launch_bounds__(64 * KW) void skinny_x_kernel(const uint8_t *__restrict__ w,
+// Narrow matrices split K over ks_n workgroups per row block (slabs
+// [k spk, (k + 1) spk) for workgroup k): each writes its partial outputs to
+// slice k of ws, and a second kernel adds the ks_n slices in order 0 ..
+// ks_n - 1 (so the result does not depend on which workgroup ends first).
+template <int G, int KIND, int TR, int NC, int KW, int PD>
+__global__ __launch_bounds__(64 * KW) __attribute__((amdgpu_waves_per_eu(kXWavesPerSimd<KW>)))
+void skinny_x_kernel(const uint8_t *__restrict__ w,
                                                            int64_t row_bytes,
                                                            const float *__restrict__ x,
                                                            float *__restrict__ y, int s, int m,
                                                            int64_t n, int nslab, int ks_n,
-                                                           int spk, float *__restrict__ ws,
-                                                           int *__restrict__ cnt) {
+                                                           int spk, float *__restrict__ ws) {
   constexpr int SB = ScaleTraits<KIND>::bytes;
   constexpr int XR = 16 * TR;                  // staged x rows
   static_assert(XR % KW == 0, "x rows split evenly over the waves");
@@ -337,12 +329,12 @@ __global__ __launch_bounds__(64 * KW) void skinny_x_kernel(const uint8_t *__rest
   constexpr int NDW = NC * 16 * SPS / 4;       // scale dwords of a wave per slab
   constexpr int NL = (NDW + 63) / 64;
   constexpr int KPG = G / 32;                  // k-steps per scale group
+  static_assert(PD >= 2 && PD % 2 == 0, "register stages pair with the two x buffers");
   __shared__ __attribute__((aligned(16))) uint16_t xh[2][XR][kXbRow];
   __shared__ __attribute__((aligned(16))) uint16_t xl[2][XR][kXbRow];
   __shared__ __attribute__((aligned(16))) uint8_t cs[KW][NC * 16][kCbRow];
   __shared__ uint32_t ss[KW][NDW];
 
-  constexpr int ROWS = 16 * NC * KW;           // weight rows of a workgroup
   const int lane = threadIdx.x & 63;
   const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int c = lane & 15, q = lane >> 4;
@@ -378,19 +370,22 @@ __global__ __launch_bounds__(64 * KW) void skinny_x_kernel(const uint8_t *__rest
     u32x4 cq[NC][4];
     uint32_t sw[NL];
   };
-  auto load_codes = [&](Slab &sl, int slab) {
+  // ok == false (uniform): the loads go to an empty buffer and read nothing
+  const rsrc_t none = make_rsrc(w, 0u);
+  auto load_codes = [&](Slab &sl, int slab, bool ok) {
+    const rsrc_t r = ok ? wr : none;
 #pragma unroll
     for (int t = 0; t < NC; ++t)
 #pragma unroll
-      for (int u = 0; u < 4; ++u) sl.cq[t][u] = bload16(wr, co[t][u] + slab * kXSlab);
+      for (int u = 0; u < 4; ++u) sl.cq[t][u] = bload16(r, co[t][u] + slab * kXSlab);
 #pragma unroll
     for (int j = 0; j < NL; ++j)
-      sl.sw[j] = __builtin_amdgcn_raw_buffer_load_b32(wr, so[j] + (uint32_t)(slab * SPS), 0, 0);
+      sl.sw[j] = __builtin_amdgcn_raw_buffer_load_b32(r, so[j] + (uint32_t)(slab * SPS), 0, 0);
   };
-  auto load_x = [&](u32x4 (&xg)[XPW], int slab) {
+  auto load_x = [&](u32x4 (&xg)[XPW], int slab, bool ok) {
     const uint32_t o = (uint32_t)(slab * kXSlab * 4) + 16 * lane;
 #pragma unroll
-    for (int u = 0; u < XPW; ++u) xg[u] = bload16(xr[u], o);
+    for (int u = 0; u < XPW; ++u) xg[u] = bload16(ok ? xr[u] : none, o);
   };
   // split this lane's 4 values of each loaded row into hi and lo bf16
   auto store_x = [&](const u32x4 (&xg)[XPW], int buf) {
@@ -414,159 +409,186 @@ __global__ __launch_bounds__(64 * KW) void skinny_x_kernel(const uint8_t *__rest
   uint8_t *cw = &cs[wid][0][0];
   uint32_t *sws = &ss[wid][0];
   auto compute = [&](const Slab &sl, int buf, int slab) {
+    // codes in k-step pair order: entry (q, ks) of a row (the 8 codes lane
+    // q feeds in k-step ks) at 64 (ks / 2) + 16 q + 8 (ks % 2), so a lane
+    // reads the codes of two k-steps with one 16-byte access; a loaded run
+    // of 16 codes (k-step ks, entries q = 2 hh and 2 hh + 1) is written as
+    // two 8-byte pieces
+    const int hq = lane & 15, kst = hq >> 1;
+    const int po = 32 * (kst & ~1) + 32 * (hq & 1) + 8 * (kst & 1);
 #pragma unroll
     for (int t = 0; t < NC; ++t)
 #pragma unroll
-      for (int u = 0; u < 4; ++u)
-        *reinterpret_cast<u32x4 *>(cw + (16 * t + 4 * u + (lane >> 4)) * kCbRow + 16 * (lane & 15)) =
-            sl.cq[t][u];
+      for (int u = 0; u < 4; ++u) {
+        uint8_t *dst = cw + (16 * t + 4 * u + (lane >> 4)) * kCbRow + po;
+        *reinterpret_cast<u32x2 *>(dst) = u32x2{sl.cq[t][u].x, sl.cq[t][u].y};
+        *reinterpret_cast<u32x2 *>(dst + 16) = u32x2{sl.cq[t][u].z, sl.cq[t][u].w};
+      }
 #pragma unroll
     for (int j = 0; j < NL; ++j)
       if (lane + 64 * j < NDW) sws[lane + 64 * j] = sl.sw[j];
+    // The slab runs in blocks of KB k-steps (4, or 2 with several tiles);
+    // the LDS reads of a block (codes and x) are issued together, one block
+    // ahead of the products that use them.  Within a block the products run as
+    // independent chains, one per scale group (hi terms of every chain
+    // first, then the lo terms), so no MFMA waits on the one issued just
+    // before it; the scale FMAs of the block's groups follow its products.
+    constexpr int NG = 8 / KPG;                // scale groups per slab
+    constexpr int KB = TR * NC > 1 ? 2 : 4;    // k-steps per block
+    constexpr int GB = KB / KPG;               // scale groups per block
+    // raw scale words of the slab's groups, read with the first block
+    uint32_t swd[NG][NC];
+    auto read_scales = [&]() {
 #pragma unroll
-    for (int g = 0; g < 8 / KPG; ++g) {
-      // scale group g of the slab (k-steps KPG g ..), forced to 0 past m
+      for (int g = 0; g < NG; ++g)
+#pragma unroll
+        for (int t = 0; t < NC; ++t) swd[g][t] = sws[((16 * t + c) * SPS + g * SB) >> 2];
+    };
+    // scale of group g of the slab (k-steps KPG g ..), forced to 0 past m
+    auto scale = [&](int g, int t) {
+      const int byte = (16 * t + c) * SPS + g * SB;
+      const uint32_t raw = KIND == SCALE_F16 ? (swd[g][t] >> (8 * (byte & 3))) & 0xffffu : swd[g][t];
       const bool live = slab * kXSlab + 32 * KPG * g < m;
-      float sc[NC];
+      return live ? (KIND == SCALE_F16 ? f16_bits_to_f32((uint16_t)raw) : __builtin_bit_cast(float, raw))
+                  : 0.0f;
+    };
+    // register sets of two blocks: block h + 1 is read before block h runs
+    u32x2 qq[2][KB][NC];
+    bf16x8_t ah[2][KB][TR], al[2][KB][TR];
+    auto read_block = [&](int h) {
+      const int r = h & 1;
 #pragma unroll
-      for (int t = 0; t < NC; ++t) {
-        const int byte = (16 * t + c) * SPS + g * SB;
-        const uint32_t wd = sws[byte >> 2];
-        const uint32_t raw = KIND == SCALE_F16 ? (wd >> (8 * (byte & 3))) & 0xffffu : wd;
-        sc[t] = live ? (KIND == SCALE_F16 ? f16_bits_to_f32((uint16_t)raw)
-                                          : __builtin_bit_cast(float, raw))
-                     : 0.0f;
-      }
-      f32x4 d[NC][TR];
-#pragma unroll
-      for (int kk = 0; kk < KPG; ++kk) {
-        const int ks = KPG * g + kk;
-        bf16x8_t ah[TR], al[TR];
-#pragma unroll
-        for (int tr = 0; tr < TR; ++tr) {
-          ah[tr] = *reinterpret_cast<const bf16x8_t *>(&xh[buf][16 * tr + c][32 * ks + 8 * q]);
-          al[tr] = *reinterpret_cast<const bf16x8_t *>(&xl[buf][16 * tr + c][32 * ks + 8 * q]);
-        }
+      for (int k = 0; k < KB; k += 2)
 #pragma unroll
         for (int t = 0; t < NC; ++t) {
-          const u32x2 qq = *reinterpret_cast<const u32x2 *>(cw + (16 * t + c) * kCbRow + 32 * ks + 8 * q);
-          const bf16x8_t bq = codes_to_bf16(qq.x, qq.y);
-#pragma unroll
-          for (int tr = 0; tr < TR; ++tr) {
-            const f32x4 z = {0.0f, 0.0f, 0.0f, 0.0f};
-            f32x4 dd = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah[tr], bq, kk == 0 ? z : d[t][tr], 0, 0, 0);
-            d[t][tr] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al[tr], bq, dd, 0, 0, 0);
-          }
+          const u32x4 v = *reinterpret_cast<const u32x4 *>(cw + (16 * t + c) * kCbRow + 32 * (KB * h + k) + 16 * q);
+          qq[r][k][t] = u32x2{v.x, v.y};
+          qq[r][k + 1][t] = u32x2{v.z, v.w};
         }
-      }
 #pragma unroll
-      for (int t = 0; t < NC; ++t)
+      for (int k = 0; k < KB; ++k)
 #pragma unroll
-        for (int tr = 0; tr < TR; ++tr)
+        for (int tr = 0; tr < TR; ++tr) {
+          ah[r][k][tr] = *reinterpret_cast<const bf16x8_t *>(&xh[buf][16 * tr + c][32 * (KB * h + k) + 8 * q]);
+          al[r][k][tr] = *reinterpret_cast<const bf16x8_t *>(&xl[buf][16 * tr + c][32 * (KB * h + k) + 8 * q]);
+        }
+    };
+    auto run_block = [&](int h) {
+      const int r = h & 1;
+      bf16x8_t bq[KB][NC];
 #pragma unroll
-          for (int v = 0; v < 4; ++v) acc[t][tr][v] = __builtin_fmaf(sc[t], d[t][tr][v], acc[t][tr][v]);
+      for (int k = 0; k < KB; ++k)
+#pragma unroll
+        for (int t = 0; t < NC; ++t) bq[k][t] = codes_to_bf16(qq[r][k][t].x, qq[r][k][t].y);
+      // k-step KB h + k is step kk = k % KPG of the block's group k / KPG;
+      // products ordered by (part, kk, group)
+      f32x4 d[GB][NC][TR];
+#pragma unroll
+      for (int part = 0; part < 2; ++part)
+#pragma unroll
+        for (int kk = 0; kk < KPG; ++kk)
+#pragma unroll
+          for (int gg = 0; gg < GB; ++gg) {
+            const int k = gg * KPG + kk;
+#pragma unroll
+            for (int t = 0; t < NC; ++t)
+#pragma unroll
+              for (int tr = 0; tr < TR; ++tr) {
+                const f32x4 z = {0.0f, 0.0f, 0.0f, 0.0f};
+                const f32x4 cin = part == 0 && kk == 0 ? z : d[gg][t][tr];
+                d[gg][t][tr] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                    part == 0 ? ah[r][k][tr] : al[r][k][tr], bq[k][t], cin, 0, 0, 0);
+              }
+          }
+#pragma unroll
+      for (int gg = 0; gg < GB; ++gg)
+#pragma unroll
+        for (int t = 0; t < NC; ++t)
+#pragma unroll
+          for (int tr = 0; tr < TR; ++tr)
+#pragma unroll
+            for (int v = 0; v < 4; ++v)
+              acc[t][tr][v] = __builtin_fmaf(scale(h * GB + gg, t), d[gg][t][tr][v], acc[t][tr][v]);
+    };
+    read_block(0);
+    read_scales();
+#pragma unroll
+    for (int h = 0; h < 8 / KB; ++h) {
+      if (h + 1 < 8 / KB) read_block(h + 1);
+      // keep the reads ahead of the block's arithmetic
+      __builtin_amdgcn_sched_barrier(0);
+      run_block(h);
     }
   };
 
-  // Slab i uses x buffer i % 2; a buffer is rewritten only after the barrier
-  // that follows every wave's last read of it; an odd last slab is skipped
-  // by a uniform branch that holds no loads.
-  Slab C0, C1;
-  u32x4 X0[XPW], X1[XPW];
-  load_codes(C0, sb);
-  load_x(X0, sb);
-  store_x(X0, 0);
-  load_codes(C1, sb + 1);
-  load_x(X1, sb + 1);
+  // Slab i is computed from register stage i % PD and x buffer i % 2.  The
+  // codes, scales and x of slab j are loaded PD slabs ahead, in the phase of
+  // slab j - PD, so PD - 1 slabs stay in flight while one is computed; x of
+  // slab i + 1 is split and stored after the compute of slab i and before
+  // the phase's barrier, so a buffer is rewritten only after the barrier
+  // that follows every wave's last read of it.  The loads are unconditional
+  // (a slab past this workgroup's range reads nothing: its offsets are out
+  // of range), and a phase past the last slab is skipped by a uniform branch
+  // that holds no loads.
+  Slab C[PD];
+  u32x4 X[PD][XPW];
+#pragma unroll
+  for (int u = 0; u < PD; ++u) {
+    load_codes(C[u], sb + u, u < ns);
+    load_x(X[u], sb + u, u < ns);
+  }
+  store_x(X[0], 0);
   __syncthreads();
-  for (int i = 0; i < ns; i += 2) {
-    compute(C0, 0, sb + i);
-    store_x(X1, 1);
-    __syncthreads();
-    load_codes(C0, sb + i + 2);
-    load_x(X0, sb + i + 2);
-    if (i + 1 < ns) compute(C1, 1, sb + i + 1);
-    store_x(X0, 0);
-    __syncthreads();
-    load_codes(C1, sb + i + 3);
-    load_x(X1, sb + i + 3);
+  for (int i0 = 0; i0 < ns; i0 += PD) {
+#pragma unroll
+    for (int u = 0; u < PD; ++u) {
+      const int i = i0 + u;
+      if (i < ns) {
+        compute(C[u], u & 1, sb + i);
+        store_x(X[(u + 1) % PD], (u + 1) & 1);
+        __syncthreads();
+      }
+      load_codes(C[u], sb + i + PD, i + PD < ns);
+      load_x(X[u], sb + i + PD, i + PD < ns);
+    }
   }
 
   // D layout of v_mfma_f32_16x16x32: lane -> weight row lane % 16, element
-  // v -> batch row 4 (lane / 16) + v
-  if (ks_n == 1) {
+  // v -> batch row 4 (lane / 16) + v.  A K split writes its partial to its
+  // own slice of ws, laid out as y.
+  float *out = ks_n == 1 ? y : ws + (int64_t)kp * s * n;
 #pragma unroll
-    for (int t = 0; t < NC; ++t) {
-      const int64_t j = j0 + 16 * t + c;
-      if (j < n) {
+  for (int t = 0; t < NC; ++t) {
+    const int64_t j = j0 + 16 * t + c;
+    if (j < n) {
 #pragma unroll
-        for (int tr = 0; tr < TR; ++tr)
+      for (int tr = 0; tr < TR; ++tr)
 #pragma unroll
-          for (int v = 0; v < 4; ++v) {
-            const int bb = 16 * tr + 4 * q + v;
-            if (bb < s) y[(int64_t)bb * n + j] = acc[t][tr][v];
-          }
-      }
+        for (int v = 0; v < 4; ++v) {
+          const int bb = 16 * tr + 4 * q + v;
+          if (bb < s) out[(int64_t)bb * n + j] = acc[t][tr][v];
+        }
     }
-    return;
   }
-  // partial tile [XR batch rows][ROWS weight rows] of this workgroup
-  constexpr int PT = XR * ROWS;
-  float *part = ws + ((int64_t)rb * ks_n + kp) * PT;
-#pragma unroll
-  for (int t = 0; t < NC; ++t)
-#pragma unroll
-    for (int tr = 0; tr < TR; ++tr)
-#pragma unroll
-      for (int v = 0; v < 4; ++v)
-        __hip_atomic_store(&part[(16 * tr + 4 * q + v) * ROWS + wid * 16 * NC + 16 * t + c],
-                           acc[t][tr][v], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  // Publication across workgroups (which may sit on different XCDs, each
-  // with its own L2): every wave waits for its partial stores, the barrier
-  // orders all waves before thread 0, and thread 0 counts the workgroup with
-  // an agent-scope release (its stores and everything before the barrier
-  // reach the agent's coherence point first).  The last workgroup to
-  // arrive takes an agent-scope acquire before it reads the partials, so
-  // the counter it saw at n - 1 orders every other workgroup's stores before
-  // its loads.
-  __builtin_amdgcn_s_waitcnt(0);
-  __shared__ int last;
-  __syncthreads();
-  if (threadIdx.x == 0)
-    last = __hip_atomic_fetch_add(&cnt[rb], 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT) ==
-           ks_n - 1;
-  __syncthreads();
-  if (!last) return;
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-  const float *p0 = ws + (int64_t)rb * ks_n * PT;
-  const int64_t r0 = (int64_t)rb * ROWS;
-  for (int o = threadIdx.x; o < PT; o += 64 * KW) {
-    float sum = 0.0f;
-    for (int k = 0; k < ks_n; ++k)
-      sum += __hip_atomic_load(&p0[(int64_t)k * PT + o], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    const int bb = o / ROWS;
-    const int64_t j = r0 + o % ROWS;
-    if (bb < s && j < n) y[(int64_t)bb * n + j] = sum;
-  }
-  if (threadIdx.x == 0) __hip_atomic_store(&cnt[rb], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // Row blocks of 16 NC KW weight rows; with ks_n > 1 each is split over
-// ks_n workgroups of spk slabs (needs a workspace and counters).
+// ks_n workgroups of spk slabs, whose partials (ks_n s n floats of the
+// workspace) are added by the split-K sum kernel.
 template <int G, int KIND, int TR, int NC, int KW>
 hipError_t launch_x(const LinearArgs &a, int ks_n, hipStream_t st) {
   constexpr int ROWS = 16 * NC * KW;
   const int64_t nrb = (a.n + ROWS - 1) / ROWS;
   const int nslab = (int)((a.m + kXSlab - 1) / kXSlab);
   if (ks_n > nslab) ks_n = nslab;
-  if (ks_n > 1 && (!a.ws || !a.cnt || nrb > a.cnt_n ||
-                   nrb * ks_n * (16 * TR) * ROWS > a.ws_floats))
-    ks_n = 1;
+  if (ks_n > 1 && (!a.ws || ks_n * a.s * a.n > a.ws_floats)) ks_n = 1;
   const int spk = (nslab + ks_n - 1) / ks_n;
   ks_n = (nslab + spk - 1) / spk;   // no empty split
-  hipLaunchKernelGGL((skinny_x_kernel<G, KIND, TR, NC, KW>), dim3((unsigned)(nrb * ks_n)),
+  constexpr int PD = kXStages;
+  hipLaunchKernelGGL((skinny_x_kernel<G, KIND, TR, NC, KW, PD>), dim3((unsigned)(nrb * ks_n)),
                      dim3(64 * KW), 0, st, a.w, a.row_bytes, static_cast<const float *>(a.x),
-                     a.y, (int)a.s, (int)a.m, a.n, nslab, ks_n, spk, a.ws, a.cnt);
+                     a.y, (int)a.s, (int)a.m, a.n, nslab, ks_n, spk, a.ws);
+  if (ks_n > 1) return launch_splitk_reduce(a.ws, a.y, a.s * a.n, ks_n, st);
   return hipGetLastError();
 }
 
@@ -591,19 +613,26 @@ hipError_t launch_tr(const LinearArgs &a, hipStream_t st) {
   return launch_nc<G, KIND, 1, TR, 8>(a, st);
 }
 
+// Shared-x form with K split over ks_n workgroups per 64-row block, ks_n
+// chosen for about `target` workgroups in all.
+template <int G, int KIND>
+hipError_t launch_x_split(const LinearArgs &a, int64_t target, hipStream_t st) {
+  const int64_t nrb = (a.n + 63) / 64;
+  return launch_x<G, KIND, 1, 1, 4>(a, (int)((target + nrb - 1) / nrb), st);
+}
+
 template <int G, int KIND>
 hipError_t launch_g(const LinearArgs &a, hipStream_t st) {
   // Shared x where the matrix gives it enough workgroups (one 16-row tile
   // per wave, 64 rows per workgroup, from n = 16384; with two row tiles,
-  // 256 rows per 8-wave workgroup, vocabulary-sized matrices only), or where
-  // long rows let K be split over workgroups.
+  // 256 rows per 8-wave workgroup, vocabulary-sized matrices only), or with
+  // K split over workgroups: long rows (about 512 workgroups) and, from 9
+  // batch rows on, narrower matrices (about 768), where the K split over the
+  // waves of the per-wave-x form reads x too often.
   if (a.s <= 16) {
     if (a.n >= 16384) return launch_x<G, KIND, 1, 1, 4>(a, 1, st);
-    // long rows: K split over workgroups of 64 rows, about 256 in all
-    if (a.m >= 8192) {
-      const int64_t nrb = (a.n + 63) / 64;
-      return launch_x<G, KIND, 1, 1, 4>(a, (int)((256 + nrb - 1) / nrb), st);
-    }
+    if (a.m >= 8192) return launch_x_split<G, KIND>(a, 512, st);
+    if (a.s > 8) return launch_x_split<G, KIND>(a, 768, st);
     return launch_tr<G, KIND, 1>(a, st);
   }
   if (a.n >= 65536) return launch_x<G, KIND, 2, 2, 8>(a, 1, st);

@@ -68,6 +68,7 @@ __device__ __forceinline__ float x_f32(const u32x4 (&xv)[4]) {
 
 constexpr int DC = 2;   // slabs of codes and scales held in registers
 constexpr int DX = 2;   // slabs of x held in registers
+constexpr int kXStages = 2;   // slabs held in registers per wave, shared-x form
 
 // Scales of one slab: 4Q rows x SPS bytes (SPS = 256 / G scales), loaded as
 // NDW dwords, lane l taking dwords l, l + 64, ... (rows in order, so a load
@@ -290,7 +291,7 @@ __global__ __launch_bounds__(64 * KW) void skinny4_kernel(const uint8_t *__restr
 // LDS region, with one barrier per slab; a workgroup then reads x once per
 // 4 Q KW weight rows instead of once per 4 Q.  Codes and scales go through
 // the wave's own LDS region as in skinny4_kernel, and no K ranges meet.
-template <int G, int KIND, int TR, int Q, int KW>
+template <int G, int KIND, int TR, int Q, int KW, int PD>
 __global__ __launch_bounds__(64 * KW) void skinny4x_kernel(const uint8_t *__restrict__ w,
                                                            int64_t row_bytes,
                                                            const float *__restrict__ x,
@@ -299,6 +300,7 @@ __global__ __launch_bounds__(64 * KW) void skinny4x_kernel(const uint8_t *__rest
   constexpr int SB = ScaleTraits<KIND>::bytes;
   constexpr int XR = 4 * TR;                 // staged x rows
   constexpr int XPW = (XR + KW - 1) / KW;    // x rows each wave loads
+  static_assert(PD >= 2 && PD % 2 == 0, "register stages pair with the two x buffers");
   typedef SlabScales<G, KIND, Q> SS;
   __shared__ __attribute__((aligned(16))) float xs[2][XR][kXRow];
   __shared__ uint32_t ss[KW][SS::NDW];
@@ -330,18 +332,21 @@ __global__ __launch_bounds__(64 * KW) void skinny4x_kernel(const uint8_t *__rest
     so[j] = i < SS::NDW ? (uint32_t)(row * row_bytes) + 4 * (i % (SS::SPS / 4)) : kOutOfRange;
   }
 
-  auto load_codes = [&](CodeSlab<Q, SS::NL> &sl, int slab) {
+  // ok == false (uniform): the loads go to an empty buffer and read nothing
+  const rsrc_t none = make_rsrc(w, 0u);
+  auto load_codes = [&](CodeSlab<Q, SS::NL> &sl, int slab, bool ok) {
+    const rsrc_t r = ok ? wr : none;
     const int k0 = slab * kSlab;
 #pragma unroll
-    for (int q = 0; q < Q; ++q) sl.cq[q] = bload16(wr, co[q] + k0);
+    for (int q = 0; q < Q; ++q) sl.cq[q] = bload16(r, co[q] + k0);
 #pragma unroll
     for (int j = 0; j < SS::NL; ++j)
-      sl.sw[j] = __builtin_amdgcn_raw_buffer_load_b32(wr, so[j] + (uint32_t)(slab * SS::SPS), 0, 0);
+      sl.sw[j] = __builtin_amdgcn_raw_buffer_load_b32(r, so[j] + (uint32_t)(slab * SS::SPS), 0, 0);
   };
-  auto load_x = [&](u32x4 (&xg)[XPW], int slab) {
+  auto load_x = [&](u32x4 (&xg)[XPW], int slab, bool ok) {
     const uint32_t o = (uint32_t)(slab * kSlab * 4) + 16 * lane;
 #pragma unroll
-    for (int u = 0; u < XPW; ++u) xg[u] = bload16(xr[u], o);
+    for (int u = 0; u < XPW; ++u) xg[u] = bload16(ok ? xr[u] : none, o);
   };
   auto store_x = [&](const u32x4 (&xg)[XPW], int buf) {
 #pragma unroll
@@ -396,28 +401,35 @@ __global__ __launch_bounds__(64 * KW) void skinny4x_kernel(const uint8_t *__rest
     }
   };
 
-  // Slab i uses x buffer i % 2.  A buffer is rewritten only after the
-  // barrier that follows every wave's last read of it; an odd last slab is
-  // skipped by a uniform branch that holds no loads.
-  CodeSlab<Q, SS::NL> C0, C1;
-  u32x4 X0[XPW], X1[XPW];
-  load_codes(C0, 0);
-  load_x(X0, 0);
-  store_x(X0, 0);
-  load_codes(C1, 1);
-  load_x(X1, 1);
+  // Slab i is computed from register stage i % PD and x buffer i % 2.  The
+  // codes, scales and x of slab j are loaded PD slabs ahead, in the phase of
+  // slab j - PD; x of slab i + 1 is stored after the compute of slab i and
+  // before the phase's barrier, so a buffer is rewritten only after the
+  // barrier that follows every wave's last read of it.  The loads are
+  // unconditional (past the last slab their offsets are out of range and
+  // they read nothing), and a phase past the last slab is skipped by a
+  // uniform branch that holds no loads.
+  CodeSlab<Q, SS::NL> C[PD];
+  u32x4 X[PD][XPW];
+#pragma unroll
+  for (int u = 0; u < PD; ++u) {
+    load_codes(C[u], u, u < nslab);
+    load_x(X[u], u, u < nslab);
+  }
+  store_x(X[0], 0);
   __syncthreads();
-  for (int i = 0; i < nslab; i += 2) {
-    compute(C0, 0, i);
-    store_x(X1, 1);
-    __syncthreads();
-    load_codes(C0, i + 2);
-    load_x(X0, i + 2);
-    if (i + 1 < nslab) compute(C1, 1, i + 1);
-    store_x(X0, 0);
-    __syncthreads();
-    load_codes(C1, i + 3);
-    load_x(X1, i + 3);
+  for (int i0 = 0; i0 < nslab; i0 += PD) {
+#pragma unroll
+    for (int u = 0; u < PD; ++u) {
+      const int i = i0 + u;
+      if (i < nslab) {
+        compute(C[u], u & 1, i);
+        store_x(X[(u + 1) % PD], (u + 1) & 1);
+        __syncthreads();
+      }
+      load_codes(C[u], i + PD, i + PD < nslab);
+      load_x(X[u], i + PD, i + PD < nslab);
+    }
   }
 
   // Sum over the 16 blocks (two rotations within each 16-lane row, then the
@@ -493,7 +505,7 @@ template <int G, int KIND, int TR, int Q, int KW>
 hipError_t launch_x(const LinearArgs &a, hipStream_t st) {
   const int64_t blocks = (a.n + 4 * Q * KW - 1) / (4 * Q * KW);
   const int nslab = (int)((a.m + kSlab - 1) / kSlab);
-  hipLaunchKernelGGL((skinny4x_kernel<G, KIND, TR, Q, KW>), dim3((unsigned)blocks),
+  hipLaunchKernelGGL((skinny4x_kernel<G, KIND, TR, Q, KW, kXStages>), dim3((unsigned)blocks),
                      dim3(64 * KW), 0, st, a.w, a.row_bytes, static_cast<const float *>(a.x),
                      a.y, (int)a.s, (int)a.m, a.n, nslab);
   return hipGetLastError();

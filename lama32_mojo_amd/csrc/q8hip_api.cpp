@@ -32,9 +32,6 @@ struct q8_ctx {
   // The decode attention's partial records use it too: both run in stream
   // order on this context.
   float *gemm_ws = nullptr;
-  // Arrival counters of the small-batch kernels' cross-workgroup K splits
-  // (zeroed at creation; the last workgroup of a row block resets its own).
-  int *kcount = nullptr;
   // Binary16 copy of the activation rows of a prefill GEMM and their
   // power-of-two factors (launch_gemm); longer inputs run in row chunks.
   void *act16 = nullptr;
@@ -47,7 +44,6 @@ struct q8_ctx {
 namespace {
 constexpr int64_t kGemmWsFloats = (int64_t)4 << 20;
 constexpr int64_t kAct16Bytes = (int64_t)64 << 20;
-constexpr int64_t kCountInts = (int64_t)1 << 16;
 }
 
 struct q8_buf {
@@ -166,12 +162,9 @@ int q8_create(int device_ordinal, q8_ctx **out) {
     // calls captured into HIP graphs can use it too.
     if (hipMalloc(&ctx->gemm_ws, kGemmWsFloats * sizeof(float)) != hipSuccess ||
         hipMalloc(&ctx->act16, kAct16Bytes) != hipSuccess ||
-        hipMalloc(&ctx->kcount, kCountInts * sizeof(int)) != hipSuccess ||
-        hipMemset(ctx->kcount, 0, kCountInts * sizeof(int)) != hipSuccess ||
         hipDeviceSynchronize() != hipSuccess) {
       if (ctx->gemm_ws) (void)hipFree(ctx->gemm_ws);
       if (ctx->act16) (void)hipFree(ctx->act16);
-      if (ctx->kcount) (void)hipFree(ctx->kcount);
       (void)hipStreamDestroy(ctx->own);
       delete ctx;
       return fail(nullptr, Q8_ERR_NOMEM, "q8_create: cannot allocate the GEMM workspace");
@@ -192,7 +185,6 @@ void q8_destroy(q8_ctx *ctx) {
     }
     if (ctx->gemm_ws) (void)hipFree(ctx->gemm_ws);
     if (ctx->act16) (void)hipFree(ctx->act16);
-    if (ctx->kcount) (void)hipFree(ctx->kcount);
     if (ctx->stage) (void)hipHostFree(ctx->stage);
     for (hipEvent_t &ev : ctx->stage_ev)
       if (ev) (void)hipEventDestroy(ev);
@@ -433,12 +425,10 @@ bool gemm_aligned(const q8::LinearArgs &a) {
 constexpr int64_t kSkinnyMinRows = 2;
 constexpr int64_t kGemmMinRows = 32;
 
-// Attach the context's split-K workspace and arrival counters to a launch.
+// Attach the context's split-K workspace to a launch.
 void attach_gemm_workspace(q8_ctx *ctx, q8::LinearArgs &la) {
   la.ws = ctx->gemm_ws;
   la.ws_floats = kGemmWsFloats;
-  la.cnt = ctx->kcount;
-  la.cnt_n = kCountInts;
 }
 
 // Layout of a GEMM activation buffer of `bytes`: the weight-row exponents
@@ -483,13 +473,10 @@ hipError_t run_gemm(q8_ctx *ctx, q8::LinearArgs la) {
 }
 
 // Device memory a W8A32 linear may use besides its inputs and outputs: the
-// split-K partial sums, the small-batch arrival counters (zero between
-// calls) and the GEMM's binary16 activation buffer.
+// split-K partial sums and the GEMM's binary16 activation buffer.
 struct Scratch {
   float *ws;
   int64_t ws_floats;
-  int *cnt;
-  int64_t cnt_n;
   void *act16;
   int64_t act_bytes;
 };
@@ -500,8 +487,6 @@ struct Scratch {
 hipError_t dispatch_linear(q8::LinearArgs la, const Scratch &sc, hipStream_t st) {
   la.ws = sc.ws;
   la.ws_floats = sc.ws_floats;
-  la.cnt = sc.cnt;
-  la.cnt_n = sc.cnt_n;
   if (la.s >= kGemmMinRows && gemm_aligned(la)) return run_gemm_in(la, sc.act16, sc.act_bytes, st);
   if (la.s >= kSkinnyMinRows && la.s <= q8::kSkinny4MaxRows && gemm_aligned(la))
     return q8::launch_skinny4(la, st);
@@ -510,7 +495,7 @@ hipError_t dispatch_linear(q8::LinearArgs la, const Scratch &sc, hipStream_t st)
 }
 
 Scratch ctx_scratch(q8_ctx *ctx) {
-  return Scratch{ctx->gemm_ws, kGemmWsFloats, ctx->kcount, kCountInts, ctx->act16, kAct16Bytes};
+  return Scratch{ctx->gemm_ws, kGemmWsFloats, ctx->act16, kAct16Bytes};
 }
 
 }  // namespace
@@ -599,19 +584,17 @@ int q8_linear_bf16act(q8_ctx *ctx, q8_buf *w, uint64_t owt_u16, q8_buf *x, uint6
 // ---- allocation-free linear -----------------------------------------------------
 //
 // q8_linear_noalloc keeps its scratch in one fixed device array per GPU
-// instead of a context's workspace: 16 MiB of split-K partial sums and 256
-// KiB of arrival counters (the sizes of a context's, so it makes the same
-// split decisions as q8_linear), then the GEMM's 16 MiB binary16
-// activation buffer.  The array's name is a host-side stand-in: host code
+// instead of a context's workspace: 16 MiB of split-K partial sums (the size
+// of a context's, so it makes the same split decisions as q8_linear), then
+// the GEMM's 16 MiB binary16 activation buffer.  The array's name is a host-side stand-in: host code
 // only ever passes the address hipGetSymbolAddress returns for the current
 // device (noalloc_scratch).
 
 namespace {
 constexpr int64_t kNoAllocWsFloats = kGemmWsFloats;
-constexpr int64_t kNoAllocCountInts = kCountInts;
 constexpr int64_t kNoAllocAct16Bytes = (int64_t)16 << 20;
 constexpr int64_t kNoAllocBytes =
-    kNoAllocWsFloats * 4 + kNoAllocCountInts * 4 + kNoAllocAct16Bytes;
+    kNoAllocWsFloats * 4 + kNoAllocAct16Bytes;
 static_assert(kNoAllocBytes == Q8_NOALLOC_SCRATCH_BYTES, "scratch size differs from the header");
 }  // namespace
 
@@ -619,21 +602,14 @@ static __device__ __align__(256) unsigned char scratch[kNoAllocBytes];
 
 namespace {
 
-__global__ void zero_ints_kernel(int *p, int64_t n) {
-  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
-       i += (int64_t)gridDim.x * blockDim.x)
-    p[i] = 0;
-}
-
 constexpr int kNoAllocMaxDevices = 64;
 std::mutex g_noalloc_mu;
 void *g_noalloc_ptr[kNoAllocMaxDevices];   // scratch's device address per device
 
 // Set-up, once per device (the first call on it), with that device current:
-// resolve this device's copy of `scratch` and clear its arrival counters
-// with a fill kernel on the caller's stream (the kernels that use them
-// leave them zero again, so later calls need no clear).
-int noalloc_scratch(int dev, hipStream_t st, Scratch *out) {
+// resolve this device's copy of `scratch`.  No part of it needs clearing:
+// every kernel writes the partials and activation rows it reads back.
+int noalloc_scratch(int dev, Scratch *out) {
   std::lock_guard<std::mutex> lock(g_noalloc_mu);
   void *base = g_noalloc_ptr[dev];
   if (!base) {
@@ -641,18 +617,12 @@ int noalloc_scratch(int dev, hipStream_t st, Scratch *out) {
     if (e != hipSuccess || !base)
       return hip_fail(nullptr, e != hipSuccess ? e : hipErrorInvalidSymbol,
                       "q8_linear_noalloc: hipGetSymbolAddress(scratch)");
-    int *cnt = reinterpret_cast<int *>(static_cast<uint8_t *>(base) + kNoAllocWsFloats * 4);
-    hipLaunchKernelGGL(zero_ints_kernel, dim3(64), dim3(256), 0, st, cnt, kNoAllocCountInts);
-    e = hipGetLastError();
-    if (e != hipSuccess) return hip_fail(nullptr, e, "q8_linear_noalloc: counter clear");
     g_noalloc_ptr[dev] = base;
   }
   uint8_t *b = static_cast<uint8_t *>(base);
   out->ws = reinterpret_cast<float *>(b);
   out->ws_floats = kNoAllocWsFloats;
-  out->cnt = reinterpret_cast<int *>(b + kNoAllocWsFloats * 4);
-  out->cnt_n = kNoAllocCountInts;
-  out->act16 = b + kNoAllocWsFloats * 4 + kNoAllocCountInts * 4;
+  out->act16 = b + kNoAllocWsFloats * 4;
   out->act_bytes = kNoAllocAct16Bytes;
   return Q8_OK;
 }
@@ -696,7 +666,7 @@ int q8_linear_noalloc(void *hip_stream, const void *w, const float *x, float *y,
                   "device is %d", what, sdev, dev);
   }
   Scratch sc;
-  if (int rc = noalloc_scratch(dev, st, &sc)) return rc;
+  if (int rc = noalloc_scratch(dev, &sc)) return rc;
   q8::LinearArgs la;
   la.w = static_cast<const uint8_t *>(w);
   la.row_bytes = rowstride_u16(m, G, scale_dtype) * 2;

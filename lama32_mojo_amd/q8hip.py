@@ -327,7 +327,7 @@ def linear_bf16act(ctx: Context, w: Buffer, owt_u16: int, x: Buffer, ox_bf16: in
                                          scale_code(scale)))
 
 
-NOALLOC_SCRATCH_BYTES = 33816576
+NOALLOC_SCRATCH_BYTES = 33554432
 
 
 def linear_noalloc(hip_stream: int | None, w_ptr: int, x_ptr: int, y_ptr: int, s: int, m: int,

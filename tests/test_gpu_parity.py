@@ -218,13 +218,12 @@ def test_linear_all_ones_gives_row_sums(ctx, cor, G, scale, s):
 @pytest.mark.parametrize("s,n,m", [(16, 4096, 12288), (8, 24, 12288), (6, 2000, 8192),
                                    (512, 2048, 2048), (64, 2048, 8192), (40, 24, 4096)])
 def test_split_k_across_workgroups_repeats_bitwise(ctx, cor, s, n, m):
-    """Long rows at 5..16 activation rows split K over workgroups whose
-    partials the last to arrive adds in a fixed order, and GEMMs whose
-    output tiles alone leave CUs idle (512x2048x2048: 4 K splits;
-    64x2048x8192: 16; 40x24x4096: 8 splits of one ragged tile) split K with
-    a reduce launch: repeated calls give the same bits (the arrival counters
-    reset themselves) and match the closed form (1e-5 on the f32 paths, 1e-3
-    through binary16 weights)."""
+    """Long rows at 5..16 activation rows split K over workgroups, and GEMMs
+    whose output tiles alone leave CUs idle (512x2048x2048: 4 K splits;
+    64x2048x8192: 16; 40x24x4096: 8 splits of one ragged tile) split K too;
+    both add the partials in a fixed order in a reduce launch: repeated
+    calls give the same bits and match the closed form (1e-5 on the f32
+    paths, 1e-3 through binary16 weights)."""
     say("split-K repeats", s, n, m)
     G, scale = 32, "f32"
     pk = cor.pack_bf16(synth_weights_bf16(n, m, seed=60 + s), G, scale)

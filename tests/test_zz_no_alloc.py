@@ -3,11 +3,11 @@
 The allocation-free entry point runs q8_linear's kernels with its scratch
 in the library's fixed per-GPU array instead of a context's workspace, so
 on every path -- the one-row GEMV, the f32 4x4-block kernel (2-4 rows),
-the split-bf16 kernel with its cross-workgroup K split (arrival counters
-and partials in the scratch), the dequant-GEMM with its binary16 buffer and
-split-K partials -- it must give q8_linear's bits.  Each case calls it twice
-in a row, the second time with a smaller input, so a first call's leftovers
-in the shared array (partials, counters, exponents) would show.  A GEMM
+the split-bf16 kernel with its cross-workgroup K split (partials in the
+scratch), the dequant-GEMM with its binary16 buffer and split-K partials --
+it must give q8_linear's bits.  Each case calls it twice in a row, the
+second time with a smaller input, so a first call's leftovers in the shared
+array (partials, exponents) would show.  A GEMM
 whose rows overflow the 16 MiB activation buffer runs in row chunks and is
 held to the 1e-3 contract against the float64 oracle instead.
 """
