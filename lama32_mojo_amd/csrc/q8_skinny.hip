@@ -306,8 +306,9 @@ constexpr int kXbRow = kXSlab + 16;        // LDS bf16 per staged x row
 constexpr int kCbRow = kXSlab + 16;        // LDS bytes per staged code row
 constexpr int kXStages = 2;                // slabs held in registers per wave
 // waves per SIMD the register allocation must allow: three 4-wave
-// workgroups per CU (their LDS, 53 KiB each, fits three times)
-template <int KW> constexpr int kXWavesPerSimd = KW == 4 ? 3 : 1;
+// workgroups per CU (their LDS, 53 KiB each, fits three times), two 6-wave
+// ones
+template <int KW> constexpr int kXWavesPerSimd = KW <= 6 ? 3 : 1;
 
 // Narrow matrices split K over ks_n workgroups per row block (slabs
 // [k spk, (k + 1) spk) for workgroup k): each writes its partial outputs to
@@ -323,8 +324,7 @@ void skinny_x_kernel(const uint8_t *__restrict__ w,
                                                            int spk, float *__restrict__ ws) {
   constexpr int SB = ScaleTraits<KIND>::bytes;
   constexpr int XR = 16 * TR;                  // staged x rows
-  static_assert(XR % KW == 0, "x rows split evenly over the waves");
-  constexpr int XPW = XR / KW;                 // x rows each wave loads
+  constexpr int XPW = (XR + KW - 1) / KW;      // x rows each wave loads
   constexpr int SPS = (kXSlab / G) * SB;       // scale bytes of a row per slab
   constexpr int NDW = NC * 16 * SPS / 4;       // scale dwords of a wave per slab
   constexpr int NL = (NDW + 63) / 64;
@@ -351,7 +351,8 @@ void skinny_x_kernel(const uint8_t *__restrict__ w,
 #pragma unroll
   for (int u = 0; u < XPW; ++u) {
     const int r = wid + KW * u;
-    xr[u] = make_rsrc(x + (int64_t)(r < s ? r : 0) * m, r < s ? (uint32_t)m * 4 : 0u);
+    xr[u] = make_rsrc(x + (int64_t)(r < s ? r : 0) * m,
+                      r < s && (XR % KW == 0 || r < XR) ? (uint32_t)m * 4 : 0u);
   }
   const uint32_t cbase = (uint32_t)((m / G) * SB);
   uint32_t co[NC][4], so[NL];
@@ -395,8 +396,10 @@ void skinny_x_kernel(const uint8_t *__restrict__ w,
       split2(xg[u].x, xg[u].y, h0, l0);
       split2(xg[u].z, xg[u].w, h1, l1);
       const int r = wid + KW * u;
-      *reinterpret_cast<u32x2 *>(&xh[buf][r][4 * lane]) = u32x2{h0, h1};
-      *reinterpret_cast<u32x2 *>(&xl[buf][r][4 * lane]) = u32x2{l0, l1};
+      if (XR % KW == 0 || r < XR) {
+        *reinterpret_cast<u32x2 *>(&xh[buf][r][4 * lane]) = u32x2{h0, h1};
+        *reinterpret_cast<u32x2 *>(&xl[buf][r][4 * lane]) = u32x2{l0, l1};
+      }
     }
   };
 
@@ -630,6 +633,11 @@ hipError_t launch_g(const LinearArgs &a, hipStream_t st) {
   // batch rows on, narrower matrices (about 768), where the K split over the
   // waves of the per-wave-x form reads x too often.
   if (a.s <= 16) {
+    // 96-row workgroups where they make one per CU and 64-row ones would
+    // make between one and two per CU (Qwen3-8B gate|up at s = 16: 36.6 ->
+    // 34.1 us); vocabulary-sized matrices keep 64 rows (lm_head 170 us
+    // against 210)
+    if (a.n > 256 * 64 && a.n <= 256 * 96) return launch_x<G, KIND, 1, 1, 6>(a, 1, st);
     if (a.n >= 16384) return launch_x<G, KIND, 1, 1, 4>(a, 1, st);
     if (a.m >= 8192) return launch_x_split<G, KIND>(a, 512, st);
     if (a.s > 8) return launch_x_split<G, KIND>(a, 768, st);
