@@ -316,12 +316,9 @@ template <int KW> constexpr int kXWavesPerSimd = KW <= 6 ? 3 : 1;
 // ks_n - 1 (so the result does not depend on which workgroup ends first).
 template <int G, int KIND, int TR, int NC, int KW, int PD>
 __global__ __launch_bounds__(64 * KW) __attribute__((amdgpu_waves_per_eu(kXWavesPerSimd<KW>)))
-void skinny_x_kernel(const uint8_t *__restrict__ w,
-                                                           int64_t row_bytes,
-                                                           const float *__restrict__ x,
-                                                           float *__restrict__ y, int s, int m,
-                                                           int64_t n, int nslab, int ks_n,
-                                                           int spk, float *__restrict__ ws) {
+void skinny_x_kernel(const uint8_t *__restrict__ w, int64_t row_bytes, const float *__restrict__ x,
+                     float *__restrict__ y, int s, int m, int64_t n, int nslab, int ks_n, int spk,
+                     float *__restrict__ ws) {
   constexpr int SB = ScaleTraits<KIND>::bytes;
   constexpr int XR = 16 * TR;                  // staged x rows
   constexpr int XPW = (XR + KW - 1) / KW;      // x rows each wave loads
