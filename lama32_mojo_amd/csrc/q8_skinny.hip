@@ -311,14 +311,14 @@ constexpr int kXStages = 2;                // slabs held in registers per wave
 template <int KW> constexpr int kXWavesPerSimd = KW <= 6 ? 3 : 1;
 
 // Narrow matrices split K over ks_n workgroups per row block (slabs
-// [k spk, (k + 1) spk) for workgroup k): each writes its partial outputs to
-// slice k of ws, and a second kernel adds the ks_n slices in order 0 ..
-// ks_n - 1 (so the result does not depend on which workgroup ends first).
+// [k spk, (k + 1) spk) for workgroup k): each writes its partial tile to
+// ws, and a second kernel adds the ks_n tiles in order 0 .. ks_n - 1 (so
+// the result does not depend on which workgroup ends first).
 template <int G, int KIND, int TR, int NC, int KW, int PD>
 __global__ __launch_bounds__(64 * KW) __attribute__((amdgpu_waves_per_eu(kXWavesPerSimd<KW>)))
 void skinny_x_kernel(const uint8_t *__restrict__ w, int64_t row_bytes, const float *__restrict__ x,
                      float *__restrict__ y, int s, int m, int64_t n, int nslab, int ks_n, int spk,
-                     float *__restrict__ ws) {
+                     int kmaj, float *__restrict__ ws) {
   constexpr int SB = ScaleTraits<KIND>::bytes;
   constexpr int XR = 16 * TR;                  // staged x rows
   constexpr int XPW = (XR + KW - 1) / KW;      // x rows each wave loads
@@ -335,7 +335,14 @@ void skinny_x_kernel(const uint8_t *__restrict__ w, int64_t row_bytes, const flo
   const int lane = threadIdx.x & 63;
   const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int c = lane & 15, q = lane >> 4;
-  const int rb = (int)blockIdx.x / ks_n, kp = (int)blockIdx.x % ks_n;
+  // The workgroups of a launch go to the 8 XCDs in turn.  Split-major
+  // (kmaj): the ks_n splits of row block rb are workgroups rb, rb + nrb, ...,
+  // so with nrb a multiple of 8 they run on one XCD, as does block rb of the
+  // launch that adds their partials.  Row-block-major: workgroup kp + ks_n rb,
+  // so with ks_n a multiple of 8 each XCD reads only its own slabs of x.
+  const int nrb = (int)gridDim.x / ks_n;
+  const int kp = kmaj ? (int)blockIdx.x / nrb : (int)blockIdx.x % ks_n;
+  const int rb = kmaj ? (int)blockIdx.x % nrb : (int)blockIdx.x / ks_n;
   // this workgroup's slabs [sb, sb + ns)
   const int sb = kp * spk;
   const int ns = nslab - sb < spk ? nslab - sb : spk;
@@ -554,41 +561,97 @@ void skinny_x_kernel(const uint8_t *__restrict__ w, int64_t row_bytes, const flo
   }
 
   // D layout of v_mfma_f32_16x16x32: lane -> weight row lane % 16, element
-  // v -> batch row 4 (lane / 16) + v.  A K split writes its partial to its
-  // own slice of ws, laid out as y.
-  float *out = ks_n == 1 ? y : ws + (int64_t)kp * s * n;
+  // v -> batch row 4 (lane / 16) + v
+  if (ks_n == 1) {
 #pragma unroll
-  for (int t = 0; t < NC; ++t) {
-    const int64_t j = j0 + 16 * t + c;
-    if (j < n) {
+    for (int t = 0; t < NC; ++t) {
+      const int64_t j = j0 + 16 * t + c;
+      if (j < n) {
 #pragma unroll
-      for (int tr = 0; tr < TR; ++tr)
+        for (int tr = 0; tr < TR; ++tr)
 #pragma unroll
-        for (int v = 0; v < 4; ++v) {
-          const int bb = 16 * tr + 4 * q + v;
-          if (bb < s) out[(int64_t)bb * n + j] = acc[t][tr][v];
-        }
+          for (int v = 0; v < 4; ++v) {
+            const int bb = 16 * tr + 4 * q + v;
+            if (bb < s) y[(int64_t)bb * n + j] = acc[t][tr][v];
+          }
+      }
+    }
+    return;
+  }
+  // A K split writes the first s rows of its partial tile [XR batch rows]
+  // [ROWS weight rows] (zeros past n) to tile kp nrb + rb of ws.
+  constexpr int ROWS = 16 * NC * KW;
+  float *part = ws + ((int64_t)kp * nrb + rb) * (XR * ROWS);
+#pragma unroll
+  for (int t = 0; t < NC; ++t)
+#pragma unroll
+    for (int tr = 0; tr < TR; ++tr)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const int bb = 16 * tr + 4 * q + v;
+        if (bb < s) part[bb * ROWS + wid * 16 * NC + 16 * t + c] = acc[t][tr][v];
+      }
+}
+
+// y = the sum of the ks_n partial tiles of each row block, added in split
+// order 0 .. ks_n - 1 (so the result does not depend on which workgroup
+// ended first).  Block rb adds the tiles of row block rb (with a
+// split-major grid, on the XCD that wrote them); a thread takes 4
+// consecutive entries and issues the loads of up to 8 splits before adding
+// them.
+template <int XR, int ROWS>
+__global__ __launch_bounds__(256) void xsplit_reduce_kernel(const float *__restrict__ ws,
+                                                            float *__restrict__ y, int s, int64_t n,
+                                                            int nrb, int ks_n) {
+  constexpr int PT = XR * ROWS;
+  const int rb = blockIdx.x;
+  const float *p0 = ws + (int64_t)rb * PT;
+  const int64_t stride = (int64_t)nrb * PT;   // between the splits of a tile
+  for (int e = 4 * (int)threadIdx.x; e < s * ROWS; e += 1024) {
+    f32x4 v = *reinterpret_cast<const f32x4 *>(p0 + e);
+    for (int z0 = 1; z0 < ks_n; z0 += 8) {
+      f32x4 t[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const int z = z0 + u < ks_n ? z0 + u : ks_n - 1;   // past the last: reread it
+        t[u] = *reinterpret_cast<const f32x4 *>(p0 + z * stride + e);
+      }
+#pragma unroll
+      for (int u = 0; u < 8; ++u) v = z0 + u < ks_n ? v + t[u] : v;
+    }
+    const int bb = e / ROWS;
+    const int64_t j = (int64_t)rb * ROWS + e % ROWS;
+    float *yp = y + (int64_t)bb * n + j;
+    if (j + 3 < n && (reinterpret_cast<uintptr_t>(yp) & 15) == 0) {
+      *reinterpret_cast<f32x4 *>(yp) = v;
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        if (j + i < n) yp[i] = v[i];
     }
   }
 }
 
 // Row blocks of 16 NC KW weight rows; with ks_n > 1 each is split over
-// ks_n workgroups of spk slabs, whose partials (ks_n s n floats of the
-// workspace) are added by the split-K sum kernel.
+// ks_n workgroups of spk slabs, whose partial tiles (ks_n nrb 16 TR ROWS
+// floats of the workspace) a second launch adds; kmaj orders the grid
+// split-major.
 template <int G, int KIND, int TR, int NC, int KW>
-hipError_t launch_x(const LinearArgs &a, int ks_n, hipStream_t st) {
-  constexpr int ROWS = 16 * NC * KW;
+hipError_t launch_x(const LinearArgs &a, int ks_n, hipStream_t st, bool kmaj = false) {
+  constexpr int ROWS = 16 * NC * KW, XR = 16 * TR;
   const int64_t nrb = (a.n + ROWS - 1) / ROWS;
   const int nslab = (int)((a.m + kXSlab - 1) / kXSlab);
   if (ks_n > nslab) ks_n = nslab;
-  if (ks_n > 1 && (!a.ws || ks_n * a.s * a.n > a.ws_floats)) ks_n = 1;
+  if (ks_n > 1 && (!a.ws || ks_n * nrb * XR * ROWS > a.ws_floats)) ks_n = 1;
   const int spk = (nslab + ks_n - 1) / ks_n;
   ks_n = (nslab + spk - 1) / spk;   // no empty split
   constexpr int PD = kXStages;
   hipLaunchKernelGGL((skinny_x_kernel<G, KIND, TR, NC, KW, PD>), dim3((unsigned)(nrb * ks_n)),
                      dim3(64 * KW), 0, st, a.w, a.row_bytes, static_cast<const float *>(a.x),
-                     a.y, (int)a.s, (int)a.m, a.n, nslab, ks_n, spk, a.ws);
-  if (ks_n > 1) return launch_splitk_reduce(a.ws, a.y, a.s * a.n, ks_n, st);
+                     a.y, (int)a.s, (int)a.m, a.n, nslab, ks_n, spk, (int)kmaj, a.ws);
+  if (ks_n > 1)
+    hipLaunchKernelGGL((xsplit_reduce_kernel<XR, ROWS>), dim3((unsigned)nrb), dim3(256), 0, st,
+                       a.ws, a.y, (int)a.s, a.n, (int)nrb, ks_n);
   return hipGetLastError();
 }
 
@@ -614,11 +677,16 @@ hipError_t launch_tr(const LinearArgs &a, hipStream_t st) {
 }
 
 // Shared-x form with K split over ks_n workgroups per 64-row block, ks_n
-// chosen for about `target` workgroups in all.
+// chosen for about `target` workgroups in all.  Short rows order the grid
+// split-major: the partial tiles (ks_n x 4 KiB per row block) then stay in
+// one XCD's L2 for the reduce, while every XCD reads all of x (16 rows x m
+// floats, 256 KiB at m = 4096); long rows (m >= 8192) keep x per XCD
+// instead (Qwen3-8B at 16 rows, against row-block-major: q|k|v 15.98 ->
+// 15.23 us, o 12.57 -> 11.47 us; down 21.6 us split-major, 21.2 not).
 template <int G, int KIND>
 hipError_t launch_x_split(const LinearArgs &a, int64_t target, hipStream_t st) {
   const int64_t nrb = (a.n + 63) / 64;
-  return launch_x<G, KIND, 1, 1, 4>(a, (int)((target + nrb - 1) / nrb), st);
+  return launch_x<G, KIND, 1, 1, 4>(a, (int)((target + nrb - 1) / nrb), st, a.m < 8192);
 }
 
 template <int G, int KIND>
