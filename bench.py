@@ -472,7 +472,9 @@ def run_decode_model(B: Bench, ctxlen: int = 1024, cfg=None, tok_metric: bool = 
                                f"embedding gather, {cfg.layers} layers (rmsnorm + fused "
                                "q|k|v GEMV, "
                                + ("q/k head norms + " if cfg.qk_norm else "")
-                               + "RoPE + fp16 KV append + attention, merge, o GEMV "
+                               + "RoPE + fp16 KV append + attention (plus a merge of "
+                               "its context splits when the cache is longer than 4 "
+                               "key chunks per wave), o GEMV "
                                "+ residual, rmsnorm + fused gate|up GEMV + swiglu, down GEMV "
                                f"+ residual), final norm + lm_head GEMV {cfg.vocab}x"
                                f"{cfg.hidden}, argmax; one HIP graph per token",
