@@ -405,16 +405,18 @@ __global__ __launch_bounds__(64 * KW) void skinny4x_kernel(const uint8_t *__rest
   // codes, scales and x of slab j are loaded PD slabs ahead, in the phase of
   // slab j - PD; x of slab i + 1 is stored after the compute of slab i and
   // before the phase's barrier, so a buffer is rewritten only after the
-  // barrier that follows every wave's last read of it.  The loads are
-  // unconditional (past the last slab their offsets are out of range and
-  // they read nothing), and a phase past the last slab is skipped by a
+  // barrier that follows every wave's last read of it.  A slab's x is
+  // loaded before its codes, so storing the latest x waits for x alone, not
+  // for the codes issued after it (loads return in issue order).  The loads
+  // are unconditional (past the last slab their offsets are out of range
+  // and they read nothing), and a phase past the last slab is skipped by a
   // uniform branch that holds no loads.
   CodeSlab<Q, SS::NL> C[PD];
   u32x4 X[PD][XPW];
 #pragma unroll
   for (int u = 0; u < PD; ++u) {
-    load_codes(C[u], u, u < nslab);
     load_x(X[u], u, u < nslab);
+    load_codes(C[u], u, u < nslab);
   }
   store_x(X[0], 0);
   __syncthreads();
@@ -427,8 +429,8 @@ __global__ __launch_bounds__(64 * KW) void skinny4x_kernel(const uint8_t *__rest
         store_x(X[(u + 1) % PD], (u + 1) & 1);
         __syncthreads();
       }
-      load_codes(C[u], i + PD, i + PD < nslab);
       load_x(X[u], i + PD, i + PD < nslab);
+      load_codes(C[u], i + PD, i + PD < nslab);
     }
   }
 
