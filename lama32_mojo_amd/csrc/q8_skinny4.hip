@@ -407,10 +407,11 @@ __global__ __launch_bounds__(64 * KW) void skinny4x_kernel(const uint8_t *__rest
   // before the phase's barrier, so a buffer is rewritten only after the
   // barrier that follows every wave's last read of it.  A slab's x is
   // loaded before its codes, so storing the latest x waits for x alone, not
-  // for the codes issued after it (loads return in issue order).  The loads
-  // are unconditional (past the last slab their offsets are out of range
-  // and they read nothing), and a phase past the last slab is skipped by a
-  // uniform branch that holds no loads.
+  // for the codes issued after it (loads return in issue order).  Loads and
+  // phases are unconditional: past the last slab the offsets are out of
+  // range, the loads read zeros and the phase adds nothing (its scales are
+  // zero).  A phase inside a branch let the compiler sink the x load into
+  // the branch that stores it, one compute later than issued here.
   CodeSlab<Q, SS::NL> C[PD];
   u32x4 X[PD][XPW];
 #pragma unroll
@@ -424,11 +425,9 @@ __global__ __launch_bounds__(64 * KW) void skinny4x_kernel(const uint8_t *__rest
 #pragma unroll
     for (int u = 0; u < PD; ++u) {
       const int i = i0 + u;
-      if (i < nslab) {
-        compute(C[u], u & 1, i);
-        store_x(X[(u + 1) % PD], (u + 1) & 1);
-        __syncthreads();
-      }
+      compute(C[u], u & 1, i);
+      store_x(X[(u + 1) % PD], (u + 1) & 1);
+      __syncthreads();
       load_x(X[u], i + PD, i + PD < nslab);
       load_codes(C[u], i + PD, i + PD < nslab);
     }
