@@ -224,7 +224,11 @@ __global__ __launch_bounds__(64) void attn_combine_kernel(const float *__restric
 
 // ---- multi-row causal attention on the matrix cores (prompt rows) -----------
 // One block of 4 waves serves one KV head and PB = 4 * (32 / GRP) consecutive
-// query rows; each wave owns 32 columns, a column being one (row, query head)
+// query rows, grid (nkv, row blocks) with the last rows' blocks first: a
+// block's key tiles grow with its rows, and blocks are dispatched in index
+// order, so the longest ones start first and the short ones fill in behind
+// them (row blocks in order left the longest for the end: 2048 rows, 128-dim
+// heads 32 / 8, 202 -> 127 us).  Each wave owns 32 columns, a column being one (row, query head)
 // pair of the group.  Per tile of 64 keys the block stages K row-major and V
 // transposed in LDS, and each wave forms S^T = K Q^T and O^T += V^T P^T with
 // v_mfma_f32_32x32x16_f16 and an online softmax over its columns.
@@ -268,12 +272,12 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(const float *__restri
   __shared__ __attribute__((aligned(16))) _Float16 ks[BK * KST];
   __shared__ __attribute__((aligned(16))) _Float16 vt[HD * VST];
 
-  const int g = blockIdx.y;
+  const int g = blockIdx.x;
   const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int col = lane & 31, hf = lane >> 5;
   const int pos0 = posp ? *posp : pos0_host;
   const int qdim = nheads * HD, kvdim = nkv * HD;
-  const int row0 = blockIdx.x * PB;
+  const int row0 = ((int)gridDim.y - 1 - (int)blockIdx.y) * PB;   // longest rows first
   const int nkeys = min(pos0 + min(row0 + PB, s), maxlen);   // keys any row of the block sees
   const int ntiles = nkeys > 0 ? (nkeys + BK - 1) / BK : 0;
   const int wend = min(pos0 + min(row0 + w * PW + PW, s), maxlen);   // ... any row of the wave
@@ -943,7 +947,7 @@ hipError_t launch_attn_t(const AttnArgs &a, hipStream_t st) {
 template <int HD, int GRP>
 hipError_t launch_prefill_t(const AttnArgs &a, hipStream_t st) {
   constexpr int PB = 4 * (32 / GRP);
-  hipLaunchKernelGGL((attn_prefill_kernel<HD, GRP>), dim3((unsigned)((a.s + PB - 1) / PB), (unsigned)a.nkv),
+  hipLaunchKernelGGL((attn_prefill_kernel<HD, GRP>), dim3((unsigned)a.nkv, (unsigned)((a.s + PB - 1) / PB)),
                      dim3(256), 0, st, a.q, a.kc, a.vc, a.out, a.s, a.nheads, a.nkv, a.posp,
                      a.pos0, a.maxlen);
   return hipGetLastError();
