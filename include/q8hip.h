@@ -205,6 +205,17 @@ int q8_linear_fused(q8_ctx *ctx, q8_buf *w, uint64_t owt_u16, q8_buf *a,
                     int scale_dtype, int pre, uint64_t onorm_u16, float eps,
                     int post, uint64_t ores_f32);
 
+/* y = W (silu(g) * u) for s rows of gate g (s x m floats at og) and up u
+ * (s x m at ou): the prompt path's swiglu folded into the binary16 pre-pass
+ * of the dequant-GEMM (the same bits as q8_swiglu into g, then q8_linear on
+ * g; g and u are left as they were).  s >= 32 (fewer rows: q8_swiglu, then
+ * q8_linear); g, u and the weight rows 16-byte aligned, m a multiple of 8.
+ * Replaces swiglu_mul_op + the down projection's mm_q8_op of run_layer_q8
+ * (src/llama_q8.mojo:221-225) for prompt rows. */
+int q8_linear_swiglu(q8_ctx *ctx, q8_buf *w, uint64_t owt_u16, q8_buf *a, uint64_t og_f32,
+                     uint64_t ou_f32, uint64_t oy_f32, int64_t s, int64_t m, int64_t n, int G,
+                     int scale_dtype);
+
 /* The end of a token step in two launches: logits y (n floats at oy) = W
  * rmsnorm(x) over the lm_head's n packed rows (norm weights at onorm of w;
  * as q8_linear_fused with Q8_PRE_RMSNORM), their argmax (as q8_argmax: the

@@ -59,13 +59,16 @@ __device__ __forceinline__ int weight_row_exponent(float mx) {
 // (one pass over memory); CH = 0 reads it twice.  Blocks [s, s + nwb): one
 // wave per weight row, the row exponent of its f32 scales (ew), f32 scales
 // only (nwb = 0 otherwise).
-template <bool XF32, int CH, int G>
+// SWIGLU (f32 x): x holds gate rows and up the matching up rows; the values
+// converted are silu(gate) * up, computed as swiglu_kernel computes them.
+template <bool XF32, int CH, int G, bool SWIGLU = false>
 __global__ __launch_bounds__(256) void act16_kernel(const void *__restrict__ xv, int64_t s,
                                                     int64_t m, uint16_t *__restrict__ x16,
                                                     int *__restrict__ ex,
                                                     const uint8_t *__restrict__ w,
                                                     int64_t row_bytes, int64_t n,
-                                                    int *__restrict__ ew) {
+                                                    int *__restrict__ ew,
+                                                    const float *__restrict__ up) {
   __shared__ float red[4];
   const int64_t r = blockIdx.x;
   const int tid = threadIdx.x;
@@ -89,6 +92,15 @@ __global__ __launch_bounds__(256) void act16_kernel(const void *__restrict__ xv,
       for (int c = 0; c < 4; ++c) {
         v[c] = a[c];
         v[4 + c] = b[c];
+      }
+      if constexpr (SWIGLU) {
+        const f32x4 *pu = reinterpret_cast<const f32x4 *>(up + r * m + k);
+        const f32x4 ua = pu[0], ub = pu[1];
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          v[c] = (v[c] / (1.0f + expf(-v[c]))) * ua[c];
+          v[4 + c] = (v[4 + c] / (1.0f + expf(-v[4 + c]))) * ub[c];
+        }
       }
     } else {
       const u32x4 d = *reinterpret_cast<const u32x4 *>(static_cast<const uint16_t *>(xv) + r * m + k);
@@ -160,13 +172,13 @@ __global__ __launch_bounds__(256) void act16_kernel(const void *__restrict__ xv,
 }
 
 // nw weight rows get their exponents (0 for none).
-template <bool XF32, int G>
+template <bool XF32, int G, bool SWIGLU = false>
 void launch_act16(const LinearArgs &a, uint16_t *x16, int *ex, int *ew, int64_t nw,
                   hipStream_t st) {
   const dim3 grid((unsigned)(a.s + (nw + 3) / 4)), block(256);
-#define Q8_ACT16(CH)                                                                         \
-  hipLaunchKernelGGL((act16_kernel<XF32, CH, G>), grid, block, 0, st, a.x, a.s, a.m, x16, ex, \
-                     a.w, a.row_bytes, nw, ew)
+#define Q8_ACT16(CH)                                                                          \
+  hipLaunchKernelGGL((act16_kernel<XF32, CH, G, SWIGLU>), grid, block, 0, st, a.x, a.s, a.m,  \
+                     x16, ex, a.w, a.row_bytes, nw, ew, a.up)
   if (a.m <= 2048)
     Q8_ACT16(1);
   else if (a.m <= 4096)
@@ -466,6 +478,8 @@ hipError_t launch_g(const LinearArgs &a, uint16_t *x16, int *ex, int *ew, bool w
   const int64_t nw = KIND == SCALE_F32 && weights ? a.n : 0;
   if (a.x_is_bf16)
     launch_act16<false, G>(a, x16, ex, ew, nw, st);
+  else if (a.up)
+    launch_act16<true, G, true>(a, x16, ex, ew, nw, st);
   else
     launch_act16<true, G>(a, x16, ex, ew, nw, st);
   // 128-row tiles once the rows fill them; two column tiles per consumer

@@ -33,6 +33,10 @@ struct LinearArgs {
   // partial sums.
   float *ws = nullptr;
   int64_t ws_floats = 0;
+  // GEMM only, f32 x: with up set, x holds gate rows [s, m], up rows
+  // [s, m] sit at up, and the linear reads silu(gate) * up (the values
+  // swiglu_kernel stores).
+  const float *up = nullptr;
 };
 // Decode path (s small, f32 x): VALU GEMV.
 hipError_t launch_gemv(const LinearArgs &a, hipStream_t st);

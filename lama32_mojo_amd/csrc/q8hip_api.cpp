@@ -455,11 +455,13 @@ hipError_t run_gemm_in(q8::LinearArgs la, void *act16, int64_t bytes, hipStream_
   int *ew = reinterpret_cast<int *>(base + bytes - (4 * la.n + 255) / 256 * 256);
   const int64_t xb = la.x_is_bf16 ? 2 : 4;
   const uint8_t *x0 = static_cast<const uint8_t *>(la.x);
+  const float *u0 = la.up;
   float *y0 = la.y;
   const int64_t s = la.s;
   for (int64_t r0 = 0; r0 < s; r0 += rows) {
     la.s = s - r0 < rows ? s - r0 : rows;
     la.x = x0 + r0 * la.m * xb;
+    if (u0) la.up = u0 + r0 * la.m;
     la.y = y0 + r0 * la.n;
     hipError_t e = q8::launch_gemm(la, x16, ex, ew, r0 == 0, st);
     if (e != hipSuccess) return e;
@@ -826,6 +828,50 @@ int q8_linear_fused(q8_ctx *ctx, q8_buf *w, uint64_t owt_u16, q8_buf *a, uint64_
   if (int rc = set_device(ctx)) return rc;
   hipError_t e = q8::launch_gemv_fused(f, ctx->stream);
   if (e != hipSuccess) return hip_fail(ctx, e, "q8_linear_fused launch");
+  return ok(ctx);
+}
+
+int q8_linear_swiglu(q8_ctx *ctx, q8_buf *w, uint64_t owt_u16, q8_buf *a, uint64_t og_f32,
+                     uint64_t ou_f32, uint64_t oy_f32, int64_t s, int64_t m, int64_t n, int G,
+                     int scale_dtype) {
+  if (int rc = check_ctx(ctx)) return rc;
+  if (int rc = check_linear(ctx, "q8_linear_swiglu", w, owt_u16, s, m, n, G, scale_dtype))
+    return rc;
+  if (!a) return fail(ctx, Q8_ERR_ARG, "q8_linear_swiglu: null activation buffer");
+  const uint64_t nx = (uint64_t)s * (uint64_t)m, ny = (uint64_t)s * (uint64_t)n;
+  if (int rc = check_f32(ctx, a, og_f32, nx, "q8_linear_swiglu", "gate")) return rc;
+  if (int rc = check_f32(ctx, a, ou_f32, nx, "q8_linear_swiglu", "up")) return rc;
+  if (int rc = check_f32(ctx, a, oy_f32, ny, "q8_linear_swiglu", "y")) return rc;
+  if (nx && ny && (overlaps(og_f32, og_f32 + nx, oy_f32, oy_f32 + ny) ||
+                   overlaps(ou_f32, ou_f32 + nx, oy_f32, oy_f32 + ny)))
+    return fail(ctx, Q8_ERR_ARG, "q8_linear_swiglu: gate or up overlaps y");
+  if (s < kGemmMinRows)
+    return fail(ctx, Q8_ERR_UNSUPPORTED, "q8_linear_swiglu: s=%lld (from %lld rows; fewer: "
+                "q8_swiglu, then q8_linear)", (long long)s, (long long)kGemmMinRows);
+  if (!gemm_fits(kAct16Bytes, m, n))
+    return fail(ctx, Q8_ERR_SHAPE, "q8_linear_swiglu: m=%lld, n=%lld too large for the GEMM's "
+                "activation buffer (%lld bytes)", (long long)m, (long long)n,
+                (long long)kAct16Bytes);
+  q8::LinearArgs la;
+  la.w = bytes(w, owt_u16 * 2);
+  la.row_bytes = rowstride_u16(m, G, scale_dtype) * 2;
+  la.x = bytes(a, og_f32 * 4);
+  la.x_is_bf16 = 0;
+  la.up = reinterpret_cast<const float *>(bytes(a, ou_f32 * 4));
+  la.y = reinterpret_cast<float *>(bytes(a, oy_f32 * 4));
+  la.s = s;
+  la.m = m;
+  la.n = n;
+  la.G = G;
+  la.kind = scale_dtype;
+  if (!gemm_aligned(la) || reinterpret_cast<uintptr_t>(la.up) % 16 != 0)
+    return fail(ctx, Q8_ERR_UNSUPPORTED, "q8_linear_swiglu: gate, up and the weight rows must "
+                "be 16-byte aligned, m a multiple of 8");
+  if (ctx->host_only) return fail(ctx, Q8_ERR_NODEVICE, "q8_linear_swiglu: host-only context");
+  if (n == 0) return ok(ctx);
+  if (int rc = set_device(ctx)) return rc;
+  hipError_t e = run_gemm(ctx, la);
+  if (e != hipSuccess) return hip_fail(ctx, e, "q8_linear_swiglu launch");
   return ok(ctx);
 }
 

@@ -354,8 +354,14 @@ class Q8Llama:
         else:
             og = self.linear(oz, s, H, lo.gate, I)
             ou = self.linear(oz, s, H, lo.up, I)
-        q8hip.swiglu(ctx, a.buf, og, ou, s * I)
-        om = self.linear(og, s, I, lo.down, H)
+        if s >= 32 and og % 4 == 0 and ou % 4 == 0:
+            # prompt rows: the swiglu folded into the down GEMM's pre-pass
+            om = a.alloc(s * H)
+            q8hip.linear_swiglu(ctx, w.buf, lo.down, a.buf, og, ou, om, s, I, H, self.G,
+                                self.scale)
+        else:
+            q8hip.swiglu(ctx, a.buf, og, ou, s * I)
+            om = self.linear(og, s, I, lo.down, H)
         q8hip.add(ctx, a.buf, om, oh, s * H)
         return oh
 

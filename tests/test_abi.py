@@ -97,6 +97,26 @@ def test_linear_validation(hctx):
     assert code_of(L, hctx, w, 8, a, 0, 4096, 0, 2048, 16)[0] == Q8_ERR_NODEVICE
 
 
+def test_linear_swiglu_validation(hctx):
+    """q8_linear_swiglu: prompt rows only (s >= 32), gate / up / y in the
+    arena and y apart from both inputs; valid calls reach the device step."""
+    m, n, s = 2048, 64, 32
+    rs = q8hip.rowstride_u16(m)
+    w = hctx.alloc(2 * n * rs)
+    a = hctx.alloc(4 * (2 * s * m + s * n))
+    L = q8hip.linear_swiglu
+    og, ou, oy = 0, s * m, 2 * s * m
+    assert code_of(L, hctx, w, 0, a, og, ou, oy, s, m, n)[0] == Q8_ERR_NODEVICE
+    assert code_of(L, hctx, w, 0, a, og, ou, oy, 31, m, n)[0] == q8hip.Q8_ERR_UNSUPPORTED
+    assert code_of(L, hctx, w, 0, a, og, ou, ou, s, m, n)[0] == Q8_ERR_ARG      # y on up
+    assert code_of(L, hctx, w, 0, a, og, ou, og + 8, s, m, n)[0] == Q8_ERR_ARG  # y on gate
+    assert code_of(L, hctx, w, 0, a, og, ou, oy + 8, s, m, n)[0] == Q8_ERR_RANGE
+    assert code_of(L, hctx, w, 0, a, og + 1, ou, oy, s, m, n)[0] == q8hip.Q8_ERR_UNSUPPORTED
+    assert code_of(L, hctx, w, 8, a, og, ou, oy, s, m, n)[0] == Q8_ERR_RANGE    # rows past w
+    w.free()
+    a.free()
+
+
 def test_linear_fused_validation(hctx):
     m, n = 2048, 64
     rs = q8hip.rowstride_u16(m)

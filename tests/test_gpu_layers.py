@@ -384,6 +384,43 @@ def test_linear_fused_equals_separate_calls(ctx, G, scale, m, n):
         b.free()
 
 
+@pytest.mark.parametrize("G,scale", [(64, "f16"), (32, "f32")])
+@pytest.mark.parametrize("s,m,n", [(32, 2048, 512), (100, 14336, 1000), (300, 4096, 4096),
+                                   (33, 20480, 256)])
+def test_linear_swiglu_equals_swiglu_then_linear(ctx, G, scale, s, m, n):
+    """q8_linear_swiglu (silu(g) * u computed in the GEMM's binary16 pre-pass)
+    gives the bits of q8_swiglu into g followed by q8_linear on g, and leaves
+    g and u unchanged: 2048..20480-code rows (the pre-pass holding up to 8
+    chunks per thread in registers, and past 16384 re-reading the row),
+    ragged row counts."""
+    say("linear_swiglu", G, scale, s, m, n)
+    rng = np.random.default_rng(s + m)
+    rs = q8hip.rowstride_u16(m, G, scale)
+    wsrc = ctx.alloc(2 * n * m)
+    wsrc.upload(f32_to_bf16_bits((0.02 * rng.standard_normal((n, m))).astype(np.float32)))
+    w = ctx.alloc(2 * n * rs)
+    q8hip.quantize_pack(ctx, wsrc, 0, q8hip.Q8_SRC_BF16, n, m, w, 0, G, scale)
+    wsrc.free()
+    g = (2 * rng.standard_normal((s, m))).astype(np.float32)
+    u = rng.standard_normal((s, m)).astype(np.float32)
+    og, ou, oy1, oy2 = 0, s * m, 2 * s * m, 2 * s * m + s * n
+    a = arena(ctx, 2 * s * m + 2 * s * n)
+    try:
+        put(a, og, g)
+        put(a, ou, u)
+        q8hip.linear_swiglu(ctx, w, 0, a, og, ou, oy2, s, m, n, G, scale)
+        got = get(a, oy2, (s, n))
+        assert np.array_equal(get(a, og, (s, m)), g) and np.array_equal(get(a, ou, (s, m)), u)
+        q8hip.swiglu(ctx, a, og, ou, s * m)
+        q8hip.linear(ctx, w, 0, a, og, oy1, s, m, n, G, scale)
+        want = get(a, oy1, (s, n))
+        assert np.all(np.isfinite(want)) and np.array_equal(got, want), \
+            max_rel_err(got, want)
+    finally:
+        a.free()
+        w.free()
+
+
 def test_fused_model_equals_unfused(ctx):
     """One-row steps with the folded launches give the logits of the
     separate rmsnorm / swiglu / add launches within max-rel-err 1e-5 (the
