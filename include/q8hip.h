@@ -255,12 +255,16 @@ int q8_add_rmsnorm(q8_ctx *ctx, q8_buf *w, uint64_t owt_u16, q8_buf *a,
  * (src/llama_common.mojo:299-342).  With posbuf != NULL the position is
  * instead the int32 at element offset opos of posbuf, read by the kernel
  * (a captured step then serves every position; rows past maxlen are dropped,
- * and attention clamps its context to maxlen). */
+ * and attention clamps its context to maxlen).  ld = 0: q, k and v are dense
+ * row-major; ld > 0: row i of each sits ld floats after row i-1 (q|k|v
+ * stacked in rows of one q8_linear output, ok = oq + nheads*head_dim,
+ * ov = ok + nkv*head_dim, ld = their sum); ld must be at least each row
+ * width, and k's columns must not meet q's at that stride (Q8_ERR_ARG). */
 int q8_rope_kv(q8_ctx *ctx, q8_buf *a, uint64_t oq_f32, uint64_t ok_f32,
                uint64_t ov_f32, uint64_t oinv_f32, q8_buf *kv, uint64_t okc_f16,
                uint64_t ovc_f16, int64_t maxlen, int64_t s, int64_t pos0,
                q8_buf *posbuf, uint64_t opos_i32, int nheads, int nkv,
-               int head_dim);
+               int head_dim, int64_t ld);
 
 /* Floats of activation-arena scratch q8_attention needs (0 from s = 16 on,
  * where attention is one pass on the matrix cores). */
@@ -275,12 +279,13 @@ uint64_t q8_attention_scratch_floats(int64_t s, int nheads, int head_dim,
  * online softmax: for s >= 16 one MFMA pass per (16..128-row block, KV
  * head), below that per-split partials in q8_attention_scratch_floats()
  * floats at oscratch (oscratch is unused when that is 0).  head_dim 64 or
- * 128, nheads / nkv in {1, 2, 4, 8}.  Position as in q8_rope_kv. */
+ * 128, nheads / nkv in {1, 2, 4, 8}.  Position as in q8_rope_kv.  Row i of q
+ * at oq + i*ldq (ldq = 0: nheads*head_dim, dense); out is dense. */
 int q8_attention(q8_ctx *ctx, q8_buf *a, uint64_t oq_f32, q8_buf *kv,
                  uint64_t okc_f16, uint64_t ovc_f16, int64_t maxlen,
                  uint64_t oy_f32, uint64_t oscratch_f32, int64_t s, int64_t pos0,
                  q8_buf *posbuf, uint64_t opos_i32, int nheads, int nkv,
-                 int head_dim);
+                 int head_dim, int64_t ldq);
 
 /* Decode step of one new token (s = 1): with wn non-null, per-head RMSNorm
  * of q and of k first (the head_dim bf16 weights at oqnorm / oknorm of wn,

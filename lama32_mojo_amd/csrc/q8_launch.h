@@ -103,13 +103,15 @@ hipError_t launch_embed_gather(const GatherArgs &a, hipStream_t st);
 // stored to h_out.
 hipError_t launch_rmsnorm(const uint16_t *wn, const float *x, const float *res, float *h_out,
                           float *y, int64_t rows, int64_t d, float eps, hipStream_t st);
-// RoPE on q [s, nheads*head_dim] and k [s, nkv*head_dim] in place; rotated k
-// and v go to binary16 cache rows pos0 .. pos0+s-1 (pos0 = *posp if posp).
+// RoPE on q [s, nheads*head_dim] (row stride ldq) and k [s, nkv*head_dim]
+// (row stride ldk, also v's) in place; rotated k and v go to binary16 cache
+// rows pos0 .. pos0+s-1 (pos0 = *posp if posp).
 hipError_t launch_rope_kv(float *q, float *k, const float *v, __half *kc, __half *vc,
                           const float *inv, int s, const int *posp, int pos0, int nheads, int nkv,
-                          int head_dim, int64_t maxlen, hipStream_t st);
+                          int head_dim, int64_t maxlen, int64_t ldq, int64_t ldk,
+                          hipStream_t st);
 struct AttnArgs {
-  const float *q;        // [s, nheads * head_dim], rotated
+  const float *q;        // [s, nheads * head_dim], rotated, row i at q + i * ldq
   const __half *kc, *vc; // [maxlen, nkv * head_dim]
   float *part;           // scratch (s < kPrefillMinRows only):
                          //   s * nheads * nsplit * (head_dim + 2) floats
@@ -118,6 +120,7 @@ struct AttnArgs {
   const int *posp;       // device position (or null: pos0)
   int pos0;
   int maxlen;            // cache rows; positions past it are clamped
+  int64_t ldq;           // q row stride in floats (nheads * head_dim when dense)
 };
 // Row counts from which attention runs as one MFMA pass per (row block, KV
 // head) with no scratch; below it, as (KV head, 64-key split) partials

@@ -74,15 +74,16 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const uint16_t *__restrict
 }
 
 // ---- RoPE on q and k + KV append (k_rope_qk_copy2) ----------------------------
-// HF rotate_half RoPE in place on q [s, qdim] and k [s, kvdim]; the rotated
-// k and the unrotated v of row i are stored as binary16 at cache row
-// pos0 + i (rows past maxlen are dropped).  One thread per rotated pair and
-// one per v element.
+// HF rotate_half RoPE in place on q [s, qdim] and k [s, kvdim] (row i of q
+// at q + i*ldq, of k and v at + i*ldk); the rotated k and the unrotated v of
+// row i are stored as binary16 at cache row pos0 + i (rows past maxlen are
+// dropped).  One thread per rotated pair and one per v element.
 __global__ __launch_bounds__(256) void rope_kv_kernel(float *q, float *k, const float *v,
                                                       __half *kc, __half *vc,
                                                       const float *inv, int s, const int *posp,
                                                       int pos0_host, int nheads, int nkv,
-                                                      int head_dim, int64_t maxlen) {
+                                                      int head_dim, int64_t maxlen,
+                                                      int64_t ldq, int64_t ldk) {
   const int half = head_dim / 2;
   const int nall = nheads + nkv;
   const int64_t nrope = (int64_t)s * nall * half;
@@ -97,14 +98,14 @@ __global__ __launch_bounds__(256) void rope_kv_kernel(float *q, float *k, const 
     float c, sn;
     rope_cs(freq, c, sn);
     if (h < nheads) {
-      float *base = q + (int64_t)i * qdim + h * head_dim;
+      float *base = q + (int64_t)i * ldq + h * head_dim;
       float y0, y1;
       rotate(base[d], base[half + d], c, sn, y0, y1);
       base[d] = y0;
       base[half + d] = y1;
     } else {
       const int hk = h - nheads;
-      float *base = k + (int64_t)i * kvdim + hk * head_dim;
+      float *base = k + (int64_t)i * ldk + hk * head_dim;
       float y0, y1;
       rotate(base[d], base[half + d], c, sn, y0, y1);
       base[d] = y0;
@@ -120,7 +121,7 @@ __global__ __launch_bounds__(256) void rope_kv_kernel(float *q, float *k, const 
     const int64_t vi = idx - nrope;
     const int64_t i = vi / kvdim;
     const int64_t row = pos0 + i;
-    if (row < maxlen) vc[row * kvdim + vi % kvdim] = __float2half_rn(v[vi]);
+    if (row < maxlen) vc[row * kvdim + vi % kvdim] = __float2half_rn(v[i * ldk + vi % kvdim]);
   }
 }
 
@@ -137,7 +138,7 @@ __global__ __launch_bounds__(64 * GRP) void attn_split_kernel(const float *__res
                                                               float *__restrict__ part, int nheads,
                                                               int nkv, const int *posp,
                                                               int pos0_host, int nsplit,
-                                                              int maxlen) {
+                                                              int maxlen, int64_t ldq) {
   constexpr int KC = 64;                       // keys per split
   constexpr int PW = HD + 2;                   // partial record: o[HD], m, l
   __shared__ float qs[GRP][HD];
@@ -145,7 +146,7 @@ __global__ __launch_bounds__(64 * GRP) void attn_split_kernel(const float *__res
   const int g = blockIdx.x, sp = blockIdx.y, i = blockIdx.z;
   const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int h = g * GRP + w;
-  const int qdim = nheads * HD, kvdim = nkv * HD;
+  const int kvdim = nkv * HD;
   const int pos0 = posp ? *posp : pos0_host;
   const int nctx = pos0 + i + 1 < maxlen ? pos0 + i + 1 : maxlen;   // cache rows that exist
   float *rec = part + (((int64_t)i * nheads + h) * nsplit + sp) * PW;
@@ -157,7 +158,7 @@ __global__ __launch_bounds__(64 * GRP) void attn_split_kernel(const float *__res
     }
     return;
   }
-  for (int d = lane; d < HD; d += 64) qs[w][d] = q[(int64_t)i * qdim + h * HD + d];
+  for (int d = lane; d < HD; d += 64) qs[w][d] = q[(int64_t)i * ldq + h * HD + d];
   __syncthreads();
   const float rd = sqrtf((float)HD);
   const int j = j0 + lane;
@@ -258,7 +259,8 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(const float *__restri
                                                            const __half *__restrict__ vc,
                                                            float *__restrict__ out, int s,
                                                            int nheads, int nkv, const int *posp,
-                                                           int pos0_host, int maxlen) {
+                                                           int pos0_host, int maxlen,
+                                                           int64_t ldq) {
   constexpr int BK = kPrefillBK;
   constexpr int KS = HD / 16;                    // 16-dim steps of a score tile
   constexpr int DT = HD / 32;                    // 32-dim tiles of the output
@@ -290,7 +292,7 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(const float *__restri
   half8 qh[KS], ql[KS];
   float cs;
   {
-    const float *qr = q + (int64_t)irow * qdim + head * HD + 8 * hf;
+    const float *qr = q + (int64_t)irow * ldq + head * HD + 8 * hf;
     f32x4 qv[KS][2];
     float mx = 0.0f;
 #pragma unroll
@@ -938,7 +940,7 @@ template <int HD, int GRP>
 hipError_t launch_attn_t(const AttnArgs &a, hipStream_t st) {
   hipLaunchKernelGGL((attn_split_kernel<HD, GRP>), dim3((unsigned)a.nkv, (unsigned)a.nsplit, (unsigned)a.s),
                      dim3(64 * GRP), 0, st, a.q, a.kc, a.vc, a.part, a.nheads, a.nkv, a.posp,
-                     a.pos0, a.nsplit, a.maxlen);
+                     a.pos0, a.nsplit, a.maxlen, a.ldq);
   hipLaunchKernelGGL((attn_combine_kernel<HD>), dim3((unsigned)a.nheads, (unsigned)a.s), dim3(64), 0,
                      st, a.part, a.out, a.nheads, a.posp, a.pos0, a.nsplit, a.maxlen);
   return hipGetLastError();
@@ -949,7 +951,7 @@ hipError_t launch_prefill_t(const AttnArgs &a, hipStream_t st) {
   constexpr int PB = 4 * (32 / GRP);
   hipLaunchKernelGGL((attn_prefill_kernel<HD, GRP>), dim3((unsigned)a.nkv, (unsigned)((a.s + PB - 1) / PB)),
                      dim3(256), 0, st, a.q, a.kc, a.vc, a.out, a.s, a.nheads, a.nkv, a.posp,
-                     a.pos0, a.maxlen);
+                     a.pos0, a.maxlen, a.ldq);
   return hipGetLastError();
 }
 
@@ -977,11 +979,12 @@ hipError_t launch_rmsnorm(const uint16_t *wn, const float *x, const float *res, 
 
 hipError_t launch_rope_kv(float *q, float *k, const float *v, __half *kc, __half *vc,
                           const float *inv, int s, const int *posp, int pos0, int nheads, int nkv,
-                          int head_dim, int64_t maxlen, hipStream_t st) {
+                          int head_dim, int64_t maxlen, int64_t ldq, int64_t ldk,
+                          hipStream_t st) {
   if (s == 0) return hipSuccess;
   const int64_t n = (int64_t)s * (nheads + nkv) * (head_dim / 2) + (int64_t)s * nkv * head_dim;
   hipLaunchKernelGGL(rope_kv_kernel, dim3(blocks_for(n, 256)), dim3(256), 0, st, q, k, v, kc, vc,
-                     inv, s, posp, pos0, nheads, nkv, head_dim, maxlen);
+                     inv, s, posp, pos0, nheads, nkv, head_dim, maxlen, ldq, ldk);
   return hipGetLastError();
 }
 

@@ -1005,10 +1005,15 @@ int q8_add_rmsnorm(q8_ctx *ctx, q8_buf *w, uint64_t owt_u16, q8_buf *a, uint64_t
   return ok(ctx);
 }
 
+// Floats spanned by s rows of `width` floats at a row stride of ld.
+static uint64_t rows_span(int64_t s, int64_t ld, uint64_t width) {
+  return s == 0 ? 0 : (uint64_t)(s - 1) * (uint64_t)ld + width;
+}
+
 int q8_rope_kv(q8_ctx *ctx, q8_buf *a, uint64_t oq_f32, uint64_t ok_f32, uint64_t ov_f32,
                uint64_t oinv_f32, q8_buf *kv, uint64_t okc_f16, uint64_t ovc_f16, int64_t maxlen,
                int64_t s, int64_t pos0, q8_buf *posbuf, uint64_t opos_i32, int nheads, int nkv,
-               int head_dim) {
+               int head_dim, int64_t ld) {
   if (int rc = check_ctx(ctx)) return rc;
   if (!a || !kv) return fail(ctx, Q8_ERR_ARG, "q8_rope_kv: null buffer");
   if (int rc = check_heads(ctx, nheads, nkv, head_dim, "q8_rope_kv")) return rc;
@@ -1018,15 +1023,30 @@ int q8_rope_kv(q8_ctx *ctx, q8_buf *a, uint64_t oq_f32, uint64_t ok_f32, uint64_
   if (!cache_block_ok(maxlen, nkv, head_dim))
     return fail(ctx, Q8_ERR_SHAPE, "q8_rope_kv: maxlen=%lld (a cache block must stay under "
                 "2 GiB)", (long long)maxlen);
-  const uint64_t qn = (uint64_t)s * nheads * head_dim, kn = (uint64_t)s * nkv * head_dim;
+  const int64_t qdim = (int64_t)nheads * head_dim, kvdim = (int64_t)nkv * head_dim;
+  if (ld != 0 && (ld < qdim || ld < kvdim || ld > INT32_MAX || s > INT32_MAX))
+    return fail(ctx, Q8_ERR_SHAPE, "q8_rope_kv: row stride %lld (0, or at least the q and k "
+                "row widths %lld, %lld)", (long long)ld, (long long)qdim, (long long)kvdim);
+  const int64_t ldq = ld ? ld : qdim, ldk = ld ? ld : kvdim;
+  const uint64_t qn = rows_span(s, ldq, qdim), kn = rows_span(s, ldk, kvdim);
   const uint64_t cn = (uint64_t)maxlen * nkv * head_dim;
   if (int rc = check_f32(ctx, a, oq_f32, qn, "q8_rope_kv", "q")) return rc;
   if (int rc = check_f32(ctx, a, ok_f32, kn, "q8_rope_kv", "k")) return rc;
   if (int rc = check_f32(ctx, a, ov_f32, kn, "q8_rope_kv", "v")) return rc;
   if (int rc = check_f32(ctx, a, oinv_f32, (uint64_t)head_dim / 2, "q8_rope_kv", "inv_freq"))
     return rc;
-  if (overlaps(oq_f32, oq_f32 + qn, ok_f32, ok_f32 + kn))
-    return fail(ctx, Q8_ERR_ARG, "q8_rope_kv: q and k overlap");
+  if (ld == 0) {
+    if (overlaps(oq_f32, oq_f32 + qn, ok_f32, ok_f32 + kn))
+      return fail(ctx, Q8_ERR_ARG, "q8_rope_kv: q and k overlap");
+  } else {
+    // rows of one stride: k's columns, taken modulo ld from q's row start,
+    // must lie in [qdim, ld) for no k element to be a q element
+    const int64_t d = (int64_t)(ok_f32 - oq_f32);   // both lie inside the arena
+    const int64_t r = (d % ld + ld) % ld;
+    if (r < qdim || r + kvdim > ld)
+      return fail(ctx, Q8_ERR_ARG, "q8_rope_kv: q and k rows overlap at stride %lld",
+                  (long long)ld);
+  }
   if (!fits(okc_f16, cn, 2, kv->size) || !fits(ovc_f16, cn, 2, kv->size))
     return fail(ctx, Q8_ERR_RANGE, "q8_rope_kv: K or V cache block exceeds the KV buffer");
   if (overlaps(okc_f16, okc_f16 + cn, ovc_f16, ovc_f16 + cn))
@@ -1039,7 +1059,8 @@ int q8_rope_kv(q8_ctx *ctx, q8_buf *a, uint64_t oq_f32, uint64_t ok_f32, uint64_
   const int *posp = posbuf ? reinterpret_cast<const int *>(bytes(posbuf, opos_i32 * 4)) : nullptr;
   hipError_t e = q8::launch_rope_kv(fptr(a, oq_f32), fptr(a, ok_f32), fptr(a, ov_f32),
                                     kvp + okc_f16, kvp + ovc_f16, fptr(a, oinv_f32), (int)s, posp,
-                                    (int)pos0, nheads, nkv, head_dim, maxlen, ctx->stream);
+                                    (int)pos0, nheads, nkv, head_dim, maxlen, ldq, ldk,
+                                    ctx->stream);
   if (e != hipSuccess) return hip_fail(ctx, e, "q8_rope_kv launch");
   return ok(ctx);
 }
@@ -1052,7 +1073,7 @@ uint64_t q8_attention_scratch_floats(int64_t s, int nheads, int head_dim, int64_
 int q8_attention(q8_ctx *ctx, q8_buf *a, uint64_t oq_f32, q8_buf *kv, uint64_t okc_f16,
                  uint64_t ovc_f16, int64_t maxlen, uint64_t oy_f32, uint64_t oscratch_f32,
                  int64_t s, int64_t pos0, q8_buf *posbuf, uint64_t opos_i32, int nheads, int nkv,
-                 int head_dim) {
+                 int head_dim, int64_t ldq) {
   if (int rc = check_ctx(ctx)) return rc;
   if (!a || !kv) return fail(ctx, Q8_ERR_ARG, "q8_attention: null buffer");
   if (int rc = check_heads(ctx, nheads, nkv, head_dim, "q8_attention")) return rc;
@@ -1066,14 +1087,19 @@ int q8_attention(q8_ctx *ctx, q8_buf *a, uint64_t oq_f32, q8_buf *kv, uint64_t o
   if (!cache_block_ok(maxlen, nkv, head_dim))
     return fail(ctx, Q8_ERR_SHAPE, "q8_attention: maxlen=%lld (a cache block must stay under "
                 "2 GiB)", (long long)maxlen);
-  const uint64_t qn = (uint64_t)s * nheads * head_dim;
+  const int64_t qdim = (int64_t)nheads * head_dim;
+  if (ldq != 0 && (ldq < qdim || ldq > INT32_MAX))
+    return fail(ctx, Q8_ERR_SHAPE, "q8_attention: q row stride %lld (0, or at least %lld)",
+                (long long)ldq, (long long)qdim);
+  if (ldq == 0) ldq = qdim;
+  const uint64_t qn = (uint64_t)s * qdim, qspan = rows_span(s, ldq, qdim);
   const uint64_t cn = (uint64_t)maxlen * nkv * head_dim;
   const uint64_t sn = q8_attention_scratch_floats(s, nheads, head_dim, maxlen);
-  if (int rc = check_f32(ctx, a, oq_f32, qn, "q8_attention", "q")) return rc;
+  if (int rc = check_f32(ctx, a, oq_f32, qspan, "q8_attention", "q")) return rc;
   if (int rc = check_f32(ctx, a, oy_f32, qn, "q8_attention", "out")) return rc;
   if (int rc = check_f32(ctx, a, oscratch_f32, sn, "q8_attention", "scratch")) return rc;
-  if (overlaps(oy_f32, oy_f32 + qn, oq_f32, oq_f32 + qn) ||
-      overlaps(oscratch_f32, oscratch_f32 + sn, oq_f32, oq_f32 + qn) ||
+  if (overlaps(oy_f32, oy_f32 + qn, oq_f32, oq_f32 + qspan) ||
+      overlaps(oscratch_f32, oscratch_f32 + sn, oq_f32, oq_f32 + qspan) ||
       overlaps(oscratch_f32, oscratch_f32 + sn, oy_f32, oy_f32 + qn))
     return fail(ctx, Q8_ERR_ARG, "q8_attention: q, out and scratch must not overlap");
   if (!fits(okc_f16, cn, 2, kv->size) || !fits(ovc_f16, cn, 2, kv->size))
@@ -1097,6 +1123,7 @@ int q8_attention(q8_ctx *ctx, q8_buf *a, uint64_t oq_f32, q8_buf *kv, uint64_t o
   aa.posp = posbuf ? reinterpret_cast<const int *>(bytes(posbuf, opos_i32 * 4)) : nullptr;
   aa.pos0 = (int)pos0;
   aa.maxlen = (int)maxlen;
+  aa.ldq = ldq;
   hipError_t e = q8::launch_attention(aa, ctx->stream);
   if (e != hipSuccess) return hip_fail(ctx, e, "q8_attention launch");
   return ok(ctx);

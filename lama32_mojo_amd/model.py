@@ -316,9 +316,13 @@ class Q8Llama:
             return self._layer_fused(L, ox, pos0, pb, oh)
         xn = a.alloc(s * H)
         q8hip.rmsnorm(ctx, w.buf, lo.in_norm, a.buf, ox, xn, s, H, cfg.eps)
-        if s == 1 and lo.k == lo.q + QD * rsH and lo.v == lo.k + KVD * rsH:
-            oq = self.linear(xn, 1, H, lo.q, QD + 2 * KVD)
+        ld = 0                                            # q, k, v row stride
+        if ((s == 1 or not cfg.qk_norm) and lo.k == lo.q + QD * rsH
+                and lo.v == lo.k + KVD * rsH):
+            # one stacked q|k|v linear; prompt rows then carry the stride
+            oq = self.linear(xn, s, H, lo.q, QD + 2 * KVD)
             okk, ov = oq + QD, oq + QD + KVD
+            ld = QD + 2 * KVD if s > 1 else 0
         else:
             oq = self.linear(xn, s, H, lo.q, QD)
             okk = self.linear(xn, s, H, lo.k, KVD)
@@ -338,11 +342,11 @@ class Q8Llama:
                                    cfg.head_dim, pb, 0)
         else:
             q8hip.rope_kv(ctx, a.buf, oq, okk, ov, self.oinv, self.kv, self.okc[L], self.ovc[L],
-                          self.maxlen, s, pos0, cfg.n_heads, cfg.n_kv, cfg.head_dim, pb, 0)
+                          self.maxlen, s, pos0, cfg.n_heads, cfg.n_kv, cfg.head_dim, pb, 0, ld)
             osc = a.alloc(q8hip.attention_scratch_floats(s, cfg.n_heads, cfg.head_dim,
                                                          self.maxlen))
             q8hip.attention(ctx, a.buf, oq, self.kv, self.okc[L], self.ovc[L], self.maxlen, oao,
-                            osc, s, pos0, cfg.n_heads, cfg.n_kv, cfg.head_dim, pb, 0)
+                            osc, s, pos0, cfg.n_heads, cfg.n_kv, cfg.head_dim, pb, 0, ld)
         oo = self.linear(oao, s, QD, lo.o, H)
         if oh is None:
             oh = a.alloc(s * H)

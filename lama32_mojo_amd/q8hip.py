@@ -98,10 +98,10 @@ SIGNATURES = {
     "q8_add_rmsnorm": (_I, [_P, _P, _U64, _P, _U64, _U64, _U64, _U64, _I64, _I64,
                            ctypes.c_float]),
     "q8_rope_kv": (_I, [_P, _P, _U64, _U64, _U64, _U64, _P, _U64, _U64, _I64, _I64, _I64, _P,
-                       _U64, _I, _I, _I]),
+                       _U64, _I, _I, _I, _I64]),
     "q8_attention_scratch_floats": (_U64, [_I64, _I, _I, _I64]),
     "q8_attention": (_I, [_P, _P, _U64, _P, _U64, _U64, _I64, _U64, _U64, _I64, _I64, _P, _U64,
-                         _I, _I, _I]),
+                         _I, _I, _I, _I64]),
     "q8_decode_attention": (_I, [_P, _P, _U64, _U64, _U64, _U64, _P, _U64, _U64, _I64, _U64,
                                 _I64, _P, _U64, _I, _I, _I, _P, _U64, _U64, ctypes.c_float]),
     "q8_linear_swiglu": (_I, [_P, _P, _U64, _P, _U64, _U64, _U64, _I64, _I64, _I64, _I, _I]),
@@ -381,11 +381,13 @@ def add_rmsnorm(ctx: Context, w: Buffer, owt_u16: int, a: Buffer, ox_f32: int, o
 
 def rope_kv(ctx: Context, a: Buffer, oq: int, ok: int, ov: int, oinv: int, kv: Buffer,
             okc_f16: int, ovc_f16: int, maxlen: int, s: int, pos0: int, nheads: int, nkv: int,
-            head_dim: int, posbuf: Buffer | None = None, opos_i32: int = 0) -> None:
+            head_dim: int, posbuf: Buffer | None = None, opos_i32: int = 0,
+            ld: int = 0) -> None:
+    """ld: row stride of q, k and v in floats (0: each dense)."""
     ctx.check(ctx._lib.q8_rope_kv(ctx.h, a.h, int(oq), int(ok), int(ov), int(oinv), kv.h,
                                   int(okc_f16), int(ovc_f16), int(maxlen), int(s), int(pos0),
                                   _h(posbuf), int(opos_i32), int(nheads), int(nkv),
-                                  int(head_dim)))
+                                  int(head_dim), int(ld)))
 
 
 def attention_scratch_floats(s: int, nheads: int, head_dim: int, maxlen: int) -> int:
@@ -395,11 +397,13 @@ def attention_scratch_floats(s: int, nheads: int, head_dim: int, maxlen: int) ->
 
 def attention(ctx: Context, a: Buffer, oq: int, kv: Buffer, okc_f16: int, ovc_f16: int,
               maxlen: int, oy: int, oscratch: int, s: int, pos0: int, nheads: int, nkv: int,
-              head_dim: int, posbuf: Buffer | None = None, opos_i32: int = 0) -> None:
+              head_dim: int, posbuf: Buffer | None = None, opos_i32: int = 0,
+              ldq: int = 0) -> None:
+    """ldq: row stride of q in floats (0: dense); out is dense."""
     ctx.check(ctx._lib.q8_attention(ctx.h, a.h, int(oq), kv.h, int(okc_f16), int(ovc_f16),
                                     int(maxlen), int(oy), int(oscratch), int(s), int(pos0),
                                     _h(posbuf), int(opos_i32), int(nheads), int(nkv),
-                                    int(head_dim)))
+                                    int(head_dim), int(ldq)))
 
 
 def decode_attention(ctx: Context, a: Buffer, oq: int, ok: int, ov: int, oinv: int, kv: Buffer,

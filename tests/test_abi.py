@@ -318,6 +318,48 @@ def test_gemm_activation_buffer_limit(hctx):
     assert c == Q8_ERR_SHAPE and "activation buffer" in msg
 
 
+def test_qkv_row_stride_validation(hctx):
+    """Row strides of q8_rope_kv / q8_attention: 0 or at least each row
+    width; k's columns may not meet q's at the stride; the q rows' span,
+    not s * qd, must fit the arena."""
+    nh, nkv, hd, s, maxlen = 8, 2, 64, 16, 64
+    qd, kvd = nh * hd, nkv * hd
+    ld = qd + 2 * kvd
+    a = hctx.alloc(4 * (s * ld + hd + 2 * s * qd))
+    kv = hctx.alloc(2 * 2 * maxlen * kvd)
+    blk = maxlen * kvd
+    oinv = s * ld
+
+    def rope(oq, ok, ov, ld_):
+        return code_of(q8hip.rope_kv, hctx, a, oq, ok, ov, oinv, kv, 0, blk, maxlen, s, 0, nh,
+                       nkv, hd, ld=ld_)
+
+    assert rope(0, qd, qd + kvd, ld)[0] == Q8_ERR_NODEVICE
+    assert rope(0, qd, qd + kvd, 0)[0] == Q8_ERR_ARG           # dense spans overlap
+    assert rope(0, qd, qd + kvd, qd - 1)[0] == Q8_ERR_SHAPE
+    assert rope(0, qd, qd + kvd, -ld)[0] == Q8_ERR_SHAPE
+    c, msg = rope(0, qd - 1, qd + kvd, ld)                     # k's first column is q's last
+    assert c == Q8_ERR_ARG and "stride" in msg
+    assert rope(0, ld - kvd + 1, qd + kvd, ld)[0] == Q8_ERR_ARG   # k wraps into the next q row
+    assert rope(qd + kvd, 2 * qd + kvd, 0, ld)[0] == Q8_ERR_NODEVICE  # rows rotated, k after q
+    assert rope(kvd, 0, qd + kvd, ld)[0] == Q8_ERR_NODEVICE   # k before q in each row
+    na = s * ld + hd + 2 * s * qd                               # arena floats
+    assert rope(na - (s - 1) * ld - qd, 0, 0, ld)[0] != Q8_ERR_RANGE
+    assert rope(na - (s - 1) * ld - qd + 1, 0, 0, ld)[0] == Q8_ERR_RANGE   # last q row past it
+
+    def attn(oq, ldq):
+        return code_of(q8hip.attention, hctx, a, oq, kv, 0, blk, maxlen, oinv + hd, 0, s, 0,
+                       nh, nkv, hd, ldq=ldq)
+
+    assert attn(0, ld)[0] == Q8_ERR_NODEVICE
+    assert attn(0, qd - 1)[0] == Q8_ERR_SHAPE
+    assert attn(2 * kvd, ld)[0] == Q8_ERR_NODEVICE
+    # a span that reaches the output
+    assert attn(oinv + hd - (s - 1) * ld - qd + 1, ld)[0] == Q8_ERR_ARG
+    for b in (a, kv):
+        b.free()
+
+
 @pytest.mark.parametrize("which", ["rope_kv", "attention"])
 def test_kv_cache_block_under_2gib(hctx, which):
     """The attention kernels address a K or V block with 32-bit buffer

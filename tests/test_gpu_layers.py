@@ -149,6 +149,56 @@ def test_attention(ctx, head_dim, nh, nkv, s, pos0):
         b.free()
 
 
+@pytest.mark.parametrize("head_dim,nh,nkv,s", [(64, 8, 2, 3), (128, 32, 8, 48),
+                                               (64, 32, 8, 130)])
+def test_stacked_qkv_rows_equal_dense(ctx, head_dim, nh, nkv, s):
+    """q|k|v stacked in the rows of one linear output (row stride
+    qd + 2*kvd): RoPE leaves the same q and k bits in place and writes the
+    same cache bits as on dense q, k, v, and attention over the stacked q
+    gives the same output bits as over the dense q (the few-row split path
+    at 3 rows, the one-pass path at 48 and 130)."""
+    say("stacked q|k|v", head_dim, nh, nkv, s)
+    rng = np.random.default_rng(11)
+    pos0, maxlen = 7, 256
+    qd, kvd = nh * head_dim, nkv * head_dim
+    ld = qd + 2 * kvd
+    inv = mo.llama3_inv_freq(head_dim, 500000.0, 32.0, 1.0, 4.0, 8192.0)
+    rows = rng.standard_normal((s, ld)).astype(np.float32)
+    q, k, v = rows[:, :qd], rows[:, qd:qd + kvd], rows[:, qd + kvd:]
+    od = s * ld                                 # dense q, k, v after the stacked rows
+    oq, ok, ov = od, od + s * qd, od + s * qd + s * kvd
+    oinv = ov + s * kvd
+    scr = q8hip.attention_scratch_floats(s, nh, head_dim, maxlen)
+    oy1, oy2 = oinv + head_dim, oinv + head_dim + s * qd
+    osc = oy2 + s * qd
+    a = arena(ctx, osc + scr)
+    put(a, 0, rows)
+    put(a, oq, np.ascontiguousarray(q))
+    put(a, ok, np.ascontiguousarray(k))
+    put(a, ov, np.ascontiguousarray(v))
+    put(a, oinv, inv)
+    kv = ctx.alloc(4 * 2 * maxlen * kvd)
+    kv.upload(np.zeros(4 * maxlen * kvd, np.float16))
+    blk = maxlen * kvd
+    q8hip.rope_kv(ctx, a, 0, qd, qd + kvd, oinv, kv, 0, blk, maxlen, s, pos0, nh, nkv, head_dim,
+                  ld=ld)
+    q8hip.rope_kv(ctx, a, oq, ok, ov, oinv, kv, 2 * blk, 3 * blk, maxlen, s, pos0, nh, nkv,
+                  head_dim)
+    st = get(a, 0, (s, ld))
+    assert np.array_equal(st[:, :qd], get(a, oq, (s, qd)))
+    assert np.array_equal(st[:, qd:qd + kvd], get(a, ok, (s, kvd)))
+    assert np.array_equal(st[:, qd + kvd:], v)               # v is only read
+    c = kv.download((4, blk), np.float16)
+    assert np.array_equal(c[0], c[2]) and np.array_equal(c[1], c[3])
+    assert np.any(c[0] != 0)
+    q8hip.attention(ctx, a, 0, kv, 0, blk, maxlen, oy1, osc, s, pos0, nh, nkv, head_dim, ldq=ld)
+    q8hip.attention(ctx, a, oq, kv, 2 * blk, 3 * blk, maxlen, oy2, osc, s, pos0, nh, nkv,
+                    head_dim)
+    assert np.array_equal(get(a, oy1, (s, qd)), get(a, oy2, (s, qd)))
+    for b in (a, kv):
+        b.free()
+
+
 @pytest.mark.parametrize("head_dim,nh,nkv", [(128, 32, 8), (64, 8, 8)])
 def test_attention_prompt_rows_any_q_scale(ctx, head_dim, nh, nkv):
     """The multi-row (s >= 16) path splits q into binary16 hi + lo after a
