@@ -61,6 +61,7 @@ __device__ __forceinline__ int weight_row_exponent(float mx) {
 // only (nwb = 0 otherwise).
 // SWIGLU (f32 x): x holds gate rows and up the matching up rows; the values
 // converted are silu(gate) * up, computed as swiglu_kernel computes them.
+// Row r of x (and of up) starts ldx elements after row r-1.
 template <bool XF32, int CH, int G, bool SWIGLU = false>
 __global__ __launch_bounds__(256) void act16_kernel(const void *__restrict__ xv, int64_t s,
                                                     int64_t m, uint16_t *__restrict__ x16,
@@ -68,7 +69,7 @@ __global__ __launch_bounds__(256) void act16_kernel(const void *__restrict__ xv,
                                                     const uint8_t *__restrict__ w,
                                                     int64_t row_bytes, int64_t n,
                                                     int *__restrict__ ew,
-                                                    const float *__restrict__ up) {
+                                                    const float *__restrict__ up, int64_t ldx) {
   __shared__ float red[4];
   const int64_t r = blockIdx.x;
   const int tid = threadIdx.x;
@@ -86,7 +87,7 @@ __global__ __launch_bounds__(256) void act16_kernel(const void *__restrict__ xv,
   // 8 consecutive values per step (m is a multiple of 8)
   auto load8 = [&](int64_t k, float (&v)[8]) {
     if constexpr (XF32) {
-      const f32x4 *p = reinterpret_cast<const f32x4 *>(static_cast<const float *>(xv) + r * m + k);
+      const f32x4 *p = reinterpret_cast<const f32x4 *>(static_cast<const float *>(xv) + r * ldx + k);
       const f32x4 a = p[0], b = p[1];
 #pragma unroll
       for (int c = 0; c < 4; ++c) {
@@ -94,7 +95,7 @@ __global__ __launch_bounds__(256) void act16_kernel(const void *__restrict__ xv,
         v[4 + c] = b[c];
       }
       if constexpr (SWIGLU) {
-        const f32x4 *pu = reinterpret_cast<const f32x4 *>(up + r * m + k);
+        const f32x4 *pu = reinterpret_cast<const f32x4 *>(up + r * ldx + k);
         const f32x4 ua = pu[0], ub = pu[1];
 #pragma unroll
         for (int c = 0; c < 4; ++c) {
@@ -103,7 +104,7 @@ __global__ __launch_bounds__(256) void act16_kernel(const void *__restrict__ xv,
         }
       }
     } else {
-      const u32x4 d = *reinterpret_cast<const u32x4 *>(static_cast<const uint16_t *>(xv) + r * m + k);
+      const u32x4 d = *reinterpret_cast<const u32x4 *>(static_cast<const uint16_t *>(xv) + r * ldx + k);
 #pragma unroll
       for (int c = 0; c < 4; ++c) {
         v[2 * c] = __builtin_bit_cast(float, d[c] << 16);
@@ -178,7 +179,7 @@ void launch_act16(const LinearArgs &a, uint16_t *x16, int *ex, int *ew, int64_t 
   const dim3 grid((unsigned)(a.s + (nw + 3) / 4)), block(256);
 #define Q8_ACT16(CH)                                                                          \
   hipLaunchKernelGGL((act16_kernel<XF32, CH, G, SWIGLU>), grid, block, 0, st, a.x, a.s, a.m,  \
-                     x16, ex, a.w, a.row_bytes, nw, ew, a.up)
+                     x16, ex, a.w, a.row_bytes, nw, ew, a.up, a.ldx ? a.ldx : a.m)
   if (a.m <= 2048)
     Q8_ACT16(1);
   else if (a.m <= 4096)

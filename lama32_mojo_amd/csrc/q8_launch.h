@@ -37,6 +37,7 @@ struct LinearArgs {
   // [s, m] sit at up, and the linear reads silu(gate) * up (the values
   // swiglu_kernel stores).
   const float *up = nullptr;
+  int64_t ldx = 0;   // GEMM only: row stride of x (and up) in elements; 0: m
 };
 // Decode path (s small, f32 x): VALU GEMV.
 hipError_t launch_gemv(const LinearArgs &a, hipStream_t st);

@@ -454,14 +454,15 @@ hipError_t run_gemm_in(q8::LinearArgs la, void *act16, int64_t bytes, hipStream_
   int *ex = reinterpret_cast<int *>(base + rows * la.m * 2);
   int *ew = reinterpret_cast<int *>(base + bytes - (4 * la.n + 255) / 256 * 256);
   const int64_t xb = la.x_is_bf16 ? 2 : 4;
+  const int64_t ldx = la.ldx ? la.ldx : la.m;
   const uint8_t *x0 = static_cast<const uint8_t *>(la.x);
   const float *u0 = la.up;
   float *y0 = la.y;
   const int64_t s = la.s;
   for (int64_t r0 = 0; r0 < s; r0 += rows) {
     la.s = s - r0 < rows ? s - r0 : rows;
-    la.x = x0 + r0 * la.m * xb;
-    if (u0) la.up = u0 + r0 * la.m;
+    la.x = x0 + r0 * ldx * xb;
+    if (u0) la.up = u0 + r0 * ldx;
     la.y = y0 + r0 * la.n;
     hipError_t e = q8::launch_gemm(la, x16, ex, ew, r0 == 0, st);
     if (e != hipSuccess) return e;
@@ -831,14 +832,23 @@ int q8_linear_fused(q8_ctx *ctx, q8_buf *w, uint64_t owt_u16, q8_buf *a, uint64_
   return ok(ctx);
 }
 
+// Floats spanned by s rows of `width` floats at a row stride of ld.
+static uint64_t rows_span(int64_t s, int64_t ld, uint64_t width) {
+  return s == 0 ? 0 : (uint64_t)(s - 1) * (uint64_t)ld + width;
+}
+
 int q8_linear_swiglu(q8_ctx *ctx, q8_buf *w, uint64_t owt_u16, q8_buf *a, uint64_t og_f32,
                      uint64_t ou_f32, uint64_t oy_f32, int64_t s, int64_t m, int64_t n, int G,
-                     int scale_dtype) {
+                     int scale_dtype, int64_t ld) {
   if (int rc = check_ctx(ctx)) return rc;
   if (int rc = check_linear(ctx, "q8_linear_swiglu", w, owt_u16, s, m, n, G, scale_dtype))
     return rc;
   if (!a) return fail(ctx, Q8_ERR_ARG, "q8_linear_swiglu: null activation buffer");
-  const uint64_t nx = (uint64_t)s * (uint64_t)m, ny = (uint64_t)s * (uint64_t)n;
+  if (ld != 0 && (ld < m || ld > INT32_MAX))
+    return fail(ctx, Q8_ERR_SHAPE, "q8_linear_swiglu: row stride %lld (0, or at least m=%lld)",
+                (long long)ld, (long long)m);
+  if (ld == 0) ld = m;
+  const uint64_t nx = rows_span(s, ld, (uint64_t)m), ny = (uint64_t)s * (uint64_t)n;
   if (int rc = check_f32(ctx, a, og_f32, nx, "q8_linear_swiglu", "gate")) return rc;
   if (int rc = check_f32(ctx, a, ou_f32, nx, "q8_linear_swiglu", "up")) return rc;
   if (int rc = check_f32(ctx, a, oy_f32, ny, "q8_linear_swiglu", "y")) return rc;
@@ -864,9 +874,10 @@ int q8_linear_swiglu(q8_ctx *ctx, q8_buf *w, uint64_t owt_u16, q8_buf *a, uint64
   la.n = n;
   la.G = G;
   la.kind = scale_dtype;
-  if (!gemm_aligned(la) || reinterpret_cast<uintptr_t>(la.up) % 16 != 0)
+  la.ldx = ld;
+  if (!gemm_aligned(la) || reinterpret_cast<uintptr_t>(la.up) % 16 != 0 || ld % 4 != 0)
     return fail(ctx, Q8_ERR_UNSUPPORTED, "q8_linear_swiglu: gate, up and the weight rows must "
-                "be 16-byte aligned, m a multiple of 8");
+                "be 16-byte aligned, m a multiple of 8, the row stride a multiple of 4");
   if (ctx->host_only) return fail(ctx, Q8_ERR_NODEVICE, "q8_linear_swiglu: host-only context");
   if (n == 0) return ok(ctx);
   if (int rc = set_device(ctx)) return rc;
@@ -1003,11 +1014,6 @@ int q8_add_rmsnorm(q8_ctx *ctx, q8_buf *w, uint64_t owt_u16, q8_buf *a, uint64_t
                                     fptr(a, oy_f32), rows, d, eps, ctx->stream);
   if (e != hipSuccess) return hip_fail(ctx, e, "q8_add_rmsnorm launch");
   return ok(ctx);
-}
-
-// Floats spanned by s rows of `width` floats at a row stride of ld.
-static uint64_t rows_span(int64_t s, int64_t ld, uint64_t width) {
-  return s == 0 ? 0 : (uint64_t)(s - 1) * (uint64_t)ld + width;
 }
 
 int q8_rope_kv(q8_ctx *ctx, q8_buf *a, uint64_t oq_f32, uint64_t ok_f32, uint64_t ov_f32,

@@ -352,17 +352,19 @@ class Q8Llama:
             oh = a.alloc(s * H)
         oz = a.alloc(s * H)
         q8hip.add_rmsnorm(ctx, w.buf, lo.post_norm, a.buf, ox, oo, oh, oz, s, H, cfg.eps)
-        if s == 1 and lo.up == lo.gate + I * rsH:
-            og = self.linear(oz, 1, H, lo.gate, 2 * I)
+        gu_stacked = lo.up == lo.gate + I * rsH and (s == 1 or (s >= 32 and I % 4 == 0))
+        if gu_stacked:
+            og = self.linear(oz, s, H, lo.gate, 2 * I)
             ou = og + I
         else:
             og = self.linear(oz, s, H, lo.gate, I)
             ou = self.linear(oz, s, H, lo.up, I)
         if s >= 32 and og % 4 == 0 and ou % 4 == 0:
-            # prompt rows: the swiglu folded into the down GEMM's pre-pass
+            # prompt rows: the swiglu folded into the down GEMM's pre-pass,
+            # gate|up rows read at their stride when stacked
             om = a.alloc(s * H)
             q8hip.linear_swiglu(ctx, w.buf, lo.down, a.buf, og, ou, om, s, I, H, self.G,
-                                self.scale)
+                                self.scale, ld=2 * I if gu_stacked else 0)
         else:
             q8hip.swiglu(ctx, a.buf, og, ou, s * I)
             om = self.linear(og, s, I, lo.down, H)

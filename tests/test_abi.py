@@ -113,8 +113,17 @@ def test_linear_swiglu_validation(hctx):
     assert code_of(L, hctx, w, 0, a, og, ou, oy + 8, s, m, n)[0] == Q8_ERR_RANGE
     assert code_of(L, hctx, w, 0, a, og + 1, ou, oy, s, m, n)[0] == q8hip.Q8_ERR_UNSUPPORTED
     assert code_of(L, hctx, w, 8, a, og, ou, oy, s, m, n)[0] == Q8_ERR_RANGE    # rows past w
+    # gate|up stacked in rows of ld >= 2m (ou = og + m); y after s rows of 2m + 8
+    a2 = hctx.alloc(4 * (s * (2 * m + 8) + s * n))
+    oy2 = s * (2 * m + 8)
+    for og2, ld, want in ((0, 2 * m, Q8_ERR_NODEVICE), (0, m - 4, Q8_ERR_SHAPE),
+                          (0, 2 * m + 2, q8hip.Q8_ERR_UNSUPPORTED),   # rows not 16-byte aligned
+                          (8, 2 * m + 8, Q8_ERR_NODEVICE),            # the last up row ends at y
+                          (12, 2 * m + 8, Q8_ERR_ARG)):               # ... and one past it
+        assert code_of(L, hctx, w, 0, a2, og2, og2 + m, oy2, s, m, n, ld=ld)[0] == want, ld
     w.free()
     a.free()
+    a2.free()
 
 
 def test_linear_fused_validation(hctx):

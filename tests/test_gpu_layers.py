@@ -442,7 +442,8 @@ def test_linear_swiglu_equals_swiglu_then_linear(ctx, G, scale, s, m, n):
     gives the bits of q8_swiglu into g followed by q8_linear on g, and leaves
     g and u unchanged: 2048..20480-code rows (the pre-pass holding up to 8
     chunks per thread in registers, and past 16384 re-reading the row),
-    ragged row counts."""
+    ragged row counts.  Gate|up stacked in rows of 2m (one linear's output,
+    read at a row stride) give the same bits."""
     say("linear_swiglu", G, scale, s, m, n)
     rng = np.random.default_rng(s + m)
     rs = q8hip.rowstride_u16(m, G, scale)
@@ -454,12 +455,17 @@ def test_linear_swiglu_equals_swiglu_then_linear(ctx, G, scale, s, m, n):
     g = (2 * rng.standard_normal((s, m))).astype(np.float32)
     u = rng.standard_normal((s, m)).astype(np.float32)
     og, ou, oy1, oy2 = 0, s * m, 2 * s * m, 2 * s * m + s * n
-    a = arena(ctx, 2 * s * m + 2 * s * n)
+    ost = (2 * s * m + 2 * s * n + 3) // 4 * 4       # stacked rows [g | u]
+    oy3 = ost + 2 * s * m
+    a = arena(ctx, oy3 + s * n)
     try:
         put(a, og, g)
         put(a, ou, u)
+        put(a, ost, np.concatenate([g, u], axis=1))
         q8hip.linear_swiglu(ctx, w, 0, a, og, ou, oy2, s, m, n, G, scale)
         got = get(a, oy2, (s, n))
+        q8hip.linear_swiglu(ctx, w, 0, a, ost, ost + m, oy3, s, m, n, G, scale, ld=2 * m)
+        assert np.array_equal(get(a, oy3, (s, n)), got)
         assert np.array_equal(get(a, og, (s, m)), g) and np.array_equal(get(a, ou, (s, m)), u)
         q8hip.swiglu(ctx, a, og, ou, s * m)
         q8hip.linear(ctx, w, 0, a, og, oy1, s, m, n, G, scale)
