@@ -212,14 +212,12 @@ int q8_linear_fused(q8_ctx *ctx, q8_buf *w, uint64_t owt_u16, q8_buf *a,
  * q8_linear); g, u and the weight rows 16-byte aligned, m a multiple of 8.
  * Row i of g and of u starts at og + i*ld and ou + i*ld (ld = 0: m; else
  * at least m and a multiple of 4 -- gate|up from one stacked q8_linear of
- * 2m outputs: ou = og + m, ld = 2m).  accumulate = 1: y += W (silu(g) * u)
- * (the residual add of the block, the same bits as q8_add of the product
- * into y); 0: y = W (silu(g) * u).
- * Replaces swiglu_mul_op + the down projection's mm_q8_op (+ k_add) of
- * run_layer_q8 (src/llama_q8.mojo:221-229) for prompt rows. */
+ * 2m outputs: ou = og + m, ld = 2m).
+ * Replaces swiglu_mul_op + the down projection's mm_q8_op of run_layer_q8
+ * (src/llama_q8.mojo:221-225) for prompt rows. */
 int q8_linear_swiglu(q8_ctx *ctx, q8_buf *w, uint64_t owt_u16, q8_buf *a, uint64_t og_f32,
                      uint64_t ou_f32, uint64_t oy_f32, int64_t s, int64_t m, int64_t n, int G,
-                     int scale_dtype, int64_t ld, int accumulate);
+                     int scale_dtype, int64_t ld);
 
 /* The end of a token step in two launches: logits y (n floats at oy) = W
  * rmsnorm(x) over the lm_head's n packed rows (norm weights at onorm of w;

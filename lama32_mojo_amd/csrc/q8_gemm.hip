@@ -241,7 +241,7 @@ __global__ __launch_bounds__(64 * (4 + NPW)) __attribute__((amdgpu_waves_per_eu(
 void gemm_kernel(const uint8_t *__restrict__ w, int64_t row_bytes,
                     const uint16_t *__restrict__ x16, const int *__restrict__ ex,
                     const int *__restrict__ ew, float *__restrict__ y, int64_t s, int64_t m,
-                    int64_t n, int nit, float *__restrict__ ws, int accum) {
+                    int64_t n, int nit, float *__restrict__ ws) {
   constexpr int BM = 32 * TM, BN = 128 * TN;
   constexpr int SB = ScaleTraits<KIND>::bytes;
   constexpr int NPT = 64 * NPW;                  // producer threads
@@ -393,9 +393,7 @@ void gemm_kernel(const uint8_t *__restrict__ w, int64_t row_bytes,
   }
   // D layout of v_mfma_f32_32x32x16: lane -> column lane % 32, element v ->
   // row 8 (v / 4) + 4 (lane / 32) + v % 4; each output scaled by 2^(e_i + f_j)
-  // (accum: y += the product, when this launch writes y itself)
   const int rows_left = (int)(s - m0 - lh * 4);
-  const bool add_y = accum && gridDim.z == 1;
 #pragma unroll
   for (int t = 0; t < TN; ++t) {
     const int jc = cb + t * 32 + lr;
@@ -407,23 +405,18 @@ void gemm_kernel(const uint8_t *__restrict__ w, int64_t row_bytes,
 #pragma unroll
         for (int v = 0; v < 16; ++v) {
           const int r = i * 32 + (v >> 2) * 8 + (v & 3);
-          if (r < rows_left) {
-            float val = __builtin_ldexpf(acc[i][t][v], exs[r + lh * 4] + ews[jc]);
-            if (add_y) val += out[(int64_t)r * n];
-            out[(int64_t)r * n] = val;
-          }
+          if (r < rows_left) out[(int64_t)r * n] = __builtin_ldexpf(acc[i][t][v], exs[r + lh * 4] + ews[jc]);
         }
     }
   }
 }
 
-// y[i] = sum over splits z (in order) of ws[z][i] (accum: y[i] plus that
-// sum); four outputs per thread.
+// y[i] = sum over splits z (in order) of ws[z][i]; four outputs per thread.
 // The loads of up to 8 splits are issued before their adds, so a thread
 // waits for one memory round trip per 8 splits rather than one per split.
 __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float *__restrict__ ws,
                                                             float *__restrict__ y, int64_t count,
-                                                            int splits, int accum) {
+                                                            int splits) {
   const int64_t i = 4 * ((int64_t)blockIdx.x * blockDim.x + threadIdx.x);
   if (i >= count) return;
   if (i + 4 <= count && (count & 3) == 0) {
@@ -446,13 +439,12 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float *__restr
     }
 #pragma unroll
     for (int u = 0; u < 7; ++u) v = z + u < splits ? v + t[u] : v;
-    if (accum) v += *reinterpret_cast<const f32x4 *>(y + i);
     *reinterpret_cast<f32x4 *>(y + i) = v;
   } else {
     for (int64_t e = i; e < i + 4 && e < count; ++e) {
       float v = ws[e];
       for (int z = 1; z < splits; ++z) v += ws[z * count + e];
-      y[e] = accum ? v + y[e] : v;
+      y[e] = v;
     }
   }
 }
@@ -474,8 +466,8 @@ hipError_t launch_t(const LinearArgs &a, const uint16_t *x16, const int *ex, con
   int64_t nit = (nit_all + splits - 1) / splits;
   dim3 grid((unsigned)gx, (unsigned)gy, (unsigned)splits), block(64 * (4 + kProducerWaves));
   hipLaunchKernelGGL((gemm_kernel<G, KIND, TM, TN>), grid, block, 0, st, a.w, a.row_bytes,
-                     x16, ex, ew, a.y, a.s, a.m, a.n, (int)nit, a.ws, a.accum);
-  if (splits > 1) return launch_splitk_reduce(a.ws, a.y, a.s * a.n, (int)splits, a.accum, st);
+                     x16, ex, ew, a.y, a.s, a.m, a.n, (int)nit, a.ws);
+  if (splits > 1) return launch_splitk_reduce(a.ws, a.y, a.s * a.n, (int)splits, st);
   return hipGetLastError();
 }
 
@@ -503,11 +495,11 @@ hipError_t launch_g(const LinearArgs &a, uint16_t *x16, int *ex, int *ew, bool w
 
 }  // namespace
 
-hipError_t launch_splitk_reduce(const float *ws, float *y, int64_t count, int splits, int accum,
+hipError_t launch_splitk_reduce(const float *ws, float *y, int64_t count, int splits,
                                 hipStream_t st) {
   const int64_t threads = (count + 3) / 4;
   hipLaunchKernelGGL(splitk_reduce_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0,
-                     st, ws, y, count, splits, accum);
+                     st, ws, y, count, splits);
   return hipGetLastError();
 }
 

@@ -38,7 +38,6 @@ struct LinearArgs {
   // swiglu_kernel stores).
   const float *up = nullptr;
   int64_t ldx = 0;   // GEMM only: row stride of x (and up) in elements; 0: m
-  int accum = 0;     // GEMM only: y += the product instead of y = it
 };
 // Decode path (s small, f32 x): VALU GEMV.
 hipError_t launch_gemv(const LinearArgs &a, hipStream_t st);
@@ -80,7 +79,7 @@ hipError_t launch_gemv_fused(const FusedLinearArgs &a, hipStream_t st);
 hipError_t launch_gemm(const LinearArgs &a, uint16_t *x16, int *ex, int *ew, bool weights,
                        hipStream_t st);
 // y[i] = sum over z < splits of ws[z * count + i] (split-K partial sums).
-hipError_t launch_splitk_reduce(const float *ws, float *y, int64_t count, int splits, int accum,
+hipError_t launch_splitk_reduce(const float *ws, float *y, int64_t count, int splits,
                                 hipStream_t st);
 // Small batches (s <= 32, f32 x; the C ABI sends it 5 <= s < 32): bf16 MFMA
 // over zero-padded 16-row tiles with x split into two bf16 terms.

@@ -839,13 +839,11 @@ static uint64_t rows_span(int64_t s, int64_t ld, uint64_t width) {
 
 int q8_linear_swiglu(q8_ctx *ctx, q8_buf *w, uint64_t owt_u16, q8_buf *a, uint64_t og_f32,
                      uint64_t ou_f32, uint64_t oy_f32, int64_t s, int64_t m, int64_t n, int G,
-                     int scale_dtype, int64_t ld, int accumulate) {
+                     int scale_dtype, int64_t ld) {
   if (int rc = check_ctx(ctx)) return rc;
   if (int rc = check_linear(ctx, "q8_linear_swiglu", w, owt_u16, s, m, n, G, scale_dtype))
     return rc;
   if (!a) return fail(ctx, Q8_ERR_ARG, "q8_linear_swiglu: null activation buffer");
-  if (accumulate != 0 && accumulate != 1)
-    return fail(ctx, Q8_ERR_ARG, "q8_linear_swiglu: accumulate=%d (0 or 1)", accumulate);
   if (ld != 0 && (ld < m || ld > INT32_MAX))
     return fail(ctx, Q8_ERR_SHAPE, "q8_linear_swiglu: row stride %lld (0, or at least m=%lld)",
                 (long long)ld, (long long)m);
@@ -877,7 +875,6 @@ int q8_linear_swiglu(q8_ctx *ctx, q8_buf *w, uint64_t owt_u16, q8_buf *a, uint64
   la.G = G;
   la.kind = scale_dtype;
   la.ldx = ld;
-  la.accum = accumulate;
   if (!gemm_aligned(la) || reinterpret_cast<uintptr_t>(la.up) % 16 != 0 || ld % 4 != 0)
     return fail(ctx, Q8_ERR_UNSUPPORTED, "q8_linear_swiglu: gate, up and the weight rows must "
                 "be 16-byte aligned, m a multiple of 8, the row stride a multiple of 4");

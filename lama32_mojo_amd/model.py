@@ -360,15 +360,15 @@ class Q8Llama:
             og = self.linear(oz, s, H, lo.gate, I)
             ou = self.linear(oz, s, H, lo.up, I)
         if s >= 32 and og % 4 == 0 and ou % 4 == 0:
-            # prompt rows: the swiglu folded into the down GEMM's pre-pass
-            # (gate|up rows read at their stride when stacked) and the
-            # residual add into its epilogue
-            q8hip.linear_swiglu(ctx, w.buf, lo.down, a.buf, og, ou, oh, s, I, H, self.G,
-                                self.scale, ld=2 * I if gu_stacked else 0, accumulate=True)
+            # prompt rows: the swiglu folded into the down GEMM's pre-pass,
+            # gate|up rows read at their stride when stacked
+            om = a.alloc(s * H)
+            q8hip.linear_swiglu(ctx, w.buf, lo.down, a.buf, og, ou, om, s, I, H, self.G,
+                                self.scale, ld=2 * I if gu_stacked else 0)
         else:
             q8hip.swiglu(ctx, a.buf, og, ou, s * I)
             om = self.linear(og, s, I, lo.down, H)
-            q8hip.add(ctx, a.buf, om, oh, s * H)
+        q8hip.add(ctx, a.buf, om, oh, s * H)
         return oh
 
     def _layer_fused(self, L: int, ox: int, pos0: int, pb, oh: int | None) -> int:

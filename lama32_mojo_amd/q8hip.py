@@ -105,7 +105,7 @@ SIGNATURES = {
     "q8_decode_attention": (_I, [_P, _P, _U64, _U64, _U64, _U64, _P, _U64, _U64, _I64, _U64,
                                 _I64, _P, _U64, _I, _I, _I, _P, _U64, _U64, ctypes.c_float]),
     "q8_linear_swiglu": (_I, [_P, _P, _U64, _P, _U64, _U64, _U64, _I64, _I64, _I64, _I, _I,
-                              _I64, _I]),
+                              _I64]),
     "q8_swiglu": (_I, [_P, _P, _U64, _U64, _I64]),
     "q8_res_add": (_I, [_P, _P, _U64, _U64, _U64, _I64]),
     "q8_add": (_I, [_P, _P, _U64, _U64, _I64]),
@@ -293,13 +293,13 @@ def linear(ctx: Context, w: Buffer, owt_u16: int, a: Buffer, ox_f32: int, oy_f32
 
 def linear_swiglu(ctx: Context, w: Buffer, owt_u16: int, a: Buffer, og_f32: int, ou_f32: int,
                   oy_f32: int, s: int, m: int, n: int, G: int = 64, scale="f16",
-                  ld: int = 0, accumulate: bool = False) -> None:
-    """y = W (silu(g) * u) (accumulate: y += it) over s >= 32 rows, the
-    swiglu folded into the GEMM's binary16 pre-pass: q8_linear_swiglu (ld:
-    row stride of g and u, 0 for m)."""
+                  ld: int = 0) -> None:
+    """y = W (silu(g) * u) over s >= 32 rows, the swiglu folded into the
+    GEMM's binary16 pre-pass: q8_linear_swiglu (ld: row stride of g and u,
+    0 for m)."""
     ctx.check(ctx._lib.q8_linear_swiglu(ctx.h, w.h, int(owt_u16), a.h, int(og_f32), int(ou_f32),
                                         int(oy_f32), int(s), int(m), int(n), int(G),
-                                        scale_code(scale), int(ld), int(bool(accumulate))))
+                                        scale_code(scale), int(ld)))
 
 
 PRE_NONE, PRE_RMSNORM, PRE_SWIGLU = 0, 1, 2
