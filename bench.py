@@ -591,8 +591,10 @@ def run_e2e_8b(B: Bench, prompt: int = 2048, gen: int = 256, rooflines: bool = T
         "dtype": "int8xf32",
         "data": "synthetic (random-init N(0,0.02) bf16 weights packed on GPU, norms ~1; "
                 "random prompt ids, seed 3)",
-        "config": {"workload": f"{cfg.name} end to end: prefill {prompt} ids (7 Q8 GEMMs per "
-                               "layer as f16-MFMA dequant-GEMMs, RoPE + "
+        "config": {"workload": f"{cfg.name} end to end: prefill {prompt} ids (the 7 Q8 "
+                               "projections per layer as 4 f16-MFMA dequant-GEMMs: "
+                               "q|k|v and gate|up stacked, the swiglu in the down "
+                               "GEMM's pre-pass; RoPE + "
                                "fp16 KV append, causal attention), then "
                                f"{gen} greedy steps of the captured decode graph",
                    "layout": f"G={G} {scale} scales", "batch": 1,
