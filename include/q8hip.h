@@ -115,10 +115,14 @@ int q8_quantize_pack(q8_ctx *ctx, q8_buf *src, uint64_t src_off, int src_dtype,
  * at f32 offset oy of the activation arena `a`, and W's packed rows at u16
  * offset owt of the weight arena `w` -- the k_mm_q8 / mm_q8_op contract
  * (src/llama_q8.mojo:54-93,124-141).  y must not overlap x.  The caller
- * allocates y (Acts.alloc), as mm_q8_op does.  Rows s < 32 run f32-exact
- * products (GEMV, or MFMA on two bf16 terms of x); s >= 32 runs the
- * dequant-GEMM on f16 MFMA (binary16 x rows after a power-of-two scaling,
- * binary16 q * s), whose max-rel-err stays near 2e-4. */
+ * allocates y (Acts.alloc), as mm_q8_op does.  One row runs the f32 GEMV
+ * and 2 .. 4 rows f32 4x4-block MFMA, both with f32 products of x and the
+ * codes; 5 .. 31 rows split each x into two bf16 terms hi + lo (x - hi - lo
+ * below 2^-17 |x|, so x is carried to that bound, not exactly) whose
+ * products with the codes are exact on bf16 MFMA; all three stay within
+ * 1e-5 of float64.  s >= 32 runs the dequant-GEMM on f16 MFMA (binary16 x
+ * rows after a power-of-two scaling, binary16 q * s), whose max-rel-err
+ * stays near 2e-4. */
 int q8_linear(q8_ctx *ctx, q8_buf *w, uint64_t owt_u16, q8_buf *a,
               uint64_t ox_f32, uint64_t oy_f32, int64_t s, int64_t m, int64_t n,
               int G, int scale_dtype);
@@ -142,11 +146,14 @@ int q8_linear_bf16act(q8_ctx *ctx, q8_buf *w, uint64_t owt_u16, q8_buf *x,
  * from s = 32 on when the rows do not fit the 16 MiB activation buffer at
  * once: they then run in chunks, within the same 1e-3 contract), on
  * hip_stream (NULL: the null stream), which must belong to the current
- * device.  w points at packed row 0 (rows back to back); x and y are f32
- * and must not overlap.
- * Scratch: one fixed array of Q8_NOALLOC_SCRATCH_BYTES per GPU, held until
- * the process ends (16 MiB of split-K partials and a 16 MiB binary16
- * activation buffer for s >= 32, which takes the rows in chunks).
+ * device.  w points at packed row 0 (rows back to back) and must be 2-byte
+ * aligned; x and y are f32, 4-byte aligned, and must not overlap (else
+ * Q8_ERR_ARG).
+ * Scratch: one fixed __device__ array of Q8_NOALLOC_SCRATCH_BYTES (32 MiB)
+ * per GPU, resident on every GPU where the library's code object is loaded
+ * until the process ends, used or not (16 MiB of split-K partials and a
+ * 16 MiB binary16 activation buffer for s >= 32, which takes the rows in
+ * chunks).
  * Limit: from s = 32 on, one activation row (2 m + 4 bytes) plus 4 n bytes
  * must fit in 16 MiB, else Q8_ERR_SHAPE.  Every call on a GPU shares that
  * GPU's array: calls that overlap on one GPU (two streams, two threads)

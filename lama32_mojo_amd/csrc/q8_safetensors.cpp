@@ -25,18 +25,24 @@
 
 #include <algorithm>
 #include <cerrno>
+#include <chrono>
 #include <cstdarg>
 #include <cstdint>
 #include <cstdio>
 #include <cstring>
 #include <map>
 #include <memory>
+#include <mutex>
 #include <string>
+#include <thread>
 #include <vector>
 
 #include "../../include/q8hip.h"
 
 namespace {
+
+constexpr int kReadAttempts = 15;     // reads of one tensor range, first included
+constexpr int kReadRetryMs = 2000;    // between two attempts
 
 thread_local std::string g_err;
 
@@ -303,17 +309,33 @@ bool shape_bytes(const std::vector<int64_t> &shape, int bits, uint64_t &bytes) {
   return true;
 }
 
-bool read_all(int fd, uint64_t off, void *dst, uint64_t n) {
+// Reads n bytes at off, advancing *done past what arrived; returns 0, the
+// errno of a failed read, or -1 when the file ends first.
+int read_some(int fd, uint64_t off, void *dst, uint64_t n, uint64_t *done) {
   char *d = static_cast<char *>(dst);
-  while (n > 0) {
-    const ssize_t r = pread(fd, d, n > (1u << 30) ? (1u << 30) : n, (off_t)off);
+  while (*done < n) {
+    const uint64_t left = n - *done;
+    const ssize_t r = pread(fd, d + *done, left > (1u << 30) ? (1u << 30) : left,
+                            (off_t)(off + *done));
     if (r < 0 && errno == EINTR) continue;
-    if (r <= 0) return false;
-    d += r;
-    off += (uint64_t)r;
-    n -= (uint64_t)r;
+    if (r < 0) return errno ? errno : EIO;
+    if (r == 0) return -1;
+    *done += (uint64_t)r;
   }
-  return true;
+  return 0;
+}
+
+bool read_all(int fd, uint64_t off, void *dst, uint64_t n) {
+  uint64_t done = 0;
+  return read_some(fd, off, dst, n, &done) == 0;
+}
+
+// A read failure that can pass (an I/O error, a timeout, a stale network
+// file handle, a busy or exhausted resource), as opposed to a file that
+// ends inside a tensor or a bad descriptor.
+bool transient_read_error(int err) {
+  return err == EIO || err == EAGAIN || err == ETIMEDOUT || err == ESTALE || err == EBUSY ||
+         err == ENOMEM || err == ENOBUFS;
 }
 
 bool write_all(int fd, uint64_t off, const void *src, uint64_t n) {
@@ -393,7 +415,9 @@ struct q8_st {
     uint64_t begin, end;   // absolute byte offsets in the file
   };
   std::vector<std::string> paths;
-  std::vector<int> fds;
+  // (reopened by a read that retries, under reopen_mu)
+  mutable std::vector<int> fds;
+  mutable std::mutex reopen_mu;
   std::vector<Tensor> tensors;
   std::map<std::string, int64_t> index;
   std::vector<std::pair<std::string, std::string>> metadata;   // first shard's
@@ -577,10 +601,33 @@ int q8_st_read(const q8_st *st, int64_t i, uint64_t byte_off, void *dst, uint64_
                    (unsigned long long)byte_off, (unsigned long long)nbytes, t.name.c_str(),
                    (unsigned long long)size);
   if (nbytes && !dst) return st_fail(Q8_ERR_ARG, "q8_st_read: null destination");
-  if (!read_all(st->fds[(size_t)t.file], t.begin + byte_off, dst, nbytes))
-    return st_fail(Q8_ERR_ARG, "q8_st_read: read of '%s' failed: %s", t.name.c_str(),
-                   strerror(errno));
-  return Q8_OK;
+  // A failed read is tried again, as the reference's loader does (15
+  // attempts 2 s apart, reopening the file each time: src/resident.mojo:41-54),
+  // when the failure can pass; the bytes already read are kept.  A file that
+  // ends inside the tensor fails at once.
+  uint64_t done = 0;
+  for (int attempt = 1;; ++attempt) {
+    int fd;
+    {
+      std::lock_guard<std::mutex> lock(st->reopen_mu);
+      fd = st->fds[(size_t)t.file];
+    }
+    const int err = read_some(fd, t.begin + byte_off, dst, nbytes, &done);
+    if (err == 0) return Q8_OK;
+    if (err < 0 || !transient_read_error(err) || attempt >= kReadAttempts)
+      return st_fail(Q8_ERR_ARG, "q8_st_read: read of '%s' failed after %d attempt%s: %s",
+                     t.name.c_str(), attempt, attempt > 1 ? "s" : "",
+                     err < 0 ? "the file ends inside the tensor" : strerror(err));
+    fprintf(stderr, "q8_st_read: read of '%s' failed (%s), retry %d\n", t.name.c_str(),
+            strerror(err), attempt);
+    std::this_thread::sleep_for(std::chrono::milliseconds(kReadRetryMs));
+    std::lock_guard<std::mutex> lock(st->reopen_mu);
+    const int nfd = open(st->paths[(size_t)t.file].c_str(), O_RDONLY | O_CLOEXEC);
+    if (nfd >= 0) {
+      close(st->fds[(size_t)t.file]);
+      st->fds[(size_t)t.file] = nfd;
+    }
+  }
 }
 
 // ---- writer -----------------------------------------------------------------

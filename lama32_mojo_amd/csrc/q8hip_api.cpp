@@ -616,7 +616,17 @@ int noalloc_scratch(int dev, Scratch *out) {
   std::lock_guard<std::mutex> lock(g_noalloc_mu);
   void *base = g_noalloc_ptr[dev];
   if (!base) {
-    hipError_t e = hipGetSymbolAddress(&base, HIP_SYMBOL(scratch));
+    // The first call may come while this thread captures a stream into a
+    // graph: the symbol lookup (which can load the code object) is not a
+    // stream operation, so it runs with this thread's capture mode relaxed
+    // for its duration, then the caller's mode is restored.
+    hipStreamCaptureMode mode = hipStreamCaptureModeRelaxed;
+    hipError_t e = hipThreadExchangeStreamCaptureMode(&mode);
+    if (e != hipSuccess)
+      return hip_fail(nullptr, e, "q8_linear_noalloc: hipThreadExchangeStreamCaptureMode");
+    e = hipGetSymbolAddress(&base, HIP_SYMBOL(scratch));
+    hipError_t e2 = hipThreadExchangeStreamCaptureMode(&mode);
+    if (e == hipSuccess && e2 != hipSuccess) e = e2;
     if (e != hipSuccess || !base)
       return hip_fail(nullptr, e != hipSuccess ? e : hipErrorInvalidSymbol,
                       "q8_linear_noalloc: hipGetSymbolAddress(scratch)");
@@ -641,6 +651,11 @@ int q8_linear_noalloc(void *hip_stream, const void *w, const float *x, float *y,
                 (long long)n);
   if (s == 0 || n == 0) return Q8_OK;
   if (!w || !x || !y) return fail(nullptr, Q8_ERR_ARG, "%s: null weight, x or y pointer", what);
+  // the alignment q8_linear's element offsets give: u16 weights, f32 x and y
+  if ((reinterpret_cast<uintptr_t>(w) & 1) || (reinterpret_cast<uintptr_t>(x) & 3) ||
+      (reinterpret_cast<uintptr_t>(y) & 3))
+    return fail(nullptr, Q8_ERR_ARG, "%s: w must be 2-byte aligned, x and y 4-byte aligned",
+                what);
   const unsigned __int128 xb = (unsigned __int128)s * (uint64_t)m * 4,
                           yb = (unsigned __int128)s * (uint64_t)n * 4;
   if (xb >= ((unsigned __int128)1 << 62) || yb >= ((unsigned __int128)1 << 62))
@@ -835,6 +850,16 @@ int q8_linear_fused(q8_ctx *ctx, q8_buf *w, uint64_t owt_u16, q8_buf *a, uint64_
 // Floats spanned by s rows of `width` floats at a row stride of ld.
 static uint64_t rows_span(int64_t s, int64_t ld, uint64_t width) {
   return s == 0 ? 0 : (uint64_t)(s - 1) * (uint64_t)ld + width;
+}
+
+// Rows of wa floats at a and rows of wb floats at b, both at row stride ld
+// (wa, wb <= ld): true when no element of one is an element of the other
+// for any pair of rows, i.e. b's columns taken modulo ld from a's row start
+// lie in [wa, ld) without wrapping.
+static bool stride_disjoint(uint64_t a, int64_t wa, uint64_t b, int64_t wb, int64_t ld) {
+  const int64_t d = (int64_t)(b - a);             // both lie inside one arena
+  const int64_t r = (d % ld + ld) % ld;
+  return r >= wa && r + wb <= ld;
 }
 
 int q8_linear_swiglu(q8_ctx *ctx, q8_buf *w, uint64_t owt_u16, q8_buf *a, uint64_t og_f32,
@@ -1041,17 +1066,30 @@ int q8_rope_kv(q8_ctx *ctx, q8_buf *a, uint64_t oq_f32, uint64_t ok_f32, uint64_
   if (int rc = check_f32(ctx, a, ov_f32, kn, "q8_rope_kv", "v")) return rc;
   if (int rc = check_f32(ctx, a, oinv_f32, (uint64_t)head_dim / 2, "q8_rope_kv", "inv_freq"))
     return rc;
+  // q and k are rotated in place while v and inv_freq are read by the same
+  // launch: no element of v or inv_freq may be a q or k element, nor q a k
+  // element.
   if (ld == 0) {
     if (overlaps(oq_f32, oq_f32 + qn, ok_f32, ok_f32 + kn))
       return fail(ctx, Q8_ERR_ARG, "q8_rope_kv: q and k overlap");
+    if (overlaps(ov_f32, ov_f32 + kn, oq_f32, oq_f32 + qn) ||
+        overlaps(ov_f32, ov_f32 + kn, ok_f32, ok_f32 + kn))
+      return fail(ctx, Q8_ERR_ARG, "q8_rope_kv: v overlaps q or k");
   } else {
-    // rows of one stride: k's columns, taken modulo ld from q's row start,
-    // must lie in [qdim, ld) for no k element to be a q element
-    const int64_t d = (int64_t)(ok_f32 - oq_f32);   // both lie inside the arena
-    const int64_t r = (d % ld + ld) % ld;
-    if (r < qdim || r + kvdim > ld)
+    // rows of one stride: k's (v's) columns, taken modulo ld from q's (k's)
+    // row start, must lie in [width, ld), wrapped rows included
+    if (!stride_disjoint(oq_f32, qdim, ok_f32, kvdim, ld))
       return fail(ctx, Q8_ERR_ARG, "q8_rope_kv: q and k rows overlap at stride %lld",
                   (long long)ld);
+    if (!stride_disjoint(oq_f32, qdim, ov_f32, kvdim, ld) ||
+        !stride_disjoint(ok_f32, kvdim, ov_f32, kvdim, ld))
+      return fail(ctx, Q8_ERR_ARG, "q8_rope_kv: v rows overlap q or k rows at stride %lld",
+                  (long long)ld);
+  }
+  {
+    const uint64_t oi = oinv_f32, ni = (uint64_t)head_dim / 2;
+    if (overlaps(oi, oi + ni, oq_f32, oq_f32 + qn) || overlaps(oi, oi + ni, ok_f32, ok_f32 + kn))
+      return fail(ctx, Q8_ERR_ARG, "q8_rope_kv: inv_freq overlaps the q or k rows");
   }
   if (!fits(okc_f16, cn, 2, kv->size) || !fits(ovc_f16, cn, 2, kv->size))
     return fail(ctx, Q8_ERR_RANGE, "q8_rope_kv: K or V cache block exceeds the KV buffer");

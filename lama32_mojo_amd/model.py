@@ -353,6 +353,11 @@ class Q8Llama:
         oz = a.alloc(s * H)
         q8hip.add_rmsnorm(ctx, w.buf, lo.post_norm, a.buf, ox, oo, oh, oz, s, H, cfg.eps)
         gu_stacked = lo.up == lo.gate + I * rsH and (s == 1 or (s >= 32 and I % 4 == 0))
+        if s >= 32:
+            # 16-byte aligned gate rows: stacked rows then always take the
+            # swiglu pre-pass below, the only path that reads them at their
+            # 2I stride
+            a.align(4)
         if gu_stacked:
             og = self.linear(oz, s, H, lo.gate, 2 * I)
             ou = og + I
@@ -366,6 +371,7 @@ class Q8Llama:
             q8hip.linear_swiglu(ctx, w.buf, lo.down, a.buf, og, ou, om, s, I, H, self.G,
                                 self.scale, ld=2 * I if gu_stacked else 0)
         else:
+            assert not (gu_stacked and s > 1), "stacked gate|up rows need the strided pre-pass"
             q8hip.swiglu(ctx, a.buf, og, ou, s * I)
             om = self.linear(og, s, I, lo.down, H)
         q8hip.add(ctx, a.buf, om, oh, s * H)

@@ -107,6 +107,12 @@ class Acts:
             raise RuntimeError("acts arena overflow")
         return off
 
+    def align(self, k: int) -> None:
+        """Round the next allocation's offset up to a multiple of k floats."""
+        self.top = (self.top + k - 1) // k * k
+        if self.top > self.cap:
+            raise RuntimeError("acts arena overflow")
+
     def mark(self) -> int:
         return self.top
 

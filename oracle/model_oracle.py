@@ -153,6 +153,10 @@ class OracleModel:
     kc: list = field(default_factory=list)
     vc: list = field(default_factory=list)
     pos: int = 0
+    # the float64 linear y = x . deq(W)^T over packed rows:
+    # linear(packed, x, G, scale); numpy's dequantise-then-matmul unless
+    # given (a model at full width passes the C closed form, same values)
+    linear: object = None
 
     def __post_init__(self):
         sp = self.spec
@@ -162,6 +166,8 @@ class OracleModel:
 
     def lin(self, name: str, x: np.ndarray) -> np.ndarray:
         sp = self.spec
+        if self.linear is not None:
+            return self.linear(self.tensors[name], x, sp.G, sp.scale)
         return linear_f64_np(self.tensors[name], x, x.shape[1], sp.G, sp.scale)
 
     def layer(self, L: int, x: np.ndarray) -> np.ndarray:

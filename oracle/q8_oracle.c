@@ -255,6 +255,31 @@ void q8o_linear_f64(const uint16_t *wpk, const float *x, int64_t s, int64_t m,
     }
 }
 
+/* The same float64 closed form for float64 inputs (the model oracle's
+ * activations are float64 between its layers): y[i,j] = sum_g s[j,g] *
+ * sum_{k in g} x[i,k] * q[j,k], every product and sum in float64. */
+void q8o_linear_f64x(const uint16_t *wpk, const double *x, int64_t s, int64_t m,
+                     int64_t n, int G, int kind, double *y)
+{
+    int64_t rs = q8o_rowstride_u16(m, G, kind);
+    int64_t ng = m / G;
+#pragma omp parallel for schedule(static)
+    for (int64_t t = 0; t < s * n; ++t) {
+        const int64_t i = t / n, j = t % n;
+        const double *xi = x + i * m;
+        const uint16_t *row = wpk + j * rs;
+        const int8_t *q = row_codes(row, m, G, kind);
+        double acc = 0.0;
+        for (int64_t g = 0; g < ng; ++g) {
+            double part = 0.0;
+            for (int k = 0; k < G; ++k)
+                part += xi[g * G + k] * (double)q[g * G + k];
+            acc += (double)row_scale(row, g, kind) * part;
+        }
+        y[t] = acc;
+    }
+}
+
 /* Group-major fp32 restatement of k_mm_q8's arithmetic (src/llama_q8.mojo:73-93):
  * 32 lanes (TG_MM) stride over groups; per group a 16-wide fp32 fma chain
  * over 16-element chunks gives the unscaled dot, reduced and scaled once

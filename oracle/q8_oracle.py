@@ -141,6 +141,38 @@ def max_rel_err(y, y_ref) -> float:
     return float(num / den)
 
 
+def abs_packed(packed, m: int, G: int = 64, scale: str = "f16") -> np.ndarray:
+    """Packed rows of |W|: every scale's sign bit cleared and every code
+    replaced by its magnitude (codes lie in [-127, 127]), so the linear over
+    them is sum_k |x_k| |w_jk| when given |x|."""
+    out = np.array(packed, dtype=np.uint16, copy=True)
+    ng = m // G
+    if scale == "f16":
+        out[:, :ng] &= np.uint16(0x7FFF)
+        codes = out[:, ng:].view(np.int8)
+    else:
+        out[:, 1:2 * ng:2] &= np.uint16(0x7FFF)     # high halves of the f32 scales
+        codes = out[:, 2 * ng:].view(np.int8)
+    np.abs(codes, out=codes)
+    return out
+
+
+def elementwise_err(y, y_ref, y_abs) -> float:
+    """Elementwise relative error max_i |y_i - y*_i| / a_i, where a_i =
+    sum_k |x_k| |w_ik| is output i's own scale: the standard componentwise
+    bound of a dot product, so the bar holds for every output, those that
+    cancel to near zero included (0 where a_i is 0 and y_i equals y*_i)."""
+    y = np.asarray(y, dtype=np.float64)
+    y_ref = np.asarray(y_ref, dtype=np.float64)
+    a = np.asarray(y_abs, dtype=np.float64)
+    d = np.abs(y - y_ref)
+    if d.size == 0:
+        return 0.0
+    with np.errstate(divide="ignore", invalid="ignore"):
+        r = np.where(d == 0.0, 0.0, d / a)
+    return float(np.max(r))
+
+
 # --------------------------------------------------------------------------
 # C restatement (ctypes)
 # --------------------------------------------------------------------------
@@ -168,6 +200,8 @@ class COracle:
         lib.q8o_pack_bf16.restype = I
         lib.q8o_linear_f64.argtypes = [P, P, I64, I64, I64, I, I, P]
         lib.q8o_linear_f64.restype = None
+        lib.q8o_linear_f64x.argtypes = [P, P, I64, I64, I64, I, I, P]
+        lib.q8o_linear_f64x.restype = None
         lib.q8o_linear_f32.argtypes = [P, P, I64, I64, I64, I, I, P]
         lib.q8o_linear_f32.restype = None
         lib.q8o_embed_gather.argtypes = [P, P, I64, I64, I, I, P]
@@ -236,6 +270,24 @@ class COracle:
         self.lib.q8o_linear_f64(self._p(packed), self._p(x), s, m, n, G,
                                 scale_kind(scale), self._p(y))
         return y
+
+    def linear_f64x(self, packed, x, G=64, scale="f16") -> np.ndarray:
+        """float64 closed form for float64 activations x [s, m]."""
+        packed = np.ascontiguousarray(packed, dtype=np.uint16)
+        x = np.ascontiguousarray(np.atleast_2d(x), dtype=np.float64)
+        s, m = x.shape
+        n = packed.shape[0]
+        assert packed.shape[1] == rowstride_u16(m, G, scale)
+        y = np.empty((s, n), dtype=np.float64)
+        self.lib.q8o_linear_f64x(self._p(packed), self._p(x), s, m, n, G,
+                                 scale_kind(scale), self._p(y))
+        return y
+
+    def linear_abs(self, packed, x, G=64, scale="f16") -> np.ndarray:
+        """sum_k |x_ik| |w_jk| in float64: each output's scale for
+        elementwise_err."""
+        x = np.abs(np.atleast_2d(np.asarray(x, dtype=np.float64)))
+        return self.linear_f64x(abs_packed(packed, x.shape[1], G, scale), x, G, scale)
 
     def linear_f32(self, packed, x, G=64, scale="f16") -> np.ndarray:
         packed = np.ascontiguousarray(packed, dtype=np.uint16)

@@ -350,8 +350,25 @@ def test_qkv_row_stride_validation(hctx):
     c, msg = rope(0, qd - 1, qd + kvd, ld)                     # k's first column is q's last
     assert c == Q8_ERR_ARG and "stride" in msg
     assert rope(0, ld - kvd + 1, qd + kvd, ld)[0] == Q8_ERR_ARG   # k wraps into the next q row
-    assert rope(qd + kvd, 2 * qd + kvd, 0, ld)[0] == Q8_ERR_NODEVICE  # rows rotated, k after q
+    # q rows wrap into the next row's v columns (and the last one into
+    # inv_freq): q is rotated in place while v is read
+    c, msg = rope(qd + kvd, 2 * qd + kvd, 0, ld)
+    assert c == Q8_ERR_ARG and "v rows" in msg
+    assert rope(2 * kvd, 0, kvd, ld)[0] == Q8_ERR_NODEVICE    # rotated: k, v, then q
     assert rope(kvd, 0, qd + kvd, ld)[0] == Q8_ERR_NODEVICE   # k before q in each row
+    assert rope(0, qd, qd + kvd - 1, ld)[0] == Q8_ERR_ARG     # v's first column is k's last
+    assert rope(0, qd, qd - 1, ld)[0] == Q8_ERR_ARG           # v's first column is q's last
+    # dense rows (one row each): v must meet neither q nor k, inv_freq
+    # neither q nor k (v and inv_freq are only read, they may meet)
+    s1 = 1
+    dense = lambda oq, ok, ov, oi: code_of(q8hip.rope_kv, hctx, a, oq, ok, ov, oi, kv, 0, blk,
+                                           maxlen, s1, 0, nh, nkv, hd)[0]
+    assert dense(0, qd, qd + kvd, qd + 2 * kvd) == Q8_ERR_NODEVICE
+    assert dense(0, qd, qd + kvd, qd + kvd) == Q8_ERR_NODEVICE    # inv_freq inside v
+    assert dense(0, qd, qd + kvd - 1, qd + 2 * kvd) == Q8_ERR_ARG   # v meets k
+    assert dense(0, qd, qd - 1, qd + 2 * kvd) == Q8_ERR_ARG         # v meets q
+    assert dense(0, qd, qd + kvd, qd - 1) == Q8_ERR_ARG             # inv_freq meets q
+    assert dense(0, qd, qd + kvd, qd + kvd - 1) == Q8_ERR_ARG       # inv_freq meets k
     na = s * ld + hd + 2 * s * qd                               # arena floats
     assert rope(na - (s - 1) * ld - qd, 0, 0, ld)[0] != Q8_ERR_RANGE
     assert rope(na - (s - 1) * ld - qd + 1, 0, 0, ld)[0] == Q8_ERR_RANGE   # last q row past it
@@ -392,3 +409,21 @@ def test_kv_cache_block_under_2gib(hctx, which):
         assert c == want, (maxlen, msg)
         if want == Q8_ERR_SHAPE:
             assert "2 GiB" in msg
+
+
+def test_noalloc_validation_without_a_device():
+    """q8_linear_noalloc rejects misaligned pointers (w 2-byte, x and y
+    4-byte: the alignment q8_linear's element offsets give), null pointers,
+    overlapping x and y and bad shapes before any HIP call."""
+    L = q8hip.linear_noalloc
+    base = 1 << 20                                   # never dereferenced
+    for wo, xo, yo in ((1, 0, 4096), (0, 2, 4096), (0, 0, 4098), (0, 1, 4096)):
+        c, msg = code_of(L, None, base + wo, base + xo, base + yo, 1, 64, 4, 64, "f16")
+        assert c == Q8_ERR_ARG and "aligned" in msg, (wo, xo, yo, msg)
+    c, msg = code_of(L, None, 0, base, base + 4096, 1, 64, 4, 64, "f16")
+    assert c == Q8_ERR_ARG and "null" in msg
+    c, msg = code_of(L, None, base, base, base + 128, 1, 64, 4, 64, "f16")
+    assert c == Q8_ERR_ARG and "overlap" in msg
+    c, msg = code_of(L, None, base, base, base + 4096, 1, 100, 4, 64, "f16")
+    assert c == Q8_ERR_SHAPE
+    assert code_of(L, None, base + 1, base + 1, base + 3, 0, 64, 4, 64, "f16")[0] == 0   # empty

@@ -227,3 +227,24 @@ def test_model_rejects_mismatched_checkpoint(tmp_path):
                 gm.Q8Llama(ctx, cfg, 8, 64, "f16", weights=st)
     finally:
         ctx.close()
+
+
+def test_read_of_a_file_cut_after_open_fails_at_once(tmp_path):
+    """A file that ends inside a tensor (cut short after its header was
+    read) is not a failure that can pass: the read fails on its first
+    attempt, without the retries of a transient read error
+    (src/resident.mojo:41-54 retries every failed read 15 times, 2 s apart;
+    here only I/O errors, timeouts, stale handles and busy resources are
+    retried)."""
+    import time
+    path = tmp_path / "m.safetensors"
+    safetensors_numpy.save_file({"a": np.arange(64, dtype=np.float32)}, str(path))
+    with ck.SafeTensors(str(path)) as st:
+        assert np.array_equal(st.read("a"), np.arange(64, dtype=np.float32))
+        with open(path, "r+b") as f:
+            f.truncate(os.path.getsize(path) - 100)
+        t0 = time.perf_counter()
+        with pytest.raises(q8hip.Q8Error) as ei:
+            st.read("a")
+        assert time.perf_counter() - t0 < 1.0
+        assert "ends inside the tensor" in ei.value.msg and "1 attempt" in ei.value.msg

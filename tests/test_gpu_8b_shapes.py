@@ -30,8 +30,8 @@ import pytest
 
 from lama32_mojo_amd import q8hip
 from oracle import model_oracle as mo
-from oracle.q8_oracle import (bf16_bits_to_f32, f32_to_bf16_bits, max_rel_err, synth_weights_bf16,
-                              synth_x)
+from oracle.q8_oracle import (bf16_bits_to_f32, elementwise_err, f32_to_bf16_bits, max_rel_err,
+                              synth_weights_bf16, synth_x)
 
 pytestmark = pytest.mark.gpu
 LAYOUTS = [(64, "f16"), (32, "f32")]
@@ -126,8 +126,20 @@ FUSED_8B = [(4096, 6144, q8hip.PRE_RMSNORM, q8hip.POST_STORE),       # q|k|v
             (4096, 128256, q8hip.PRE_RMSNORM, q8hip.POST_STORE)]     # untied lm_head
 
 
+# (m, n, pre, post): the fused launches of the Llama-3.2-1B decode step (the
+# headline workload) and the Qwen3-0.6B ones the 8B widths do not reach
+FUSED_1B = [(2048, 3072, q8hip.PRE_RMSNORM, q8hip.POST_STORE),       # rmsnorm + q|k|v
+            (2048, 2048, q8hip.PRE_NONE, q8hip.POST_RESIDUAL),       # o + residual
+            (2048, 16384, q8hip.PRE_RMSNORM, q8hip.POST_SWIGLU),     # rmsnorm + gate|up + swiglu
+            (8192, 2048, q8hip.PRE_NONE, q8hip.POST_RESIDUAL),       # down + residual
+            (2048, 128256, q8hip.PRE_RMSNORM, q8hip.POST_STORE),     # final norm + tied lm_head
+            (1024, 6144, q8hip.PRE_RMSNORM, q8hip.POST_SWIGLU),      # Qwen3-0.6B gate|up
+            (2048, 1024, q8hip.PRE_NONE, q8hip.POST_RESIDUAL),       # Qwen3-0.6B o
+            (3072, 1024, q8hip.PRE_NONE, q8hip.POST_RESIDUAL)]       # Qwen3-0.6B down
+
+
 @pytest.mark.parametrize("G,scale", LAYOUTS)
-@pytest.mark.parametrize("m,n,pre,post", FUSED_8B)
+@pytest.mark.parametrize("m,n,pre,post", FUSED_8B + FUSED_1B)
 def test_fused_gemv_8b_shapes_against_float64(ctx, cor, G, scale, m, n, pre, post):
     """q8_linear_fused against float64 rmsnorm / swiglu of the input, the
     float64 linear of the oracle and float64 swiglu / residual of its
@@ -201,11 +213,13 @@ def test_long_rows_ragged_against_float64(ctx, cor, G, scale, m, n):
 
 
 @pytest.mark.parametrize("G,scale", LAYOUTS)
-def test_head_argmax_untied_8b_head(ctx, cor, G, scale):
-    """q8_head_argmax over the untied Llama-3.1-8B head (4096 -> 128256):
-    the float64 model's token, logits within 1e-5."""
-    say("8B head argmax", G, scale)
-    m, n = 4096, 128256
+@pytest.mark.parametrize("m,n", [(4096, 128256), (2048, 128256), (1024, 151936)])
+def test_head_argmax_untied_8b_head(ctx, cor, G, scale, m, n):
+    """q8_head_argmax over the Llama-3.1-8B head (4096 -> 128256), the
+    Llama-3.2-1B head of the headline step (2048 -> 128256) and the
+    Qwen3-0.6B one (1024 -> 151936): the float64 model's token, logits
+    within 1e-5."""
+    say("head argmax", G, scale, m, n)
     rng = np.random.default_rng(17)
     P = Packed(ctx, n, m, G, scale, seed=99, extra_u16=m)
     wn = f32_to_bf16_bits((1 + 0.1 * rng.standard_normal(m)).astype(np.float32))
@@ -273,7 +287,41 @@ def test_gemm_large_shapes(ctx, cor, G, scale, s, n, m, act):
     assert err <= 1e-3, err
     for i, r in enumerate(rows):
         assert max_rel_err(got[i], ref[i]) <= 1e-3, r
+    ew = elementwise_err(got, ref, cor.linear_abs(P.pk, np.ascontiguousarray(x[rows]), G, scale))
+    assert ew <= 1e-3, ew
     assert np.all(np.isfinite(y))
+    P.free()
+
+
+@pytest.mark.parametrize("G,scale", LAYOUTS)
+def test_linear_swiglu_8b_prompt_against_float64(ctx, cor, G, scale):
+    """The Llama-3.1-8B prompt path's down projection: q8_linear_swiglu over
+    2048 stacked gate|up rows (row stride 2 x 14336, silu(g) * u formed in
+    the binary16 pre-pass) -> 4096 outputs, against float64 swiglu and the
+    float64 linear on rows spread over every row tile: within 1e-3
+    normwise, per row and elementwise (each output against sum |x||w|)."""
+    say("linear_swiglu 8B", G, scale)
+    s, m, n = 2048, 14336, 4096
+    P = Packed(ctx, n, m, G, scale, seed=77)
+    rng = np.random.default_rng(78)
+    gu = rng.standard_normal((s, 2 * m), dtype=np.float32)
+    gu[:, :m] *= 2.0
+    a = ctx.alloc(4 * (s * 2 * m + s * n))
+    a.upload(gu)
+    oy = s * 2 * m
+    q8hip.linear_swiglu(ctx, P.w, 0, a, 0, m, oy, s, m, n, G, scale, ld=2 * m)
+    y = a.download((s, n), np.float32, 4 * oy)
+    a.free()
+    rows = sample_rows(s)
+    xs = mo.swiglu(gu[rows, :m], gu[rows, m:].astype(np.float64))
+    ref = cor.linear_f64x(P.pk, xs, G, scale)
+    got = y[rows]
+    assert np.all(np.isfinite(y))
+    assert max_rel_err(got, ref) <= 1e-3
+    for i, r in enumerate(rows):
+        assert max_rel_err(got[i], ref[i]) <= 1e-3, r
+    ew = elementwise_err(got, ref, cor.linear_abs(P.pk, xs, G, scale))
+    assert ew <= 1e-3, ew
     P.free()
 
 

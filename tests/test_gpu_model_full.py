@@ -1,0 +1,123 @@
+"""Whole models at their real widths on the GPU (through the C ABI) against
+the float64 model oracle -- the reference's own Q8 gate is a whole-model
+check (prefill, greedy ids, a logit bound against an f32 oracle:
+qwen3_mojo/src/qwen_q8.mojo:180-224) over the layer runner
+src/llama_q8.mojo:144-230.
+
+Models: Llama-3.2-1B (16 layers, hidden 2048, 32 / 8 heads of 64, MLP 8192,
+tied 128256-row head -- the headline decode step), Qwen3-0.6B (28 layers,
+hidden 1024, 16 / 8 heads of 128 with q/k head norms, MLP 3072, tied
+151936-row head -- the reference's own Q8 model) and Llama-3.1-8B (32
+layers, hidden 4096, MLP 14336, untied head), with random bf16 weights
+packed on the GPU (G64 / binary16 scales, the reference layout) and
+downloaded for the oracle, which runs every linear as the float64 closed
+form over the same packed rows.
+
+What is compared (bars written in each test):
+  * a short prompt (the few-row linears and the split-KV attention):
+    last-position logits within max-rel-err 1e-3 of float64;
+  * then one eager fused step and graph-replayed steps (the decode step the
+    bench times: fused GEMVs, the one-launch attention with its merge, the
+    head with its argmax on the GPU): logits within 1e-3, and each step's
+    token equal to the float64 model's unless the float64 model's two best
+    logits lie within the bar of each other.
+The oracle is fed the GPU's tokens, so both walk the same sequence.
+"""
+
+import sys
+
+import numpy as np
+import pytest
+
+from lama32_mojo_amd import model as gm
+from lama32_mojo_amd.q8 import q8_rowstride
+from oracle import model_oracle as mo
+from oracle.q8_oracle import max_rel_err
+
+pytestmark = pytest.mark.gpu
+TOL = 1e-3
+
+
+def say(*a):
+    print(*a, flush=True)
+    sys.stdout.flush()
+
+
+def oracle_for(m: gm.Q8Llama, cor, maxlen: int) -> mo.OracleModel:
+    """The GPU model's packed arena, downloaded tensor by tensor, as a
+    float64 model oracle with the configuration's own RoPE frequencies
+    (the oracle's restatement of them)."""
+    cfg = m.cfg
+    shapes = gm.tensor_shapes(cfg)
+    tensors = {}
+    for name in gm.weight_names(cfg):
+        sh = shapes[name]
+        off = m.w.offs[name]
+        if len(sh) == 2:
+            rs = q8_rowstride(sh[1], m.G, m.scale)
+            tensors[name] = m.w.buf.download((sh[0], rs), np.uint16, 2 * off)
+        else:
+            tensors[name] = m.w.buf.download((sh[0],), np.uint16, 2 * off)
+    spec = mo.ModelSpec(hidden=cfg.hidden, layers=cfg.layers, n_heads=cfg.n_heads,
+                        n_kv=cfg.n_kv, head_dim=cfg.head_dim, inter=cfg.inter, vocab=cfg.vocab,
+                        eps=cfg.eps, G=m.G, scale=m.scale, tied=cfg.tied, qk_norm=cfg.qk_norm)
+    if cfg.rope == "plain":
+        inv = mo.rope_inv_freq(cfg.head_dim, cfg.theta)
+    else:
+        inv = mo.llama3_inv_freq(cfg.head_dim, cfg.theta, cfg.rope_factor, cfg.low_ff,
+                                 cfg.high_ff, cfg.orig_ctx)
+    return mo.OracleModel(spec, tensors, inv, maxlen, linear=cor.linear_f64x)
+
+
+def check_logits(lg, lr, what):
+    """Logits within TOL of float64, and the same best token unless the
+    float64 model's best two are within the bar of each other."""
+    assert np.all(np.isfinite(lg)), what
+    err = max_rel_err(lg, lr)
+    say(f"  {what}: max-rel-err {err:.2e}")
+    assert err <= TOL, (what, err)
+    check_token(int(np.argmax(lg)), lr, what)
+
+
+def check_token(tok, lr, what):
+    best = int(np.argmax(lr))
+    if tok != best:
+        gap = float(lr[best] - lr[tok])
+        assert gap <= 2 * TOL * float(np.max(np.abs(lr))), (what, tok, best, gap)
+
+
+MODELS = {"llama-3.2-1b": gm.LLAMA_32_1B, "qwen3-0.6b": gm.QWEN3_06B,
+          "llama-3.1-8b": gm.LLAMA_31_8B}
+
+
+@pytest.mark.timeout(600)
+@pytest.mark.parametrize("name", list(MODELS))
+def test_full_width_model_against_float64(ctx, cor, name):
+    cfg = MODELS[name]
+    maxlen = 32
+    say("full-width model", name)
+    m = gm.Q8Llama(ctx, cfg, maxlen, 64, "f16", seed=3, max_prefill=8)
+    try:
+        ref = oracle_for(m, cor, maxlen)
+        say("  weights packed and downloaded")
+        prompt = [int(v) for v in np.random.default_rng(5).integers(0, cfg.vocab, size=6)]
+        lg = m.forward(prompt)
+        lr = ref.forward(prompt)
+        check_logits(lg, lr, "prompt of 6")
+        tok = int(np.argmax(lg))
+        # one eager fused step (device argmax), the oracle fed the same token
+        nxt = m.forward_argmax([tok])
+        lr = ref.forward([tok])
+        check_token(nxt, lr, "eager fused step")
+        tok = nxt
+        # graph-replayed steps: logits of each replay and its token
+        for step in range(3):
+            ids = m.decode_steps(tok, 1)
+            lg = m.a.read(m.graph_logits, cfg.vocab)
+            lr = ref.forward([tok])
+            check_logits(lg, lr, f"graph step {step}")
+            assert ids[0] == int(np.argmax(lg)), step
+            tok = ids[0]
+        assert ref.pos == m.n_cached == len(prompt) + 4
+    finally:
+        m.close()

@@ -4,7 +4,9 @@ Bars (written in each test):
   * pack: codes and scales bit-exact (reference golden vectors and oracle);
   * linear / GEMM: normwise max relative error  max|y - y*| / max|y*|
     <= 1e-3 against the float64 closed form over the same codes, scales and
-    (bf16-rounded, for bf16 activations) inputs;
+    (bf16-rounded, for bf16 activations) inputs; elementwise, each output
+    against its own scale sum_k |x_k||w_k| (elementwise_err), <= 1e-5 on the
+    f32 paths (s < 32) and <= 1e-3 on the f16-MFMA GEMM;
   * one-hot inputs, fused-vs-separate calls and embedding gathers: bit-exact.
 """
 
@@ -14,8 +16,8 @@ import numpy as np
 import pytest
 
 from lama32_mojo_amd import q8, q8hip
-from oracle.q8_oracle import (bf16_bits_to_f32, f32_to_bf16_bits, max_rel_err, rowstride_u16,
-                              synth_weights_bf16, synth_x, unpack_q8_np)
+from oracle.q8_oracle import (bf16_bits_to_f32, elementwise_err, f32_to_bf16_bits, max_rel_err,
+                              rowstride_u16, synth_weights_bf16, synth_x, unpack_q8_np)
 
 pytestmark = pytest.mark.gpu
 TOL = 1e-3
@@ -120,7 +122,10 @@ def test_pack_unaligned_offsets(ctx, cor):
 # decode GEMV (q8_linear, small s)
 # ---------------------------------------------------------------------------
 
-SHAPES = [(8192, 2048), (3072, 2048), (2048, 8192), (1000, 1536), (1, 64), (7, 96)]
+# (n, m): the Llama-3.2-1B decode projections (gate|up 16384, up 8192,
+# q|k|v 3072, o 2048, down 2048 x 8192) and ragged ones
+SHAPES = [(8192, 2048), (3072, 2048), (2048, 2048), (16384, 2048), (2048, 8192), (1000, 1536),
+          (1, 64), (7, 96)]
 
 
 def layout_shapes(shapes, m_index):
@@ -141,6 +146,8 @@ def test_linear_matches_closed_form(ctx, cor, G, scale, n, m, s):
     err = max_rel_err(y, ref)
     assert err <= TOL, err
     assert err <= 1e-5, err      # fp32 accumulation is far inside the bar
+    ew = elementwise_err(y, ref, cor.linear_abs(pk, x, G, scale))
+    assert ew <= 1e-5, ew
 
 
 @pytest.mark.parametrize("G,scale,n,m", [(32, "f32", 4099, 640), (32, "f32", 16386, 640),
@@ -311,6 +318,8 @@ def test_gemm_bf16act_matches_closed_form(ctx, cor, G, scale, s, n, m):
     ref = cor.linear_f64(pk, bf16_bits_to_f32(xbits), G, scale)
     err = max_rel_err(y, ref)
     assert err <= TOL, err
+    ew = elementwise_err(y, ref, cor.linear_abs(pk, bf16_bits_to_f32(xbits), G, scale))
+    assert ew <= TOL, ew
 
 
 @pytest.mark.parametrize("G,scale", LAYOUTS)
@@ -326,9 +335,12 @@ def test_gemm_f32act_matches_closed_form(ctx, cor, G, scale, s):
     pk = cor.pack_bf16(synth_weights_bf16(n, m, seed=41), G, scale)
     x = synth_x(s, m, seed=42)
     y = gpu_linear(ctx, pk, x, G, scale)
-    err = max_rel_err(y, cor.linear_f64(pk, x, G, scale))
+    ref = cor.linear_f64(pk, x, G, scale)
+    err = max_rel_err(y, ref)
     assert err <= TOL, err
     assert err <= 5e-4, err
+    ew = elementwise_err(y, ref, cor.linear_abs(pk, x, G, scale))
+    assert ew <= TOL, ew
 
 
 @pytest.mark.parametrize("bf16", [False, True])

@@ -220,3 +220,69 @@ def test_qk_norm_removes_the_scale_of_q_and_k_projections():
     a = mo.OracleModel(plain, t, inv, 16).forward(ids)
     b = mo.OracleModel(plain, scaled(t), inv, 16).forward(ids)
     assert np.max(np.abs(a - b)) > 1e-3
+
+
+def zero_rows(t, name):
+    """Packed rows of zeros (scale 0, codes 0): the matrix dequantises to 0."""
+    out = dict(t)
+    out[name] = np.zeros_like(t[name])
+    return out
+
+
+def test_layer_with_zero_o_and_down_is_the_identity():
+    """With W_o = W_down = 0 a pre-norm block adds nothing to its input: the
+    layer returns x exactly (a dropped or doubled residual fails this), while
+    the KV cache still receives the rotated k and v rows."""
+    spec, t, inv = tiny_model(seed=21)
+    for name in ["self_attn.o_proj.weight", "mlp.down_proj.weight"]:
+        t = zero_rows(t, "model.layers.0." + name)
+    m = mo.OracleModel(spec, t, inv, 16)
+    x = np.random.default_rng(22).standard_normal((3, spec.hidden))
+    y = m.layer(0, x)
+    assert np.array_equal(y, x)
+    assert np.abs(m.kc[0][:3]).max() > 0 and np.abs(m.vc[0][:3]).max() > 0
+    # with either projection back the output moves off x
+    spec2, t2, _ = tiny_model(seed=21)
+    for keep in ["self_attn.o_proj.weight", "mlp.down_proj.weight"]:
+        other = ({"self_attn.o_proj.weight", "mlp.down_proj.weight"} - {keep}).pop()
+        m2 = mo.OracleModel(spec, zero_rows(t2, "model.layers.0." + other), inv, 16)
+        assert np.abs(m2.layer(0, x) - x).max() > 1e-3, keep
+
+
+def test_each_norm_weight_feeds_its_own_branch():
+    """input_layernorm feeds only the attention branch and
+    post_attention_layernorm only the MLP branch: with the MLP zeroed
+    (W_down = 0) scaling the post-attention norm weights changes nothing and
+    scaling the input norm weights changes the output; with the attention
+    zeroed (W_o = 0) the other way round.  Swapped norm weights fail it."""
+    spec, t, inv = tiny_model(seed=23)
+    x = np.random.default_rng(24).standard_normal((2, spec.hidden))
+    p = "model.layers.0."
+
+    def run(tensors):
+        return mo.OracleModel(spec, tensors, inv, 16).layer(0, x)
+
+    def scaled_norm(tensors, name):
+        out = dict(tensors)
+        w = bf16_bits_to_f32(tensors[p + name]) * np.float32(1.5)
+        out[p + name] = f32_to_bf16_bits(w.astype(np.float32))
+        return out
+
+    for zeroed, inert, live in (("mlp.down_proj.weight", "post_attention_layernorm.weight",
+                                 "input_layernorm.weight"),
+                                ("self_attn.o_proj.weight", "input_layernorm.weight",
+                                 "post_attention_layernorm.weight")):
+        tz = zero_rows(t, p + zeroed)
+        base = run(tz)
+        np.testing.assert_array_equal(run(scaled_norm(tz, inert)), base)
+        assert np.abs(run(scaled_norm(tz, live)) - base).max() > 1e-3, live
+
+
+def test_injected_linear_gives_the_same_model(cor):
+    """The model oracle with the C float64 closed form as its linear gives
+    the logits of its numpy dequantise-then-matmul form (1e-12)."""
+    spec, t, inv = tiny_model(seed=25)
+    ids = [7, 8, 9, 10]
+    a = mo.OracleModel(spec, t, inv, 16).forward(ids)
+    b = mo.OracleModel(spec, t, inv, 16, linear=cor.linear_f64x).forward(ids)
+    assert np.max(np.abs(a - b)) <= 1e-12 * np.max(np.abs(a))

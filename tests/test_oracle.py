@@ -18,7 +18,8 @@ Checks, each chosen so that a plausible mistake in the oracle fails it:
 import numpy as np
 import pytest
 
-from oracle.q8_oracle import (bf16_bits_to_f32, embed_gather_np, linear_f64_np, max_rel_err,
+from oracle.q8_oracle import (abs_packed, bf16_bits_to_f32, elementwise_err, embed_gather_np,
+                              linear_f64_np, max_rel_err,
                               pack_q8_np, rowstride_u16, synth_weights_bf16, synth_x,
                               unpack_q8_np)
 
@@ -143,6 +144,46 @@ def test_linear_f64_closed_form(cor, G, scale):
     y = cor.linear_f64(pk, x, G, scale)
     y2 = linear_f64_np(pk, x, 512, G, scale)
     assert max_rel_err(y, y2) < 1e-12
+
+
+@pytest.mark.parametrize("G,scale", [(64, "f16"), (32, "f32")])
+def test_linear_f64x_closed_form(cor, G, scale):
+    """The float64-input closed form: the bits of the f32-input one on f32
+    values (same float64 sums in the same order), and within 1e-12 of the
+    dequantise-then-matmul form on inputs that need all 53 bits."""
+    wb = synth_weights_bf16(96, 512, seed=3)
+    pk = cor.pack_bf16(wb, G, scale)
+    x = synth_x(5, 512, seed=4)
+    assert np.array_equal(cor.linear_f64x(pk, x.astype(np.float64), G, scale),
+                          cor.linear_f64(pk, x, G, scale))
+    xd = np.random.default_rng(5).standard_normal((3, 512)) * np.pi
+    assert not np.array_equal(xd, xd.astype(np.float32).astype(np.float64))
+    assert max_rel_err(cor.linear_f64x(pk, xd, G, scale), linear_f64_np(pk, xd, 512, G, scale)) \
+        < 1e-12
+
+
+@pytest.mark.parametrize("G,scale", [(64, "f16"), (32, "f32")])
+def test_abs_packed_and_elementwise_err(cor, G, scale):
+    """abs_packed dequantises to |deq(W)| (every code and scale sign
+    removed, nothing else changed), so linear_abs equals |x| . |deq(W)|^T;
+    elementwise_err measures each output against that scale."""
+    wb = synth_weights_bf16(64, 512, seed=31)
+    pk = cor.pack_bf16(wb, G, scale)
+    codes, s = unpack_q8_np(pk, 512, G, scale)
+    assert (codes < 0).any() and (s >= 0).all()      # pack_q8's scales are absmax / 127
+    ac, asc = unpack_q8_np(abs_packed(pk, 512, G, scale), 512, G, scale)
+    assert np.array_equal(ac, np.abs(codes)) and np.array_equal(asc, np.abs(s))
+    x = synth_x(3, 512, seed=32)
+    want = np.abs(x).astype(np.float64) @ (np.abs(codes).astype(np.float64) *
+                                           np.repeat(np.abs(s).astype(np.float64), G, axis=1)).T
+    got = cor.linear_abs(pk, x, G, scale)
+    assert max_rel_err(got, want) < 1e-12
+    y = cor.linear_f64(pk, x, G, scale)
+    assert np.all(got >= np.abs(y))
+    assert elementwise_err(y, y, got) == 0.0
+    bumped = y.copy()
+    bumped[1, 7] += 1e-3 * got[1, 7]
+    assert abs(elementwise_err(bumped, y, got) - 1e-3) < 1e-9
 
 
 @pytest.mark.parametrize("G,scale", [(64, "f16"), (32, "f32")])
