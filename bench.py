@@ -61,6 +61,10 @@ Other workloads (--workload) run one of these alone:
   e2e-8b   Llama-3.1-8B end to end
   qwen3-06b  Qwen3-0.6B decode; value is tok/s, vs_baseline against the
            reference's published 29 tok/s (Apple M4, QUANTIZATION.md:28)
+  calib    ceilings on this GPU: an empty kernel node of a graph, a plain
+           streaming read at the step's GEMV sizes, 2 MB read by 8 .. 512
+           workgroups, register-only f16 MFMA, hipBLASLt dense GEMMs on the
+           prefill shapes (lama32_mojo_amd/calib/q8_calib.hip, torch.matmul)
   lmhead-pmc / gateup-pmc  the launches the HBM-traffic counter passes read:
            3 copies of 1 GiB by torch's copy kernel (the calibration of
            known size), then 8 lm_head GEMVs 128256x2048 alternating over
@@ -97,7 +101,7 @@ def parse():
     p.add_argument("--warmup", type=int, default=5)
     p.add_argument("--workload", default="all",
                    choices=["all", "decode", "decode-linears", "linear", "prefill", "qwen8b",
-                            "e2e-8b", "lmhead-pmc", "gateup-pmc", "qwen3-06b"])
+                            "e2e-8b", "lmhead-pmc", "gateup-pmc", "qwen3-06b", "calib"])
     p.add_argument("--layout", default=None, choices=["g64f16", "g32f32"],
                    help="packed layout (default: g64f16; g32f32 for --workload linear)")
     p.add_argument("--batch", type=int, default=1)
@@ -738,6 +742,103 @@ def run_prefill(B: Bench, cfg=LLAMA_1B, M=512):
     }
 
 
+def run_calib(B: Bench):
+    """Ceilings the roofline arguments rest on, measured on this GPU:
+    the kernel-boundary floor (one dependent empty kernel node of a graph),
+    a plain streaming read at the sizes of the Llama-3.2-1B decode step's
+    GEMVs (rotated over copies larger than the Infinity Cache), how fast a
+    few CUs pull a decode layer's 2 MB of K and V, the register-only f16
+    MFMA rate on random operands, and hipBLASLt's dense bf16 / f16 GEMM
+    (torch.matmul, 2-byte weights, no dequantization) on the prefill
+    shapes.  Kernels: lama32_mojo_amd/calib/q8_calib.hip (libq8calib.so)."""
+    import ctypes
+    torch = B.torch
+    path = os.path.join(ROOT, "lama32_mojo_amd", "libq8calib.so")
+    if not os.path.exists(path):
+        raise RuntimeError(f"{path} is missing: run __graft_entry__.build()")
+    lib = ctypes.CDLL(path)
+    f = ctypes.c_float()
+
+    def call(fn, *a):
+        rc = fn(*a, ctypes.byref(f))
+        if rc != 0:
+            raise RuntimeError(f"{fn.__name__} failed ({rc})")
+        return float(f.value)
+
+    lib.q8calib_empty_node_us.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_void_p]
+    lib.q8calib_stream_us.argtypes = [ctypes.c_uint64, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                      ctypes.c_void_p]
+    lib.q8calib_cu_read_us.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_uint64, ctypes.c_int,
+                                       ctypes.c_int, ctypes.c_void_p]
+    lib.q8calib_mfma_tflops.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_void_p]
+    out = {}
+    empty = call(lib.q8calib_empty_node_us, 64, 20)
+    out["empty_node_us"] = round(empty, 3)
+    print(f"empty kernel node {empty:.2f} us", file=sys.stderr, flush=True)
+    # the decode step's GEMV sizes at G64/f16 (bytes per launch)
+    sizes = {"o 2048x2048": 4349952, "q|k|v 2048x3072": 6508544, "down 8192x2048": 17350656,
+             "gate|up 2048x16384": 34603008, "lm_head 2048x128256": 270876672}
+    stream = {}
+    for name, nb in sizes.items():
+        nb16 = nb // 16 * 16
+        copies = max(3, -(-(640 << 20) // nb16))
+        best = None
+        for grid in (1024, 2048, 4096, 8192):
+            us = call(lib.q8calib_stream_us, nb16, copies, grid, 5)
+            if best is None or us < best[0]:
+                best = (us, grid)
+        stream[name] = {"bytes": nb16, "us": round(best[0], 3), "grid": best[1],
+                        "TB_s": round(nb16 / best[0] / 1e6, 3)}
+        print(f"stream {name}: {best[0]:.2f} us", file=sys.stderr, flush=True)
+    out["stream_read"] = stream
+    kv = 2 << 20                       # K + V of one Llama-3.2-1B layer at 1024 tokens
+    cu = []
+    for blocks, threads in ((8, 1024), (16, 1024), (40, 1024), (64, 1024), (136, 256),
+                            (512, 256)):
+        per = kv // blocks // 16 * 16
+        us = call(lib.q8calib_cu_read_us, blocks, threads, per, 160, 5)
+        cu.append({"blocks": blocks, "threads": threads, "bytes_per_block": per,
+                   "us": round(us, 3), "above_empty_us": round(us - empty, 3),
+                   "GB_s_per_block": round(per / max(us - empty, 1e-3) / 1e3, 1)})
+    out["two_mb_over_blocks"] = cu
+    mf = {}
+    for blocks in (256, 512, 1024):
+        mf[str(blocks)] = round(call(lib.q8calib_mfma_tflops, blocks, 4000, 5), 1)
+    out["mfma_f16_32x32x16_tflops_by_workgroups"] = mf
+    print(f"mfma {mf}", file=sys.stderr, flush=True)
+    dense = []
+    shapes = [(512, 16384, 2048), (512, 3072, 2048), (512, 2048, 2048), (512, 2048, 8192),
+              (2048, 14336, 4096), (2048, 4096, 14336), (2048, 28672, 4096)]
+    g = torch.Generator(device="cuda")
+    g.manual_seed(7)
+    for dt in (torch.bfloat16, torch.float16):
+        for (M, N, K) in shapes:
+            x = torch.randn((M, K), device="cuda", generator=g).to(dt)
+            wt = torch.randn((K, N), device="cuda", generator=g).to(dt).contiguous()
+            for _ in range(3):
+                torch.matmul(x, wt)
+            torch.cuda.synchronize()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            reps = 20
+            e0.record()
+            for _ in range(reps):
+                torch.matmul(x, wt)
+            e1.record()
+            e1.synchronize()
+            us = e0.elapsed_time(e1) * 1000.0 / reps
+            dense.append({"dtype": str(dt).replace("torch.", ""), "M": M, "N": N, "K": K,
+                          "us": round(us, 2), "TFLOP_s": round(2 * M * N * K / us / 1e6, 1)})
+            del x, wt
+    out["hipblaslt_dense"] = dense
+    best_mfma = max(mf.values())
+    return {"metric": "calibration: register-only f16 MFMA rate (random operands)",
+            "value": best_mfma, "unit": "TFLOP/s", "higher_is_better": True,
+            "dtype": "f16", "data": "synthetic",
+            "config": {"workload": "calibration ceilings (empty kernel node, streaming read, "
+                                   "few-CU reads of 2 MB, register-only MFMA, hipBLASLt dense)"},
+            "calibration": out}
+
+
 def cpu_baseline(packs, G, scale, budget_s, label):
     """Q8 linears over host copies of the packed weights on the host cores,
     three legs of about budget_s seconds each:
@@ -928,6 +1029,8 @@ def main():
         res = run_decode(B, QWEN3_8B)
     elif args.workload == "linear":
         res = run_linear(B)
+    elif args.workload == "calib":
+        res = run_calib(B)
     else:
         res = run_prefill(B)
     out = {"metric": res.pop("metric"), "value": res.pop("value"), "unit": res.pop("unit"),
@@ -937,7 +1040,7 @@ def main():
     out.setdefault("vs_baseline", None)
     order = ["metric", "value", "unit", "n_gpus", "steps", "warmup", "ms_per_step",
              "higher_is_better", "scaling", "vs_baseline", "dtype", "data", "config",
-             "roofline", "roofline_lm_head", "cpu_baseline", "configs"]
+             "roofline", "roofline_lm_head", "cpu_baseline", "configs", "calibration"]
     print(json.dumps({k: out[k] for k in order if k in out}), flush=True)
     ctx.close()
 

@@ -92,7 +92,22 @@ def build(verbose: bool = True, jobs: int | None = None, incremental: bool = Fal
     _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", f"-Wl,--version-script={vscript}",
           "-o", tmp, *objs], verbose)
     os.replace(tmp, LIB_PATH)
+    build_calib(verbose)
     return LIB_PATH
+
+
+CALIB_SRC = os.path.join(HERE, "calib", "q8_calib.hip")
+CALIB_PATH = os.path.join(HERE, "libq8calib.so")
+
+
+def build_calib(verbose: bool = True) -> str:
+    """libq8calib.so: the calibration kernels bench.py --workload calib
+    times (empty kernel node, streaming read, few-CU reads, register-only
+    MFMA); measurement infrastructure, not part of libq8hip.so."""
+    tmp = CALIB_PATH + ".tmp"
+    _run([HIPCC, *COMMON_FLAGS, "-shared", "-o", tmp, CALIB_SRC], verbose)
+    os.replace(tmp, CALIB_PATH)
+    return CALIB_PATH
 
 
 if __name__ == "__main__":

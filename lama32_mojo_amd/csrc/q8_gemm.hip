@@ -206,11 +206,15 @@ __device__ __forceinline__ f16x8 dequant8(uint32_t d0, uint32_t d1, f16x2 s2) {
   return f16x8{a.x, a.y, b.x, b.y, c.x, c.y, d.x, d.y};
 }
 
-// One workgroup per BM x BN output tile (BM = 32 TM, BN = 128 TN), its 12
-// waves split by role, three per SIMD:
+// One workgroup per BM x BN output tile (BM = 32 TM CR, BN = 32 TN (4 /
+// CR)), its 12 waves split by role, three per SIMD:
 //   * waves 0-3 (consumers) only read MFMA fragments from LDS and issue the
-//     MFMAs, each over all BM rows and its own 32 TN columns (TM x TN
-//     accumulator tiles of 32 x 32);
+//     MFMAs, each over 32 TM rows and 32 TN columns of the tile (TM x TN
+//     accumulator tiles of 32 x 32): with CR = 1 all four share the BM rows
+//     and split the columns, with CR = 2 they sit 2 x 2, so a 256 x 128
+//     tile dequantizes half the weights per flop of a 128 x 256 one for the
+//     same LDS traffic (2048x14336x4096 and 512x16384x2048 about 3 % faster,
+//     the same bits);
 //   * waves 4-11 (producers) stream the tiles of later iterations
 //     (activations and codes PD iterations ahead, in registers), dequantize
 //     each weight once into binary16 q * s 2^-f_j and write both tiles into
@@ -236,13 +240,14 @@ constexpr int LDS_ROW = KS + 8;    // halves per LDS row
 constexpr int kProducerWaves = 8;
 constexpr int kStages = 2;         // register stages of the producers
 
-template <int G, int KIND, int TM, int TN, int NPW = kProducerWaves, int PD = kStages>
+template <int G, int KIND, int TM, int TN, int CR = 1, int NPW = kProducerWaves, int PD = kStages>
 __global__ __launch_bounds__(64 * (4 + NPW)) __attribute__((amdgpu_waves_per_eu(1 + NPW / 4, 1 + NPW / 4)))
 void gemm_kernel(const uint8_t *__restrict__ w, int64_t row_bytes,
                     const uint16_t *__restrict__ x16, const int *__restrict__ ex,
                     const int *__restrict__ ew, float *__restrict__ y, int64_t s, int64_t m,
                     int64_t n, int nit, float *__restrict__ ws) {
-  constexpr int BM = 32 * TM, BN = 128 * TN;
+  constexpr int CC = 4 / CR;                     // consumer waves per row group
+  constexpr int BM = 32 * TM * CR, BN = 32 * TN * CC;
   constexpr int SB = ScaleTraits<KIND>::bytes;
   constexpr int NPT = 64 * NPW;                  // producer threads
   constexpr int NT = 256 + NPT;                  // threads
@@ -360,7 +365,8 @@ void gemm_kernel(const uint8_t *__restrict__ w, int64_t row_bytes,
 
   // ---- consumers ----
   const int lr = lane & 31, lh = lane >> 5;
-  const int cb = wid * 32 * TN;                  // this wave's first column in the tile
+  const int cb = (wid % CC) * 32 * TN;           // this wave's first column in the tile
+  const int rb = (wid / CC) * 32 * TM;           // and its first row
   f32x16 acc[TM][TN];
 #pragma unroll
   for (int i = 0; i < TM; ++i)
@@ -379,7 +385,7 @@ void gemm_kernel(const uint8_t *__restrict__ w, int64_t row_bytes,
       f16x8 af[TM], bf[TN];
 #pragma unroll
       for (int i = 0; i < TM; ++i)
-        af[i] = *reinterpret_cast<const f16x8 *>(&at[(i * 32 + lr) * LDS_ROW + 16 * ks + 8 * lh]);
+        af[i] = *reinterpret_cast<const f16x8 *>(&at[(rb + i * 32 + lr) * LDS_ROW + 16 * ks + 8 * lh]);
 #pragma unroll
       for (int t = 0; t < TN; ++t)
         bf[t] = *reinterpret_cast<const f16x8 *>(&bt[(cb + t * 32 + lr) * LDS_ROW + 16 * ks + 8 * lh]);
@@ -393,19 +399,19 @@ void gemm_kernel(const uint8_t *__restrict__ w, int64_t row_bytes,
   }
   // D layout of v_mfma_f32_32x32x16: lane -> column lane % 32, element v ->
   // row 8 (v / 4) + 4 (lane / 32) + v % 4; each output scaled by 2^(e_i + f_j)
-  const int rows_left = (int)(s - m0 - lh * 4);
+  const int rows_left = (int)(s - m0 - rb - lh * 4);
 #pragma unroll
   for (int t = 0; t < TN; ++t) {
     const int jc = cb + t * 32 + lr;
     const int64_t col = n0 + jc;
     if (col < n) {
-      float *out = (gridDim.z == 1 ? y : ws + (int64_t)blockIdx.z * s * n) + (m0 + lh * 4) * n + col;
+      float *out = (gridDim.z == 1 ? y : ws + (int64_t)blockIdx.z * s * n) + (m0 + rb + lh * 4) * n + col;
 #pragma unroll
       for (int i = 0; i < TM; ++i)
 #pragma unroll
         for (int v = 0; v < 16; ++v) {
           const int r = i * 32 + (v >> 2) * 8 + (v & 3);
-          if (r < rows_left) out[(int64_t)r * n] = __builtin_ldexpf(acc[i][t][v], exs[r + lh * 4] + ews[jc]);
+          if (r < rows_left) out[(int64_t)r * n] = __builtin_ldexpf(acc[i][t][v], exs[rb + r + lh * 4] + ews[jc]);
         }
     }
   }
@@ -449,10 +455,10 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float *__restr
   }
 }
 
-template <int G, int KIND, int TM, int TN>
+template <int G, int KIND, int TM, int TN, int CR = 1>
 hipError_t launch_t(const LinearArgs &a, const uint16_t *x16, const int *ex, const int *ew,
                        hipStream_t st) {
-  constexpr int BM = 32 * TM, BN = 128 * TN;
+  constexpr int BM = 32 * TM * CR, BN = 32 * TN * (4 / CR);
   const int64_t nit_all = (a.m + KS - 1) / KS;
   const int64_t gx = (a.n + BN - 1) / BN, gy = (a.s + BM - 1) / BM;
   // Split K when the output tiles alone leave CUs idle (256 CUs, one
@@ -465,7 +471,7 @@ hipError_t launch_t(const LinearArgs &a, const uint16_t *x16, const int *ex, con
   }
   int64_t nit = (nit_all + splits - 1) / splits;
   dim3 grid((unsigned)gx, (unsigned)gy, (unsigned)splits), block(64 * (4 + kProducerWaves));
-  hipLaunchKernelGGL((gemm_kernel<G, KIND, TM, TN>), grid, block, 0, st, a.w, a.row_bytes,
+  hipLaunchKernelGGL((gemm_kernel<G, KIND, TM, TN, CR>), grid, block, 0, st, a.w, a.row_bytes,
                      x16, ex, ew, a.y, a.s, a.m, a.n, (int)nit, a.ws);
   if (splits > 1) return launch_splitk_reduce(a.ws, a.y, a.s * a.n, (int)splits, st);
   return hipGetLastError();
@@ -487,6 +493,10 @@ hipError_t launch_g(const LinearArgs &a, uint16_t *x16, int *ex, int *ew, bool w
   // wave when the 256-column tiles still give every CU a workgroup.
   if (a.s > 64) {
     const int64_t tiles256 = (a.n + 255) / 256 * ((a.s + 127) / 128);
+    // 256 x 128 tiles (2 x 2 consumer waves) once they give every CU a
+    // workgroup, else 128 x 256 ones
+    const int64_t tiles_tall = (a.n + 127) / 128 * ((a.s + 255) / 256);
+    if (tiles_tall >= 256) return launch_t<G, KIND, 4, 2, 2>(a, x16, ex, ew, st);
     if (tiles256 >= 256) return launch_t<G, KIND, 4, 2>(a, x16, ex, ew, st);
     return launch_t<G, KIND, 4, 1>(a, x16, ex, ew, st);
   }
