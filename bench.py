@@ -374,9 +374,19 @@ def gateup_roofline(B: Bench, m):
     per = ms / len(launches)
     nbytes = fused_gateup_bytes(cfg.hidden, cfg.inter, B.G, B.sb)
     achieved = nbytes / (per * 1e-3) / 1e9
+    # the practical ceiling at this size: a plain streaming read of the
+    # packed rows' bytes, timed the same way (graph nodes, copies larger than
+    # the Infinity Cache)
+    rows = 2 * cfg.inter * (cfg.hidden // B.G) * B.sb + 2 * cfg.inter * cfg.hidden
+    ceil = calib_stream(rows)
     return {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
             "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
             "traffic": measured_traffic("gateup_gemv_pmc.md", B.G, B.sb),
+            "stream_ceiling": ceil and {
+                "GB_s": ceil["GB_s"], "frac": round(achieved / ceil["GB_s"], 3),
+                "what": f"plain streaming read of the {rows} bytes of packed rows per launch "
+                        f"(16-byte loads, best of grids {ceil['grids']}), per node of a graph: "
+                        f"{ceil['us']} us; lama32_mojo_amd/calib/q8_calib.hip"},
             "kernel": f"fused rmsnorm + gate|up GEMV {2 * cfg.inter}x{cfg.hidden} + swiglu "
                       f"(the step's dominant kernel): {nbytes} B/launch, {per * 1e3:.2f} us avg "
                       f"over {reps} x {len(launches)} launches (graph replays)"}
@@ -742,6 +752,40 @@ def run_prefill(B: Bench, cfg=LLAMA_1B, M=512):
     }
 
 
+def calib_lib():
+    """libq8calib.so (the calibration kernels), or None when it is not built."""
+    import ctypes
+    path = os.path.join(ROOT, "lama32_mojo_amd", "libq8calib.so")
+    if not os.path.exists(path):
+        return None
+    lib = ctypes.CDLL(path)
+    lib.q8calib_empty_node_us.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_void_p]
+    lib.q8calib_stream_us.argtypes = [ctypes.c_uint64, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                      ctypes.c_void_p]
+    lib.q8calib_cu_read_us.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_uint64, ctypes.c_int,
+                                       ctypes.c_int, ctypes.c_void_p]
+    lib.q8calib_mfma_tflops.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_void_p]
+    return lib
+
+
+def calib_stream(nbytes: int, grids=(4096, 8192)):
+    """Per-node time of a plain streaming read of nbytes (best grid)."""
+    import ctypes
+    lib = calib_lib()
+    if lib is None:
+        return None
+    nb16 = nbytes // 16 * 16
+    copies = max(3, -(-(640 << 20) // nb16))
+    f = ctypes.c_float()
+    best = None
+    for grid in grids:
+        if lib.q8calib_stream_us(nb16, copies, grid, 5, ctypes.byref(f)) != 0:
+            return None
+        if best is None or f.value < best:
+            best = f.value
+    return {"us": round(best, 3), "GB_s": round(nb16 / best / 1e3, 1), "grids": list(grids)}
+
+
 def run_calib(B: Bench):
     """Ceilings the roofline arguments rest on, measured on this GPU:
     the kernel-boundary floor (one dependent empty kernel node of a graph),
@@ -753,10 +797,9 @@ def run_calib(B: Bench):
     shapes.  Kernels: lama32_mojo_amd/calib/q8_calib.hip (libq8calib.so)."""
     import ctypes
     torch = B.torch
-    path = os.path.join(ROOT, "lama32_mojo_amd", "libq8calib.so")
-    if not os.path.exists(path):
-        raise RuntimeError(f"{path} is missing: run __graft_entry__.build()")
-    lib = ctypes.CDLL(path)
+    lib = calib_lib()
+    if lib is None:
+        raise RuntimeError("lama32_mojo_amd/libq8calib.so is missing: run __graft_entry__.build()")
     f = ctypes.c_float()
 
     def call(fn, *a):
@@ -765,12 +808,6 @@ def run_calib(B: Bench):
             raise RuntimeError(f"{fn.__name__} failed ({rc})")
         return float(f.value)
 
-    lib.q8calib_empty_node_us.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_void_p]
-    lib.q8calib_stream_us.argtypes = [ctypes.c_uint64, ctypes.c_int, ctypes.c_int, ctypes.c_int,
-                                      ctypes.c_void_p]
-    lib.q8calib_cu_read_us.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_uint64, ctypes.c_int,
-                                       ctypes.c_int, ctypes.c_void_p]
-    lib.q8calib_mfma_tflops.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_void_p]
     out = {}
     empty = call(lib.q8calib_empty_node_us, 64, 20)
     out["empty_node_us"] = round(empty, 3)
