@@ -188,6 +188,10 @@ class Q8Llama:
         # one-row steps fold rmsnorm, swiglu and the residual adds into the
         # GEMV launches
         self.fuse = bool(fuse)
+        # prompt rows leave each block's down-projection output pending and
+        # add it in the next block's input norm (one residual pass fewer per
+        # block; the same bits as the separate add)
+        self.fold_residual = True
         self.G, self.scale = G, scale
         self.qk = Q8Kernels(ctx, G, scale)
         names = weight_names(cfg)
@@ -212,15 +216,16 @@ class Q8Llama:
                                      o(p + "post_attention_layernorm.weight"), *qn))
         H, QD, KVD, I = cfg.hidden, cfg.q_dim(), cfg.kv_dim(), cfg.inter
         if act_floats is None:
-            # two residual rows sets, one layer's temporaries (the arena is
-            # reset after every layer), the head, and room for one captured
-            # decode step besides a forward pass
+            # three residual row sets (two ping-pong, one pending down
+            # output), one layer's temporaries (the arena is reset after every
+            # layer), the head, and room for one captured decode step besides
+            # a forward pass
             s = max(1, int(max_prefill))
             # (attention scratch grows with the rows up to 15 and is 0 from 16)
             att = q8hip.attention_scratch_floats(min(s, 15), cfg.n_heads, cfg.head_dim,
                                                  self.maxlen)
             layer = s * (4 * H + 3 * QD + 3 * KVD + 2 * I) + att    # incl. q/k norm outputs
-            one = 2 * s * H + layer + H + cfg.vocab + 64
+            one = 3 * s * H + layer + H + cfg.vocab + 64
             act_floats = PAD + cfg.half() + one + (2 * H + (4 * H + 3 * QD + 3 * KVD + 2 * I)
                                                    + q8hip.attention_scratch_floats(
                                                        1, cfg.n_heads, cfg.head_dim, self.maxlen)
@@ -303,9 +308,13 @@ class Q8Llama:
         return oy
 
     def layer(self, L: int, ox: int, s: int, pos0: int, device_pos: bool = False,
-              oh: int | None = None) -> int:
+              oh: int | None = None, pending: int | None = None,
+              oout: int | None = None) -> int:
         """One block on the s rows at ox; the new residual rows go to oh
-        (allocated here when None); returns oh."""
+        (allocated here when None); returns oh.  With pending, the rows at
+        pending (the previous block's down output) are first added to ox in
+        place, in the input norm's launch; with oout, the down output is left
+        at oout instead of being added to oh."""
         cfg, ctx, a, w = self.cfg, self.ctx, self.a, self.w
         lo = self.lo[L]
         H, QD, KVD, I = cfg.hidden, cfg.q_dim(), cfg.kv_dim(), cfg.inter
@@ -315,7 +324,10 @@ class Q8Llama:
                 and lo.up == lo.gate + I * rsH):
             return self._layer_fused(L, ox, pos0, pb, oh)
         xn = a.alloc(s * H)
-        q8hip.rmsnorm(ctx, w.buf, lo.in_norm, a.buf, ox, xn, s, H, cfg.eps)
+        if pending is not None:
+            q8hip.add_rmsnorm(ctx, w.buf, lo.in_norm, a.buf, ox, pending, ox, xn, s, H, cfg.eps)
+        else:
+            q8hip.rmsnorm(ctx, w.buf, lo.in_norm, a.buf, ox, xn, s, H, cfg.eps)
         ld = 0                                            # q, k, v row stride
         if ((s == 1 or not cfg.qk_norm) and lo.k == lo.q + QD * rsH
                 and lo.v == lo.k + KVD * rsH):
@@ -367,14 +379,16 @@ class Q8Llama:
         if s >= 32 and og % 4 == 0 and ou % 4 == 0:
             # prompt rows: the swiglu folded into the down GEMM's pre-pass,
             # gate|up rows read at their stride when stacked
-            om = a.alloc(s * H)
+            om = a.alloc(s * H) if oout is None else oout
             q8hip.linear_swiglu(ctx, w.buf, lo.down, a.buf, og, ou, om, s, I, H, self.G,
                                 self.scale, ld=2 * I if gu_stacked else 0)
         else:
             assert not (gu_stacked and s > 1), "stacked gate|up rows need the strided pre-pass"
             q8hip.swiglu(ctx, a.buf, og, ou, s * I)
-            om = self.linear(og, s, I, lo.down, H)
-        q8hip.add(ctx, a.buf, om, oh, s * H)
+            om = a.alloc(s * H) if oout is None else oout
+            q8hip.linear(ctx, w.buf, lo.down, a.buf, og, om, s, I, H, self.G, self.scale)
+        if oout is None:
+            q8hip.add(ctx, a.buf, om, oh, s * H)
         return oh
 
     def _layer_fused(self, L: int, ox: int, pos0: int, pb, oh: int | None) -> int:
@@ -433,12 +447,18 @@ class Q8Llama:
     def _layers(self, cur: int, s: int, pos0: int, device_pos: bool) -> int:
         """Every layer over the s rows at cur (ping-pong residual buffers);
         returns the offset of the final residual rows."""
-        nxt = self.a.alloc(s * self.cfg.hidden)
+        H = self.cfg.hidden
+        nxt = self.a.alloc(s * H)
+        # (one-row steps fold the residual into the down GEMV instead)
+        pend = self.a.alloc(s * H) if s > 1 and self.fold_residual else None
         for L in range(self.cfg.layers):
             mark = self.a.mark()
-            self.layer(L, cur, s, pos0, device_pos, oh=nxt)
+            self.layer(L, cur, s, pos0, device_pos, oh=nxt,
+                       pending=pend if L > 0 else None, oout=pend)
             self.a.reset(mark)
             cur, nxt = nxt, cur
+        if pend is not None:
+            q8hip.add(self.ctx, self.a.buf, pend, cur, s * H)
         return cur
 
     def _run(self, s: int, pos0: int, device_pos: bool) -> int:

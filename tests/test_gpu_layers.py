@@ -46,10 +46,14 @@ def get(buf, off_f32, shape):
     return buf.download(shape, np.float32, 4 * off_f32)
 
 
-def test_rmsnorm_and_add_rmsnorm(ctx):
-    say("rmsnorm")
-    rng = np.random.default_rng(0)
-    rows, d, eps = 3, 2048, 1e-5
+@pytest.mark.parametrize("d", [64, 100, 1000, 2048, 4096, 5000, 8192, 9000])
+def test_rmsnorm_and_add_rmsnorm(ctx, d):
+    """Every row-length class of the norm (one to 32 register values per
+    thread, ragged rows, and the loop form past 8192) against float64; the
+    residual form's h bit-exact, in place too."""
+    say("rmsnorm", d)
+    rng = np.random.default_rng(d)
+    rows, eps = 3, 1e-5
     x = rng.standard_normal((rows, d)).astype(np.float32)
     o = rng.standard_normal((rows, d)).astype(np.float32)
     wbits = f32_to_bf16_bits((1 + 0.2 * rng.standard_normal(d)).astype(np.float32))
@@ -66,6 +70,12 @@ def test_rmsnorm_and_add_rmsnorm(ctx):
     assert np.array_equal(h, x + o)
     y2 = get(a, 4 * rows * d, (rows, d))
     assert max_rel_err(y2, mo.rmsnorm(h, wbits, eps)) <= 1e-5
+    # residual sum in place (h == x)
+    put(a, 3 * rows * d, x)
+    q8hip.add_rmsnorm(ctx, w, 16, a, 3 * rows * d, rows * d, 3 * rows * d, 4 * rows * d, rows, d,
+                      eps)
+    assert np.array_equal(get(a, 3 * rows * d, (rows, d)), h)
+    assert np.array_equal(get(a, 4 * rows * d, (rows, d)), y2)
     # in place (y == x)
     q8hip.rmsnorm(ctx, w, 16, a, 0, 0, rows, d, eps)
     assert np.array_equal(get(a, 0, (rows, d)), y)
