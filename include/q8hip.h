@@ -226,6 +226,22 @@ int q8_linear_swiglu(q8_ctx *ctx, q8_buf *w, uint64_t owt_u16, q8_buf *a, uint64
                      uint64_t ou_f32, uint64_t oy_f32, int64_t s, int64_t m, int64_t n, int G,
                      int scale_dtype, int64_t ld);
 
+/* y = W rmsnorm(h) for s rows (s x m floats at ox), h = x, or with has_res
+ * h = x + res (res: s x m at ores), h then also stored at oh (which may be
+ * x or res itself): the prompt path's RMSNorm (and residual add) folded into
+ * the binary16 pre-pass of the dequant-GEMM.  Norm weights: m bf16 values at
+ * onorm_u16 of w.  The same bits as q8_rmsnorm (or q8_add_rmsnorm) into a
+ * temporary, then q8_linear on it; the normalised rows are not stored.
+ * s >= 32 and m <= 16384 (otherwise the two calls); x and the weight rows
+ * 16-byte aligned, m a multiple of 8; y may not overlap x, res or h.
+ * Replaces rmsnorm_op + mm_q8_op (q|k|v, src/llama_q8.mojo:159-170) and
+ * k_res_add + rmsnorm_op + mm_q8_op (gate|up, :207-220) of run_layer_q8
+ * for prompt rows. */
+int q8_linear_rmsnorm(q8_ctx *ctx, q8_buf *w, uint64_t owt_u16, uint64_t onorm_u16, float eps,
+                      q8_buf *a, uint64_t ox_f32, int has_res, uint64_t ores_f32,
+                      uint64_t oh_f32, uint64_t oy_f32, int64_t s, int64_t m, int64_t n, int G,
+                      int scale_dtype);
+
 /* The end of a token step in two launches: logits y (n floats at oy) = W
  * rmsnorm(x) over the lm_head's n packed rows (norm weights at onorm of w;
  * as q8_linear_fused with Q8_PRE_RMSNORM), their argmax (as q8_argmax: the

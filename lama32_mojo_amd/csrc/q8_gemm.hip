@@ -4,7 +4,9 @@
 // y[i, j] = sum_k x[i, k] * (q[j, k] * scale[j, k / G])
 // (k_mm_q8's product, src/llama_q8.mojo:73-84) as a dequant-GEMM on
 // v_mfma_f32_32x32x16_f16, in two launches:
-//   1. act16_kernel: each activation row is scaled by a power of two 2^-e_i
+//   1. act16_kernel (or norm16_kernel, which first forms the row's RMSNorm
+//      exactly as rmsnorm_kernel does): each activation row is scaled by a
+//      power of two 2^-e_i
 //      so that its largest |x| lies in [2^14, 2^15), rounded to binary16
 //      (exact for bf16 input: binary16 has three more mantissa bits and the
 //      scaled row sits inside its normal range), and written with e_i.  With
@@ -54,6 +56,41 @@ __device__ __forceinline__ int weight_row_exponent(float mx) {
   return (int)((__builtin_bit_cast(uint32_t, mx) >> 23) & 255u) - 127 - 7 - bias;
 }
 
+// Exponent e of an activation row whose largest |value| (over the block)
+// is mx: the row is stored as binary16 x 2^-e, largest |x| 2^-e in
+// [2^14, 2^15); rows of zeros, inf or NaN keep e = 0.  Block-wide (256
+// threads; red holds 4 floats).
+__device__ __forceinline__ int act_row_exponent(float mx, float *red) {
+  const int tid = threadIdx.x;
+  mx = wave_max(mx);
+  if ((tid & 63) == 0) red[tid >> 6] = mx;
+  __syncthreads();
+  mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  int e = 0;
+  if (mx > 0.0f && mx <= 3.4028235e38f) {
+    e = (int)((__builtin_bit_cast(uint32_t, mx) >> 23) & 255u) - 127 - 14;
+    if (mx < 1.17549435e-38f) e = -126;     // subnormal maximum: as far as 2^126 goes
+    e = e < -126 ? -126 : e;
+  }
+  return e;
+}
+
+// Block b of the weight-row part of a pre-pass: one wave per weight row
+// j = 4 b + wave, the exponent of its f32 scales.
+template <int G>
+__device__ __forceinline__ void weight_exponents(int64_t b, const uint8_t *__restrict__ w,
+                                                 int64_t row_bytes, int64_t m, int64_t n,
+                                                 int *__restrict__ ew) {
+  const int tid = threadIdx.x;
+  const int64_t j = b * 4 + (tid >> 6);
+  if (j >= n) return;
+  const float *sc = reinterpret_cast<const float *>(w + j * row_bytes);
+  float mx = 0.0f;
+  for (int64_t g = tid & 63; g < m / G; g += 64) mx = fmaxf(mx, fabsf(sc[g]));
+  mx = wave_max(mx);
+  if ((tid & 63) == 0) ew[j] = weight_row_exponent(mx);
+}
+
 // Blocks [0, s): one 256-thread block per activation row.  With CH > 0 the
 // row (m <= 2048 CH) stays in registers between the max and the conversion
 // (one pass over memory); CH = 0 reads it twice.  Blocks [s, s + nwb): one
@@ -75,13 +112,7 @@ __global__ __launch_bounds__(256) void act16_kernel(const void *__restrict__ xv,
   const int tid = threadIdx.x;
   if (r >= s) {
     // the whole block takes this branch (no barrier in it)
-    const int64_t j = (r - s) * 4 + (tid >> 6);
-    if (j >= n) return;
-    const float *sc = reinterpret_cast<const float *>(w + j * row_bytes);
-    float mx = 0.0f;
-    for (int64_t g = tid & 63; g < m / G; g += 64) mx = fmaxf(mx, fabsf(sc[g]));
-    mx = wave_max(mx);
-    if ((tid & 63) == 0) ew[j] = weight_row_exponent(mx);
+    weight_exponents<G>(r - s, w, row_bytes, m, n, ew);
     return;
   }
   // 8 consecutive values per step (m is a multiple of 8)
@@ -122,20 +153,7 @@ __global__ __launch_bounds__(256) void act16_kernel(const void *__restrict__ xv,
     }
     *reinterpret_cast<u32x4 *>(x16 + r * m + k) = o;
   };
-  auto exponent = [&](float mx) {
-    mx = wave_max(mx);
-    if ((tid & 63) == 0) red[tid >> 6] = mx;
-    __syncthreads();
-    mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-    // largest |x| * 2^-e in [2^14, 2^15); rows of zeros, inf or NaN keep e = 0
-    int e = 0;
-    if (mx > 0.0f && mx <= 3.4028235e38f) {
-      e = (int)((__builtin_bit_cast(uint32_t, mx) >> 23) & 255u) - 127 - 14;
-      if (mx < 1.17549435e-38f) e = -126;     // subnormal maximum: as far as 2^126 goes
-      e = e < -126 ? -126 : e;
-    }
-    return e;
-  };
+  auto exponent = [&](float mx) { return act_row_exponent(mx, red); };
   float mx = 0.0f;
   int e;
   if constexpr (CH > 0) {
@@ -191,6 +209,93 @@ void launch_act16(const LinearArgs &a, uint16_t *x16, int *ex, int *ew, int64_t 
   else
     Q8_ACT16(0);
 #undef Q8_ACT16
+}
+
+// The pre-pass with the row's RMSNorm folded in (k_rmsnorm_w, after k_res_add
+// when res is set): blocks [0, s) form h = x + res (stored to hout) and
+// y = bf16(wn) h / sqrt(mean(h^2) + eps) exactly as rmsnorm_kernel does --
+// thread t owns elements t, t + 256, ... (at most NV of them), sums their
+// squares in that order and the block adds the threads with block_sum256 --
+// then y's row exponent and binary16 row exactly as act16_kernel forms them
+// from a stored y.  So the GEMM reads the bits that rmsnorm (or add +
+// rmsnorm) and then the plain pre-pass give, without y in memory.  Every
+// load of a row is issued before its first use; the row stays in registers.
+// Blocks [s, s + nwb): weight-row exponents (f32 scales).
+template <int NV, int G>
+__global__ __launch_bounds__(256) void norm16_kernel(const float *x, const float *res, float *hout,
+                                                     const uint16_t *__restrict__ wn, float eps,
+                                                     int64_t s, int64_t m,
+                                                     uint16_t *__restrict__ x16,
+                                                     int *__restrict__ ex,
+                                                     const uint8_t *__restrict__ w,
+                                                     int64_t row_bytes, int64_t n,
+                                                     int *__restrict__ ew) {
+  __shared__ float red[4];
+  const int64_t r = blockIdx.x;
+  const int tid = threadIdx.x;
+  if (r >= s) {
+    weight_exponents<G>(r - s, w, row_bytes, m, n, ew);
+    return;
+  }
+  float v[NV], u[NV];
+  uint16_t wb[NV];
+#pragma unroll
+  for (int j = 0; j < NV; ++j) {
+    const int64_t k = tid + 256 * j;
+    v[j] = k < m ? x[r * m + k] : 0.0f;
+    u[j] = res && k < m ? res[r * m + k] : 0.0f;
+    wb[j] = k < m ? wn[k] : (uint16_t)0;
+  }
+  float ss = 0.0f;
+#pragma unroll
+  for (int j = 0; j < NV; ++j) {
+    if (tid + 256 * j < m) {
+      if (res) v[j] += u[j];
+      ss = __builtin_fmaf(v[j], v[j], ss);
+    }
+  }
+  if (res) {
+#pragma unroll
+    for (int j = 0; j < NV; ++j)
+      if (tid + 256 * j < m) hout[r * m + tid + 256 * j] = v[j];
+  }
+  ss = block_sum256(ss, red);
+  const float inv = 1.0f / sqrtf(ss / (float)m + eps);
+  float mx = 0.0f;
+#pragma unroll
+  for (int j = 0; j < NV; ++j) {
+    if (tid + 256 * j < m) {
+      v[j] = bf16_bits_to_f32(wb[j]) * v[j] * inv;
+      mx = fmaxf(mx, fabsf(v[j]));
+    }
+  }
+  const int e = act_row_exponent(mx, red);
+#pragma unroll
+  for (int j = 0; j < NV; ++j) {
+    const int64_t k = tid + 256 * j;
+    if (k < m) x16[r * m + k] = __builtin_bit_cast(uint16_t, (_Float16)__builtin_ldexpf(v[j], -e));
+  }
+  if (tid == 0) ex[r] = e;
+}
+
+// Rows of at most 16384 elements (the C ABI checks it).
+template <int G>
+void launch_norm16(const LinearArgs &a, uint16_t *x16, int *ex, int *ew, int64_t nw,
+                   hipStream_t st) {
+  const dim3 grid((unsigned)(a.s + (nw + 3) / 4)), block(256);
+  const float *x = static_cast<const float *>(a.x);
+#define Q8_NORM16(NV)                                                                          \
+  hipLaunchKernelGGL((norm16_kernel<NV, G>), grid, block, 0, st, x, a.res, a.hout, a.wn,      \
+                     a.eps, a.s, a.m, x16, ex, a.w, a.row_bytes, nw, ew)
+  if (a.m <= 2048)
+    Q8_NORM16(8);
+  else if (a.m <= 4096)
+    Q8_NORM16(16);
+  else if (a.m <= 8192)
+    Q8_NORM16(32);
+  else
+    Q8_NORM16(64);
+#undef Q8_NORM16
 }
 
 // ---- 2. the GEMM --------------------------------------------------------------
@@ -485,6 +590,8 @@ hipError_t launch_g(const LinearArgs &a, uint16_t *x16, int *ex, int *ew, bool w
   const int64_t nw = KIND == SCALE_F32 && weights ? a.n : 0;
   if (a.x_is_bf16)
     launch_act16<false, G>(a, x16, ex, ew, nw, st);
+  else if (a.wn)
+    launch_norm16<G>(a, x16, ex, ew, nw, st);
   else if (a.up)
     launch_act16<true, G, true>(a, x16, ex, ew, nw, st);
   else

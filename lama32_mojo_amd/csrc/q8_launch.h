@@ -38,6 +38,14 @@ struct LinearArgs {
   // swiglu_kernel stores).
   const float *up = nullptr;
   int64_t ldx = 0;   // GEMM only: row stride of x (and up) in elements; 0: m
+  // GEMM only, f32 x, dense rows: with wn set the rows read are
+  // rmsnorm(x + res) with bf16 weights wn (res null: rmsnorm(x)), formed as
+  // rmsnorm_kernel forms them; with res set, x + res is also stored to hout
+  // (which may be x or res itself).
+  const uint16_t *wn = nullptr;
+  float eps = 0.0f;
+  const float *res = nullptr;
+  float *hout = nullptr;
 };
 // Decode path (s small, f32 x): VALU GEMV.
 hipError_t launch_gemv(const LinearArgs &a, hipStream_t st);

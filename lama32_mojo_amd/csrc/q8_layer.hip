@@ -87,7 +87,7 @@ __global__ __launch_bounds__(256) void rope_kv_kernel(float *q, float *k, const 
   const int half = head_dim / 2;
   const int nall = nheads + nkv;
   const int64_t nrope = (int64_t)s * nall * half;
-  const int qdim = nheads * head_dim, kvdim = nkv * head_dim;
+  const int kvdim = nkv * head_dim;
   const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   const int pos0 = posp ? *posp : pos0_host;
   if (idx < nrope) {

@@ -456,13 +456,15 @@ hipError_t run_gemm_in(q8::LinearArgs la, void *act16, int64_t bytes, hipStream_
   const int64_t xb = la.x_is_bf16 ? 2 : 4;
   const int64_t ldx = la.ldx ? la.ldx : la.m;
   const uint8_t *x0 = static_cast<const uint8_t *>(la.x);
-  const float *u0 = la.up;
-  float *y0 = la.y;
+  const float *u0 = la.up, *res0 = la.res;
+  float *y0 = la.y, *h0 = la.hout;
   const int64_t s = la.s;
   for (int64_t r0 = 0; r0 < s; r0 += rows) {
     la.s = s - r0 < rows ? s - r0 : rows;
     la.x = x0 + r0 * ldx * xb;
     if (u0) la.up = u0 + r0 * ldx;
+    if (res0) la.res = res0 + r0 * la.m;
+    if (h0) la.hout = h0 + r0 * la.m;
     la.y = y0 + r0 * la.n;
     hipError_t e = q8::launch_gemm(la, x16, ex, ew, r0 == 0, st);
     if (e != hipSuccess) return e;
@@ -908,6 +910,72 @@ int q8_linear_swiglu(q8_ctx *ctx, q8_buf *w, uint64_t owt_u16, q8_buf *a, uint64
   if (int rc = set_device(ctx)) return rc;
   hipError_t e = run_gemm(ctx, la);
   if (e != hipSuccess) return hip_fail(ctx, e, "q8_linear_swiglu launch");
+  return ok(ctx);
+}
+
+int q8_linear_rmsnorm(q8_ctx *ctx, q8_buf *w, uint64_t owt_u16, uint64_t onorm_u16, float eps,
+                      q8_buf *a, uint64_t ox_f32, int has_res, uint64_t ores_f32,
+                      uint64_t oh_f32, uint64_t oy_f32, int64_t s, int64_t m, int64_t n, int G,
+                      int scale_dtype) {
+  if (int rc = check_ctx(ctx)) return rc;
+  if (int rc = check_linear(ctx, "q8_linear_rmsnorm", w, owt_u16, s, m, n, G, scale_dtype))
+    return rc;
+  if (!a) return fail(ctx, Q8_ERR_ARG, "q8_linear_rmsnorm: null activation buffer");
+  if (!fits(onorm_u16, (uint64_t)m, 2, w->size))
+    return fail(ctx, Q8_ERR_RANGE, "q8_linear_rmsnorm: norm weights exceed the weight buffer");
+  const uint64_t nx = (uint64_t)s * (uint64_t)m, ny = (uint64_t)s * (uint64_t)n;
+  if (int rc = check_f32(ctx, a, ox_f32, nx, "q8_linear_rmsnorm", "x")) return rc;
+  if (int rc = check_f32(ctx, a, oy_f32, ny, "q8_linear_rmsnorm", "y")) return rc;
+  if (has_res) {
+    if (int rc = check_f32(ctx, a, ores_f32, nx, "q8_linear_rmsnorm", "res")) return rc;
+    if (int rc = check_f32(ctx, a, oh_f32, nx, "q8_linear_rmsnorm", "h")) return rc;
+    // h may be x or res itself (each element is read before the same thread
+    // writes it), but not a shifted copy of either
+    if (bad_alias(oh_f32, nx, ox_f32, nx) || bad_alias(oh_f32, nx, ores_f32, nx))
+      return fail(ctx, Q8_ERR_ARG, "q8_linear_rmsnorm: h partially overlaps x or res");
+  }
+  // y is written while later row chunks of x (res, h) are still to be read
+  if (nx && ny &&
+      (overlaps(ox_f32, ox_f32 + nx, oy_f32, oy_f32 + ny) ||
+       (has_res && (overlaps(ores_f32, ores_f32 + nx, oy_f32, oy_f32 + ny) ||
+                    overlaps(oh_f32, oh_f32 + nx, oy_f32, oy_f32 + ny)))))
+    return fail(ctx, Q8_ERR_ARG, "q8_linear_rmsnorm: y overlaps x, res or h");
+  if (s < kGemmMinRows)
+    return fail(ctx, Q8_ERR_UNSUPPORTED, "q8_linear_rmsnorm: s=%lld (from %lld rows; fewer: "
+                "q8_rmsnorm or q8_add_rmsnorm, then q8_linear)", (long long)s,
+                (long long)kGemmMinRows);
+  if (m > 16384)
+    return fail(ctx, Q8_ERR_UNSUPPORTED, "q8_linear_rmsnorm: m=%lld (at most 16384; longer "
+                "rows: q8_rmsnorm, then q8_linear)", (long long)m);
+  if (!gemm_fits(kAct16Bytes, m, n))
+    return fail(ctx, Q8_ERR_SHAPE, "q8_linear_rmsnorm: m=%lld, n=%lld too large for the GEMM's "
+                "activation buffer (%lld bytes)", (long long)m, (long long)n,
+                (long long)kAct16Bytes);
+  q8::LinearArgs la;
+  la.w = bytes(w, owt_u16 * 2);
+  la.row_bytes = rowstride_u16(m, G, scale_dtype) * 2;
+  la.x = bytes(a, ox_f32 * 4);
+  la.x_is_bf16 = 0;
+  la.y = reinterpret_cast<float *>(bytes(a, oy_f32 * 4));
+  la.s = s;
+  la.m = m;
+  la.n = n;
+  la.G = G;
+  la.kind = scale_dtype;
+  la.wn = reinterpret_cast<const uint16_t *>(bytes(w, onorm_u16 * 2));
+  la.eps = eps;
+  if (has_res) {
+    la.res = reinterpret_cast<const float *>(bytes(a, ores_f32 * 4));
+    la.hout = reinterpret_cast<float *>(bytes(a, oh_f32 * 4));
+  }
+  if (!gemm_aligned(la))
+    return fail(ctx, Q8_ERR_UNSUPPORTED, "q8_linear_rmsnorm: x and the weight rows must be "
+                "16-byte aligned, m a multiple of 8");
+  if (ctx->host_only) return fail(ctx, Q8_ERR_NODEVICE, "q8_linear_rmsnorm: host-only context");
+  if (n == 0) return ok(ctx);
+  if (int rc = set_device(ctx)) return rc;
+  hipError_t e = run_gemm(ctx, la);
+  if (e != hipSuccess) return hip_fail(ctx, e, "q8_linear_rmsnorm launch");
   return ok(ctx);
 }
 

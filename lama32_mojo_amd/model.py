@@ -192,6 +192,9 @@ class Q8Llama:
         # add it in the next block's input norm (one residual pass fewer per
         # block; the same bits as the separate add)
         self.fold_residual = True
+        # prompt rows run the q|k|v and gate|up GEMMs with their norm (and
+        # the residual add before it) in the GEMM's pre-pass (the same bits)
+        self.fold_norm = True
         self.G, self.scale = G, scale
         self.qk = Q8Kernels(ctx, G, scale)
         names = weight_names(cfg)
@@ -307,6 +310,11 @@ class Q8Llama:
         q8hip.linear(self.ctx, self.w.buf, owt, self.a.buf, ox, oy, s, m, n, self.G, self.scale)
         return oy
 
+    def _norm_in_gemm(self, s: int, ox: int) -> bool:
+        """Whether s rows at ox can take q8_linear_rmsnorm (GEMM rows, rows of
+        at most 16384, 16-byte aligned)."""
+        return self.fold_norm and s >= 32 and self.cfg.hidden <= 16384 and ox % 4 == 0
+
     def layer(self, L: int, ox: int, s: int, pos0: int, device_pos: bool = False,
               oh: int | None = None, pending: int | None = None,
               oout: int | None = None) -> int:
@@ -323,22 +331,34 @@ class Q8Llama:
         if (s == 1 and self.fuse and lo.k == lo.q + QD * rsH and lo.v == lo.k + KVD * rsH
                 and lo.up == lo.gate + I * rsH):
             return self._layer_fused(L, ox, pos0, pb, oh)
-        xn = a.alloc(s * H)
-        if pending is not None:
-            q8hip.add_rmsnorm(ctx, w.buf, lo.in_norm, a.buf, ox, pending, ox, xn, s, H, cfg.eps)
-        else:
-            q8hip.rmsnorm(ctx, w.buf, lo.in_norm, a.buf, ox, xn, s, H, cfg.eps)
         ld = 0                                            # q, k, v row stride
-        if ((s == 1 or not cfg.qk_norm) and lo.k == lo.q + QD * rsH
-                and lo.v == lo.k + KVD * rsH):
-            # one stacked q|k|v linear; prompt rows then carry the stride
-            oq = self.linear(xn, s, H, lo.q, QD + 2 * KVD)
+        qkv_stacked = ((s == 1 or not cfg.qk_norm) and lo.k == lo.q + QD * rsH
+                       and lo.v == lo.k + KVD * rsH)
+        if qkv_stacked and self._norm_in_gemm(s, ox):
+            # prompt rows: the input norm (after the pending residual add,
+            # stored over ox) in the stacked q|k|v GEMM's pre-pass
+            oq = a.alloc(s * (QD + 2 * KVD))
+            q8hip.linear_rmsnorm(ctx, w.buf, lo.q, lo.in_norm, cfg.eps, a.buf, ox, oq, s, H,
+                                 QD + 2 * KVD, self.G, self.scale, ores_f32=pending,
+                                 oh_f32=ox if pending is not None else None)
             okk, ov = oq + QD, oq + QD + KVD
-            ld = QD + 2 * KVD if s > 1 else 0
+            ld = QD + 2 * KVD
         else:
-            oq = self.linear(xn, s, H, lo.q, QD)
-            okk = self.linear(xn, s, H, lo.k, KVD)
-            ov = self.linear(xn, s, H, lo.v, KVD)
+            xn = a.alloc(s * H)
+            if pending is not None:
+                q8hip.add_rmsnorm(ctx, w.buf, lo.in_norm, a.buf, ox, pending, ox, xn, s, H,
+                                  cfg.eps)
+            else:
+                q8hip.rmsnorm(ctx, w.buf, lo.in_norm, a.buf, ox, xn, s, H, cfg.eps)
+            if qkv_stacked:
+                # one stacked q|k|v linear; prompt rows then carry the stride
+                oq = self.linear(xn, s, H, lo.q, QD + 2 * KVD)
+                okk, ov = oq + QD, oq + QD + KVD
+                ld = QD + 2 * KVD if s > 1 else 0
+            else:
+                oq = self.linear(xn, s, H, lo.q, QD)
+                okk = self.linear(xn, s, H, lo.k, KVD)
+                ov = self.linear(xn, s, H, lo.v, KVD)
         if cfg.qk_norm:                                   # k_rmsnorm2_w
             oqn, okn = a.alloc(s * QD), a.alloc(s * KVD)
             q8hip.rmsnorm(ctx, w.buf, lo.q_norm, a.buf, oq, oqn, s * cfg.n_heads, cfg.head_dim,
@@ -362,15 +382,24 @@ class Q8Llama:
         oo = self.linear(oao, s, QD, lo.o, H)
         if oh is None:
             oh = a.alloc(s * H)
-        oz = a.alloc(s * H)
-        q8hip.add_rmsnorm(ctx, w.buf, lo.post_norm, a.buf, ox, oo, oh, oz, s, H, cfg.eps)
         gu_stacked = lo.up == lo.gate + I * rsH and (s == 1 or (s >= 32 and I % 4 == 0))
+        oz = None
+        if not (gu_stacked and self._norm_in_gemm(s, ox)):
+            oz = a.alloc(s * H)
+            q8hip.add_rmsnorm(ctx, w.buf, lo.post_norm, a.buf, ox, oo, oh, oz, s, H, cfg.eps)
         if s >= 32:
             # 16-byte aligned gate rows: stacked rows then always take the
             # swiglu pre-pass below, the only path that reads them at their
             # 2I stride
             a.align(4)
-        if gu_stacked:
+        if oz is None:
+            # prompt rows: residual add and post-attention norm in the stacked
+            # gate|up GEMM's pre-pass
+            og = a.alloc(s * 2 * I)
+            q8hip.linear_rmsnorm(ctx, w.buf, lo.gate, lo.post_norm, cfg.eps, a.buf, ox, og, s,
+                                 H, 2 * I, self.G, self.scale, ores_f32=oo, oh_f32=oh)
+            ou = og + I
+        elif gu_stacked:
             og = self.linear(oz, s, H, lo.gate, 2 * I)
             ou = og + I
         else:

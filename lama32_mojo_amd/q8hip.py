@@ -106,6 +106,8 @@ SIGNATURES = {
                                 _I64, _P, _U64, _I, _I, _I, _P, _U64, _U64, ctypes.c_float]),
     "q8_linear_swiglu": (_I, [_P, _P, _U64, _P, _U64, _U64, _U64, _I64, _I64, _I64, _I, _I,
                               _I64]),
+    "q8_linear_rmsnorm": (_I, [_P, _P, _U64, _U64, ctypes.c_float, _P, _U64, _I, _U64, _U64,
+                               _U64, _I64, _I64, _I64, _I, _I]),
     "q8_swiglu": (_I, [_P, _P, _U64, _U64, _I64]),
     "q8_res_add": (_I, [_P, _P, _U64, _U64, _U64, _I64]),
     "q8_add": (_I, [_P, _P, _U64, _U64, _I64]),
@@ -300,6 +302,21 @@ def linear_swiglu(ctx: Context, w: Buffer, owt_u16: int, a: Buffer, og_f32: int,
     ctx.check(ctx._lib.q8_linear_swiglu(ctx.h, w.h, int(owt_u16), a.h, int(og_f32), int(ou_f32),
                                         int(oy_f32), int(s), int(m), int(n), int(G),
                                         scale_code(scale), int(ld)))
+
+
+def linear_rmsnorm(ctx: Context, w: Buffer, owt_u16: int, onorm_u16: int, eps: float, a: Buffer,
+                   ox_f32: int, oy_f32: int, s: int, m: int, n: int, G: int = 64, scale="f16",
+                   ores_f32: int | None = None, oh_f32: int | None = None) -> None:
+    """y = W rmsnorm(x [+ res]) over s >= 32 rows, the norm (and the residual
+    add, stored to oh when ores is given) folded into the GEMM's binary16
+    pre-pass: q8_linear_rmsnorm."""
+    has_res = ores_f32 is not None
+    if has_res and oh_f32 is None:
+        raise ValueError("linear_rmsnorm: a residual needs oh_f32 for x + res")
+    ctx.check(ctx._lib.q8_linear_rmsnorm(ctx.h, w.h, int(owt_u16), int(onorm_u16), float(eps),
+                                         a.h, int(ox_f32), int(has_res),
+                                         int(ores_f32 or 0), int(oh_f32 or 0), int(oy_f32),
+                                         int(s), int(m), int(n), int(G), scale_code(scale)))
 
 
 PRE_NONE, PRE_RMSNORM, PRE_SWIGLU = 0, 1, 2

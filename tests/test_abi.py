@@ -126,6 +126,49 @@ def test_linear_swiglu_validation(hctx):
     a2.free()
 
 
+def test_linear_rmsnorm_validation(hctx):
+    """q8_linear_rmsnorm: prompt rows only (s >= 32) and rows of at most
+    16384; norm weights inside w; x, res, h and y in the arena, h equal to x
+    or res or apart from both, y apart from all three; valid calls reach the
+    device step."""
+    m, n, s = 2048, 64, 32
+    rs = q8hip.rowstride_u16(m)
+    w = hctx.alloc(2 * (n * rs + m))               # rows, then m bf16 norm weights
+    norm = n * rs
+    a = hctx.alloc(4 * (3 * s * m + s * n))
+    L = q8hip.linear_rmsnorm
+    ox, ores, oh, oy = 0, s * m, 2 * s * m, 3 * s * m
+
+    def code(*args, **kw):
+        return code_of(L, hctx, w, 0, norm, 1e-5, a, *args, **kw)[0]
+
+    assert code(ox, oy, s, m, n) == Q8_ERR_NODEVICE
+    assert code(ox, oy, s, m, n, ores_f32=ores, oh_f32=oh) == Q8_ERR_NODEVICE
+    assert code(ox, oy, s, m, n, ores_f32=ores, oh_f32=ox) == Q8_ERR_NODEVICE     # h over x
+    assert code(ox, oy, s, m, n, ores_f32=ores, oh_f32=ores) == Q8_ERR_NODEVICE   # h over res
+    assert code(ox, oy, s, m, n, ores_f32=ores, oh_f32=ox + 8) == Q8_ERR_ARG      # shifted x
+    assert code(ox, oy, s, m, n, ores_f32=ores, oh_f32=ores - 8) == Q8_ERR_ARG    # shifted res
+    assert code(ox, ores, s, m, n, ores_f32=ores, oh_f32=oh) == Q8_ERR_ARG        # y on res
+    assert code(ox, oh, s, m, n, ores_f32=ores, oh_f32=oh) == Q8_ERR_ARG          # y on h
+    assert code(ox, ox + 8, s, m, n) == Q8_ERR_ARG                                # y on x
+    assert code(ox, oy, 31, m, n) == q8hip.Q8_ERR_UNSUPPORTED
+    assert code(ox + 1, oy, s, m, n) == q8hip.Q8_ERR_UNSUPPORTED                  # x misaligned
+    assert code(ox, oy + 8, s, m, n) == Q8_ERR_RANGE
+    assert code_of(L, hctx, w, 0, norm + 8, 1e-5, a, ox, oy, s, m, n)[0] == Q8_ERR_RANGE
+    with pytest.raises(ValueError):
+        L(hctx, w, 0, norm, 1e-5, a, ox, oy, s, m, n, ores_f32=ores)
+    w.free()
+    a.free()
+    # rows longer than 16384
+    m2 = 16384 + 64
+    w2 = hctx.alloc(2 * (n * q8hip.rowstride_u16(m2) + m2))
+    a2 = hctx.alloc(4 * (s * m2 + s * n))
+    assert code_of(L, hctx, w2, 0, n * q8hip.rowstride_u16(m2), 1e-5, a2, 0, s * m2, s, m2,
+                   n)[0] == q8hip.Q8_ERR_UNSUPPORTED
+    w2.free()
+    a2.free()
+
+
 def test_linear_fused_validation(hctx):
     m, n = 2048, 64
     rs = q8hip.rowstride_u16(m)

@@ -48,9 +48,9 @@ def get(buf, off_f32, shape):
 
 @pytest.mark.parametrize("d", [64, 100, 1000, 2048, 4096, 5000, 8192, 9000])
 def test_rmsnorm_and_add_rmsnorm(ctx, d):
-    """Every row-length class of the norm (one to 32 register values per
-    thread, ragged rows, and the loop form past 8192) against float64; the
-    residual form's h bit-exact, in place too."""
+    """Rows of 64 to 9000 elements (ragged ones too: fewer than 256, or not
+    a multiple of 256) against float64; the residual form's h bit-exact, in
+    place too."""
     say("rmsnorm", d)
     rng = np.random.default_rng(d)
     rows, eps = 3, 1e-5
@@ -485,6 +485,103 @@ def test_linear_swiglu_equals_swiglu_then_linear(ctx, G, scale, s, m, n):
     finally:
         a.free()
         w.free()
+
+
+@pytest.mark.parametrize("G,scale", [(64, "f16"), (32, "f32")])
+@pytest.mark.parametrize("s,m,n,res", [(32, 2048, 512, False), (77, 1024, 3072, True),
+                                       (300, 4096, 1000, True), (40, 16384, 256, True),
+                                       (64, 5120, 512, False), (2100, 16384, 64, True)])
+def test_linear_rmsnorm_equals_norm_then_linear(ctx, cor, G, scale, s, m, n, res):
+    """q8_linear_rmsnorm (the RMSNorm, after the residual add, computed in
+    the GEMM's binary16 pre-pass) gives the bits of q8_add_rmsnorm /
+    q8_rmsnorm into a temporary followed by q8_linear on it, stores h = x +
+    res with the bits of q8_add_rmsnorm (h over x in place too), and stays
+    within the GEMM's 1e-3 of float64: rows of 1024..16384 codes (8 to 64
+    values per thread), ragged row counts, and 2100 rows of 16384 codes (the
+    call runs in two row chunks of the activation buffer)."""
+    say("linear_rmsnorm", G, scale, s, m, n, res)
+    rng = np.random.default_rng(s + m + n)
+    rs = q8hip.rowstride_u16(m, G, scale)
+    wsrc = ctx.alloc(2 * n * m)
+    wsrc.upload(f32_to_bf16_bits((0.02 * rng.standard_normal((n, m))).astype(np.float32)))
+    w = ctx.alloc(2 * (n * rs + m))
+    q8hip.quantize_pack(ctx, wsrc, 0, q8hip.Q8_SRC_BF16, n, m, w, 0, G, scale)
+    wsrc.free()
+    onorm = n * rs
+    wbits = f32_to_bf16_bits((1 + 0.2 * rng.standard_normal(m)).astype(np.float32))
+    w.upload(wbits, 2 * onorm)
+    eps = 1e-5
+    x = (3 * rng.standard_normal((s, m))).astype(np.float32)
+    r = rng.standard_normal((s, m)).astype(np.float32)
+    sm, sn = s * m, s * n
+    ox, ores, oh, oz, ox2, oy1, oy2, oy3 = (0, sm, 2 * sm, 3 * sm, 4 * sm, 5 * sm, 5 * sm + sn,
+                                          5 * sm + 2 * sn)
+    a = arena(ctx, 5 * sm + 3 * sn)
+    try:
+        put(a, ox, x)
+        put(a, ores, r)
+        put(a, ox2, x)
+        kw = dict(ores_f32=ores, oh_f32=oh) if res else {}
+        q8hip.linear_rmsnorm(ctx, w, 0, onorm, eps, a, ox, oy2, s, m, n, G, scale, **kw)
+        got = get(a, oy2, (s, n))
+        if res:
+            h = get(a, oh, (s, m))
+            q8hip.add_rmsnorm(ctx, w, onorm, a, ox, ores, oh, oz, s, m, eps)
+            assert np.array_equal(get(a, oh, (s, m)), h)
+            # h stored over x
+            q8hip.linear_rmsnorm(ctx, w, 0, onorm, eps, a, ox2, oy3, s, m, n, G, scale,
+                                 ores_f32=ores, oh_f32=ox2)
+            assert np.array_equal(get(a, oy3, (s, n)), got)
+            assert np.array_equal(get(a, ox2, (s, m)), h)
+        else:
+            h = x
+            q8hip.rmsnorm(ctx, w, onorm, a, ox, oz, s, m, eps)
+            assert np.array_equal(get(a, ox, (s, m)), x)
+        q8hip.linear(ctx, w, 0, a, oz, oy1, s, m, n, G, scale)
+        want = get(a, oy1, (s, n))
+        assert np.all(np.isfinite(want)) and np.array_equal(got, want), \
+            max_rel_err(got, want)
+        if s * m * n <= 300 * 4096 * 1000:
+            rows = np.arange(0, s, max(1, s // 16))
+            pk = w.download((n, rs), np.uint16)
+            ref = cor.linear_f64x(pk, mo.rmsnorm(h[rows], wbits, eps), G, scale)
+            assert max_rel_err(got[rows], ref) <= 1e-3
+    finally:
+        a.free()
+        w.free()
+
+
+def test_model_prompt_folds_equal_separate_launches(ctx):
+    """A prompt whose norms run in the GEMM pre-passes and whose residual adds
+    run in the next block's norm gives the logits bits of the separate
+    rmsnorm / add / linear launches, and the same cache."""
+    say("prompt folds")
+    spec, t, inv = tiny_model(seed=11)
+    maxlen = 64
+    prompt = [int(v) for v in np.random.default_rng(12).integers(0, spec.vocab, size=40)]
+    a = gpu_model(ctx, spec, t, maxlen, max_prefill=40)
+    b = gpu_model(ctx, spec, t, maxlen, max_prefill=40)
+    b.fold_norm = b.fold_residual = False
+    calls = []
+    real = q8hip.linear_rmsnorm
+
+    def counted(*args, **kw):
+        calls.append(1)
+        return real(*args, **kw)
+
+    try:
+        q8hip.linear_rmsnorm = counted
+        la = a.forward(prompt)
+        q8hip.linear_rmsnorm = real
+        assert len(calls) == 2 * spec.layers          # q|k|v and gate|up of every block
+        lb = b.forward(prompt)
+        assert np.all(np.isfinite(la)) and np.array_equal(la, lb)
+        la, lb = a.forward([3]), b.forward([3])
+        assert np.array_equal(la, lb)
+    finally:
+        q8hip.linear_rmsnorm = real
+        a.close()
+        b.close()
 
 
 def test_fused_model_equals_unfused(ctx):
