@@ -267,6 +267,16 @@ int q8_rmsnorm(q8_ctx *ctx, q8_buf *w, uint64_t owt_u16, q8_buf *a,
                uint64_t ox_f32, uint64_t oy_f32, int64_t rows, int64_t d,
                float eps);
 
+/* Per-head RMSNorm (k_rmsnorm2_w, src/llama_common.mojo:228-270: the q and k
+ * head norms of Qwen3) of `heads` consecutive head rows of head_dim in each
+ * of `tokens` rows, token rows ld floats apart (ld = 0: heads * head_dim),
+ * e.g. the q or k heads inside stacked q|k|v rows; y has x's layout and may
+ * be x itself (in place), else it may not overlap x.  Each head row gets the
+ * bits q8_rmsnorm gives it as a dense row. */
+int q8_head_rmsnorm(q8_ctx *ctx, q8_buf *w, uint64_t owt_u16, q8_buf *a, uint64_t ox_f32,
+                    uint64_t oy_f32, int64_t tokens, int64_t heads, int64_t head_dim, int64_t ld,
+                    float eps);
+
 /* h = x + o stored at oh, then y = rmsnorm(h): k_res_add then k_rmsnorm_w
  * (src/llama_common.mojo:354-359,197-225) in one dispatch. */
 int q8_add_rmsnorm(q8_ctx *ctx, q8_buf *w, uint64_t owt_u16, q8_buf *a,

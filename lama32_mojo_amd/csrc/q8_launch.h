@@ -109,9 +109,11 @@ hipError_t launch_embed_gather(const GatherArgs &a, hipStream_t st);
 
 // ---- decode-step layer kernels (q8_layer.hip) ------------------------------
 // RMSNorm of `rows` rows of d; with res != null the rows are x + res, also
-// stored to h_out.
+// stored to h_out.  per > 0: rows in groups of per consecutive rows of d,
+// groups ld elements apart (x, res, h_out and y alike); else dense rows.
 hipError_t launch_rmsnorm(const uint16_t *wn, const float *x, const float *res, float *h_out,
-                          float *y, int64_t rows, int64_t d, float eps, hipStream_t st);
+                          float *y, int64_t rows, int64_t d, float eps, hipStream_t st,
+                          int64_t per = 0, int64_t ld = 0);
 // RoPE on q [s, nheads*head_dim] (row stride ldq) and k [s, nkv*head_dim]
 // (row stride ldk, also v's) in place; rotated k and v go to binary16 cache
 // rows pos0 .. pos0+s-1 (pos0 = *posp if posp).

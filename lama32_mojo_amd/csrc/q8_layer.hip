@@ -49,28 +49,32 @@ __device__ __forceinline__ void rotate(float x0, float x1, float c, float sn, fl
 // ---- RMSNorm (k_rmsnorm_w): y = bf16(w) * x * 1/sqrt(mean(x^2) + eps) -------
 // One 256-thread block per row.  With res != null the row is h = x + res,
 // stored to h_out, and normalised (k_res_add followed by k_rmsnorm_w).
+// Rows come in groups of `per` consecutive rows of d, groups `ld` elements
+// apart (per = 1, ld = d: dense rows; per heads of a token row at stride
+// ld: the per-head norms of q or k inside stacked q|k|v rows, k_rmsnorm2_w).
 __global__ __launch_bounds__(256) void rmsnorm_kernel(const uint16_t *__restrict__ wn,
                                                       const float *x, const float *res,
                                                       float *h_out, float *y, int64_t d,
-                                                      float eps) {
+                                                      float eps, int64_t per, int64_t ld) {
   __shared__ float red[4];
   const int64_t row = blockIdx.x;
-  const float *xr = x + row * d;
-  const float *rr = res ? res + row * d : nullptr;
+  const int64_t base = (row / per) * ld + (row % per) * d;
+  const float *xr = x + base;
+  const float *rr = res ? res + base : nullptr;
   float ss = 0.0f;
   for (int64_t k = threadIdx.x; k < d; k += 256) {
     float v = xr[k];
     if (rr) {
       v += rr[k];
-      h_out[row * d + k] = v;
+      h_out[base + k] = v;
     }
     ss = __builtin_fmaf(v, v, ss);
   }
   ss = block_sum256(ss, red);
   const float inv = 1.0f / sqrtf(ss / (float)d + eps);
-  const float *src = rr ? h_out + row * d : xr;
+  const float *src = rr ? h_out + base : xr;
   for (int64_t k = threadIdx.x; k < d; k += 256)
-    y[row * d + k] = bf16_bits_to_f32(wn[k]) * src[k] * inv;
+    y[base + k] = bf16_bits_to_f32(wn[k]) * src[k] * inv;
 }
 
 // ---- RoPE on q and k + KV append (k_rope_qk_copy2) ----------------------------
@@ -970,10 +974,15 @@ hipError_t launch_attn_hd(const AttnArgs &a, hipStream_t st) {
 }  // namespace
 
 hipError_t launch_rmsnorm(const uint16_t *wn, const float *x, const float *res, float *h_out,
-                          float *y, int64_t rows, int64_t d, float eps, hipStream_t st) {
+                          float *y, int64_t rows, int64_t d, float eps, hipStream_t st,
+                          int64_t per, int64_t ld) {
   if (rows == 0) return hipSuccess;
+  if (per <= 0) {          // dense rows
+    per = 1;
+    ld = d;
+  }
   hipLaunchKernelGGL(rmsnorm_kernel, dim3((unsigned)rows), dim3(256), 0, st, wn, x, res, h_out, y,
-                     d, eps);
+                     d, eps, per, ld);
   return hipGetLastError();
 }
 

@@ -1057,6 +1057,38 @@ int q8_head_argmax(q8_ctx *ctx, q8_buf *w, uint64_t owt_u16, uint64_t onorm_u16,
   return ok(ctx);
 }
 
+int q8_head_rmsnorm(q8_ctx *ctx, q8_buf *w, uint64_t owt_u16, q8_buf *a, uint64_t ox_f32,
+                    uint64_t oy_f32, int64_t tokens, int64_t heads, int64_t head_dim, int64_t ld,
+                    float eps) {
+  if (int rc = check_ctx(ctx)) return rc;
+  if (!w || !a) return fail(ctx, Q8_ERR_ARG, "q8_head_rmsnorm: null buffer");
+  if (tokens < 0 || heads <= 0 || head_dim <= 0 || heads > INT32_MAX / head_dim ||
+      tokens > INT32_MAX / heads)
+    return fail(ctx, Q8_ERR_SHAPE, "q8_head_rmsnorm: tokens=%lld, heads=%lld, head_dim=%lld",
+                (long long)tokens, (long long)heads, (long long)head_dim);
+  const int64_t width = heads * head_dim;
+  if (ld == 0) ld = width;
+  if (ld < width)
+    return fail(ctx, Q8_ERR_SHAPE, "q8_head_rmsnorm: row stride %lld (0, or at least "
+                "heads * head_dim = %lld)", (long long)ld, (long long)width);
+  if (!fits(owt_u16, (uint64_t)head_dim, 2, w->size))
+    return fail(ctx, Q8_ERR_RANGE, "q8_head_rmsnorm: norm weights exceed the weight buffer");
+  const uint64_t span = rows_span(tokens, ld, (uint64_t)width);
+  if (int rc = check_f32(ctx, a, ox_f32, span, "q8_head_rmsnorm", "x")) return rc;
+  if (int rc = check_f32(ctx, a, oy_f32, span, "q8_head_rmsnorm", "y")) return rc;
+  // y is x itself (in place) or apart from every row of x
+  if (oy_f32 != ox_f32 && span && overlaps(ox_f32, ox_f32 + span, oy_f32, oy_f32 + span))
+    return fail(ctx, Q8_ERR_ARG, "q8_head_rmsnorm: y overlaps x without being x");
+  if (ctx->host_only) return fail(ctx, Q8_ERR_NODEVICE, "q8_head_rmsnorm: host-only context");
+  if (tokens == 0) return ok(ctx);
+  if (int rc = set_device(ctx)) return rc;
+  hipError_t e = q8::launch_rmsnorm(reinterpret_cast<const uint16_t *>(bytes(w, owt_u16 * 2)),
+                                    fptr(a, ox_f32), nullptr, nullptr, fptr(a, oy_f32),
+                                    tokens * heads, head_dim, eps, ctx->stream, heads, ld);
+  if (e != hipSuccess) return hip_fail(ctx, e, "q8_head_rmsnorm launch");
+  return ok(ctx);
+}
+
 int q8_rmsnorm(q8_ctx *ctx, q8_buf *w, uint64_t owt_u16, q8_buf *a, uint64_t ox_f32,
                uint64_t oy_f32, int64_t rows, int64_t d, float eps) {
   if (int rc = check_ctx(ctx)) return rc;

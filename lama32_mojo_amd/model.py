@@ -332,8 +332,7 @@ class Q8Llama:
                 and lo.up == lo.gate + I * rsH):
             return self._layer_fused(L, ox, pos0, pb, oh)
         ld = 0                                            # q, k, v row stride
-        qkv_stacked = ((s == 1 or not cfg.qk_norm) and lo.k == lo.q + QD * rsH
-                       and lo.v == lo.k + KVD * rsH)
+        qkv_stacked = lo.k == lo.q + QD * rsH and lo.v == lo.k + KVD * rsH
         if qkv_stacked and self._norm_in_gemm(s, ox):
             # prompt rows: the input norm (after the pending residual add,
             # stored over ox) in the stacked q|k|v GEMM's pre-pass
@@ -359,7 +358,13 @@ class Q8Llama:
                 oq = self.linear(xn, s, H, lo.q, QD)
                 okk = self.linear(xn, s, H, lo.k, KVD)
                 ov = self.linear(xn, s, H, lo.v, KVD)
-        if cfg.qk_norm:                                   # k_rmsnorm2_w
+        if cfg.qk_norm and ld:                            # k_rmsnorm2_w
+            # the q and k heads normalised in place inside the stacked rows
+            q8hip.head_rmsnorm(ctx, w.buf, lo.q_norm, a.buf, oq, oq, s, cfg.n_heads,
+                               cfg.head_dim, ld, cfg.eps)
+            q8hip.head_rmsnorm(ctx, w.buf, lo.k_norm, a.buf, okk, okk, s, cfg.n_kv,
+                               cfg.head_dim, ld, cfg.eps)
+        elif cfg.qk_norm:
             oqn, okn = a.alloc(s * QD), a.alloc(s * KVD)
             q8hip.rmsnorm(ctx, w.buf, lo.q_norm, a.buf, oq, oqn, s * cfg.n_heads, cfg.head_dim,
                           cfg.eps)

@@ -75,6 +75,8 @@ SIGNATURES = {
     "q8_head_argmax": (_I, [_P, _P, _U64, _U64, ctypes.c_float, _P, _U64, _U64, _I64, _I64, _I,
                            _I, _P, _U64, _P, _U64, _I64, _I, _U64, _U64]),
     "q8_rmsnorm": (_I, [_P, _P, _U64, _P, _U64, _U64, _I64, _I64, ctypes.c_float]),
+    "q8_head_rmsnorm": (_I, [_P, _P, _U64, _P, _U64, _U64, _I64, _I64, _I64, _I64,
+                             ctypes.c_float]),
     "q8_st_open": (_I, [ctypes.c_char_p, ctypes.POINTER(_P)]),
     "q8_st_close": (None, [_P]),
     "q8_st_error": (ctypes.c_char_p, []),
@@ -391,6 +393,15 @@ def rmsnorm(ctx: Context, w: Buffer, owt_u16: int, a: Buffer, ox_f32: int, oy_f3
             rows: int, d: int, eps: float) -> None:
     ctx.check(ctx._lib.q8_rmsnorm(ctx.h, w.h, int(owt_u16), a.h, int(ox_f32), int(oy_f32),
                                   int(rows), int(d), float(eps)))
+
+
+def head_rmsnorm(ctx: Context, w: Buffer, owt_u16: int, a: Buffer, ox_f32: int, oy_f32: int,
+                 tokens: int, heads: int, head_dim: int, ld: int = 0, eps: float = 1e-6) -> None:
+    """Per-head RMSNorm of `heads` head rows in each of `tokens` rows at row
+    stride ld (0: dense), y in x's layout (in place allowed): q8_head_rmsnorm."""
+    ctx.check(ctx._lib.q8_head_rmsnorm(ctx.h, w.h, int(owt_u16), a.h, int(ox_f32), int(oy_f32),
+                                       int(tokens), int(heads), int(head_dim), int(ld),
+                                       float(eps)))
 
 
 def add_rmsnorm(ctx: Context, w: Buffer, owt_u16: int, a: Buffer, ox_f32: int, oo_f32: int,

@@ -126,6 +126,34 @@ def test_linear_swiglu_validation(hctx):
     a2.free()
 
 
+def test_head_rmsnorm_validation(hctx):
+    """q8_head_rmsnorm: heads of head_dim inside rows of ld >= heads *
+    head_dim, in place or apart from x, norm weights inside w; valid calls
+    reach the device step."""
+    tokens, heads, hd, ld = 5, 4, 128, 1024
+    w = hctx.alloc(2 * hd)
+    a = hctx.alloc(4 * (2 * tokens * ld))
+    H = q8hip.head_rmsnorm
+
+    def code(ox, oy, t=tokens, h=heads, d=hd, l=ld, wbuf=w, owt=0):
+        return code_of(H, hctx, wbuf, owt, a, ox, oy, t, h, d, l, 1e-6)[0]
+
+    assert code(0, 0) == Q8_ERR_NODEVICE                       # in place
+    assert code(0, tokens * ld) == Q8_ERR_NODEVICE             # apart
+    assert code(512, 512) == Q8_ERR_NODEVICE                   # k heads after 4 q heads
+    assert code(0, 8) == Q8_ERR_ARG                            # shifted copy of x
+    assert code(0, 0, l=heads * hd - 1) == Q8_ERR_SHAPE       # rows narrower than the heads
+    assert code(0, 0, l=0) == Q8_ERR_NODEVICE                  # dense
+    span = (tokens - 1) * ld + heads * hd
+    assert code(0, 2 * tokens * ld - span) == Q8_ERR_NODEVICE  # y ends at the arena's end
+    assert code(0, 2 * tokens * ld - span + 4) == Q8_ERR_RANGE # ... and past it
+    assert code(0, 0, h=0) == Q8_ERR_SHAPE
+    assert code(0, 0, owt=1) == Q8_ERR_RANGE                   # norm weights past w
+    assert code(0, 0, t=0) == Q8_ERR_NODEVICE
+    w.free()
+    a.free()
+
+
 def test_linear_rmsnorm_validation(hctx):
     """q8_linear_rmsnorm: prompt rows only (s >= 32) and rows of at most
     16384; norm weights inside w; x, res, h and y in the arena, h equal to x

@@ -778,6 +778,66 @@ def test_decode_attention_qk_norm_equals_rmsnorm_rope_attention(ctx, head_dim, n
         b.free()
 
 
+@pytest.mark.parametrize("tokens,heads,hd,ld", [(3, 16, 128, 4096), (40, 8, 128, 2048),
+                                                (7, 32, 64, 3072), (5, 4, 128, 0)])
+def test_head_rmsnorm_equals_dense_rows(ctx, tokens, heads, hd, ld):
+    """q8_head_rmsnorm over the heads inside strided rows (q or k of stacked
+    q|k|v) gives each head row the bits q8_rmsnorm gives it as a dense row,
+    in place and into another buffer, and leaves the rest of the rows alone."""
+    say("head_rmsnorm", tokens, heads, hd, ld)
+    rng = np.random.default_rng(tokens * heads)
+    width = heads * hd
+    L = ld or width
+    rows = rng.standard_normal((tokens, L)).astype(np.float32)
+    wbits = f32_to_bf16_bits((1 + 0.3 * rng.standard_normal(hd)).astype(np.float32))
+    w = ctx.alloc(2 * hd)
+    w.upload(wbits)
+    dense = np.ascontiguousarray(rows[:, :width]).reshape(tokens * heads, hd)
+    od, ody, ox, oy = 0, tokens * width, 2 * tokens * width, 2 * tokens * width + tokens * L
+    a = arena(ctx, oy + tokens * L)
+    try:
+        put(a, od, dense)
+        q8hip.rmsnorm(ctx, w, 0, a, od, ody, tokens * heads, hd, 1e-6)
+        want = get(a, ody, (tokens, width))
+        assert max_rel_err(want, mo.head_rmsnorm(rows[:, :width], wbits, heads, hd, 1e-6)) <= 1e-5
+        put(a, ox, rows)
+        put(a, oy, np.zeros_like(rows))
+        q8hip.head_rmsnorm(ctx, w, 0, a, ox, oy, tokens, heads, hd, ld, 1e-6)
+        got = get(a, oy, (tokens, L))
+        assert np.array_equal(got[:, :width], want)
+        assert not got[:, width:].any()
+        q8hip.head_rmsnorm(ctx, w, 0, a, ox, ox, tokens, heads, hd, ld, 1e-6)
+        got = get(a, ox, (tokens, L))
+        assert np.array_equal(got[:, :width], want)
+        assert np.array_equal(got[:, width:], rows[:, width:])
+    finally:
+        a.free()
+        w.free()
+
+
+def test_qwen_style_model_long_prompt(ctx):
+    """A 40-token prompt through a Qwen3-style tiny model (q/k head norms):
+    q|k|v as one stacked GEMM whose q and k heads are normalised in place at
+    the row stride, the norms in the GEMM pre-passes; logits within 3e-3 of
+    the float64 model, and the same bits with the separate norm and add
+    launches."""
+    say("qwen-style long prompt")
+    spec, t, inv = qwen_tiny(seed=13)
+    maxlen = 64
+    prompt = [int(v) for v in np.random.default_rng(14).integers(0, spec.vocab, size=40)]
+    ref = mo.OracleModel(spec, t, inv, maxlen)
+    m = gpu_model(ctx, spec, t, maxlen, max_prefill=40)
+    u = gpu_model(ctx, spec, t, maxlen, max_prefill=40)
+    u.fold_norm = u.fold_residual = False
+    try:
+        lg, lr = m.forward(prompt), ref.forward(prompt)
+        assert max_rel_err(lg, lr) <= 3e-3, max_rel_err(lg, lr)
+        assert np.array_equal(u.forward(prompt), lg)
+    finally:
+        m.close()
+        u.close()
+
+
 def test_qwen_style_model_forward_and_greedy_decode(ctx):
     """Qwen3-style tiny model (q/k head norms, plain RoPE, head_dim 128):
     logits within 1e-3 of the float64 model, the same greedy ids through
