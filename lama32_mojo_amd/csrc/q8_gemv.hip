@@ -494,7 +494,9 @@ inline bool long_row_groups(const LinearArgs &a) {
 // Shape classes (tuned on MI355X, decode shapes of Llama-3.2-1B / Qwen3-8B):
 //   long rows (m > 4096):         K split over the 4 waves, 4 rows per workgroup
 //   vocabulary heads (n >= 64K):  2 rows per wave, up to 8192 workgroups
+//   one row, n >= 16384:          2 rows per wave, up to 2048 workgroups
 //   wide (n >= 8192):             4 rows per wave, up to 1024 workgroups
+//   one row, n >= 4096:           2 rows per wave
 //   small:                        1 row per wave
 template <int G, int KIND, int S>
 hipError_t launch_rows(const LinearArgs &a, const float *x, float *y, hipStream_t st) {
@@ -509,6 +511,10 @@ hipError_t launch_rows(const LinearArgs &a, const float *x, float *y, hipStream_
   // round of loads, covers the latency: 2 steps made the 1B lm_head 42 ->
   // 47 us)
   if (a.n >= 65536) return launch_fast_t<G, KIND, S, 2, 1, 1>(a, x, y, 8192, st);
+  // one row, 16384 .. 65535 outputs: 2 rows per wave, up to 2048 workgroups
+  // (Qwen3-8B gate|up 4096 -> 24576: its decode-linears step 1.762 -> 1.750
+  // ms; the 8192 x 2048 linear keeps 4 rows, 2 were 0.4-1.1 % slower)
+  if (S == 1 && a.n >= 16384) return launch_fast<G, KIND, S, 2, 1>(a, x, y, 2048, st);
   if (a.n >= 8192) return launch_fast<G, KIND, S, 4, 1>(a, x, y, 1024, st);
   // one row, 4096 .. 8191 outputs: 2 rows per wave (Qwen3-8B o and q|k|v)
   if (S == 1 && a.n >= 4096) return launch_fast<G, KIND, S, 2, 1>(a, x, y, 2048, st);
