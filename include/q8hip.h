@@ -316,7 +316,9 @@ uint64_t q8_attention_scratch_floats(int64_t s, int nheads, int head_dim,
  * head), below that per-split partials in q8_attention_scratch_floats()
  * floats at oscratch (oscratch is unused when that is 0).  head_dim 64 or
  * 128, nheads / nkv in {1, 2, 4, 8}.  Position as in q8_rope_kv.  Row i of q
- * at oq + i*ldq (ldq = 0: nheads*head_dim, dense); out is dense. */
+ * at oq + i*ldq (ldq = 0: nheads*head_dim, dense); out is dense.  From
+ * s = 16 on, q and out must start 16-byte aligned and ldq be a multiple of 4
+ * (Q8_ERR_UNSUPPORTED otherwise). */
 int q8_attention(q8_ctx *ctx, q8_buf *a, uint64_t oq_f32, q8_buf *kv,
                  uint64_t okc_f16, uint64_t ovc_f16, int64_t maxlen,
                  uint64_t oy_f32, uint64_t oscratch_f32, int64_t s, int64_t pos0,

@@ -1246,6 +1246,12 @@ int q8_attention(q8_ctx *ctx, q8_buf *a, uint64_t oq_f32, q8_buf *kv, uint64_t o
       overlaps(oscratch_f32, oscratch_f32 + sn, oq_f32, oq_f32 + qspan) ||
       overlaps(oscratch_f32, oscratch_f32 + sn, oy_f32, oy_f32 + qn))
     return fail(ctx, Q8_ERR_ARG, "q8_attention: q, out and scratch must not overlap");
+  // The one-pass kernel moves q and out rows as 16-byte vectors.
+  const uintptr_t abase = reinterpret_cast<uintptr_t>(a->ptr);
+  if (s >= q8::kPrefillMinRows &&
+      ((abase + oq_f32 * 4) % 16 != 0 || (abase + oy_f32 * 4) % 16 != 0 || ldq % 4 != 0))
+    return fail(ctx, Q8_ERR_UNSUPPORTED, "q8_attention: from %d rows on, q and out must start "
+                "16-byte aligned and the q row stride be a multiple of 4", q8::kPrefillMinRows);
   if (!fits(okc_f16, cn, 2, kv->size) || !fits(ovc_f16, cn, 2, kv->size))
     return fail(ctx, Q8_ERR_RANGE, "q8_attention: K or V cache block exceeds the KV buffer");
   if (int rc = check_pos(ctx, posbuf, opos_i32, pos0, s, maxlen, "q8_attention")) return rc;

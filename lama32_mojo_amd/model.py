@@ -306,6 +306,7 @@ class Q8Llama:
 
     # ---- layer runner (run_layer_q8) ---------------------------------------
     def linear(self, ox: int, s: int, m: int, owt: int, n: int) -> int:
+        self.a.align(4)                 # 16-byte rows for the vector kernels that read them
         oy = self.a.alloc(s * n)
         q8hip.linear(self.ctx, self.w.buf, owt, self.a.buf, ox, oy, s, m, n, self.G, self.scale)
         return oy
@@ -336,6 +337,7 @@ class Q8Llama:
         if qkv_stacked and self._norm_in_gemm(s, ox):
             # prompt rows: the input norm (after the pending residual add,
             # stored over ox) in the stacked q|k|v GEMM's pre-pass
+            a.align(4)
             oq = a.alloc(s * (QD + 2 * KVD))
             q8hip.linear_rmsnorm(ctx, w.buf, lo.q, lo.in_norm, cfg.eps, a.buf, ox, oq, s, H,
                                  QD + 2 * KVD, self.G, self.scale, ores_f32=pending,
@@ -365,12 +367,14 @@ class Q8Llama:
             q8hip.head_rmsnorm(ctx, w.buf, lo.k_norm, a.buf, okk, okk, s, cfg.n_kv,
                                cfg.head_dim, ld, cfg.eps)
         elif cfg.qk_norm:
+            a.align(4)
             oqn, okn = a.alloc(s * QD), a.alloc(s * KVD)
             q8hip.rmsnorm(ctx, w.buf, lo.q_norm, a.buf, oq, oqn, s * cfg.n_heads, cfg.head_dim,
                           cfg.eps)
             q8hip.rmsnorm(ctx, w.buf, lo.k_norm, a.buf, okk, okn, s * cfg.n_kv, cfg.head_dim,
                           cfg.eps)
             oq, okk = oqn, okn
+        a.align(4)                      # q and out of the prompt attention: 16-byte aligned
         oao = a.alloc(s * QD)
         if s == 1:
             # (q and k are already normalised here when the model has q/k norms)

@@ -453,6 +453,11 @@ def test_qkv_row_stride_validation(hctx):
     assert attn(2 * kvd, ld)[0] == Q8_ERR_NODEVICE
     # a span that reaches the output
     assert attn(oinv + hd - (s - 1) * ld - qd + 1, ld)[0] == Q8_ERR_ARG
+    # 16 rows take the one-pass kernel, which moves q and out in 16-byte vectors
+    for oq, ldq, oy in ((1, ld, oinv + hd), (0, ld + 1, oinv + hd), (0, ld, oinv + hd + 2)):
+        c, msg = code_of(q8hip.attention, hctx, a, oq, kv, 0, blk, maxlen, oy, 0, s, 0, nh, nkv,
+                         hd, ldq=ldq)
+        assert c == q8hip.Q8_ERR_UNSUPPORTED and "aligned" in msg, (oq, ldq, oy)
     for b in (a, kv):
         b.free()
 
