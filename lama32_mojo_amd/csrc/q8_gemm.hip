@@ -312,7 +312,8 @@ __device__ __forceinline__ f16x8 dequant8(uint32_t d0, uint32_t d1, f16x2 s2) {
 }
 
 // One workgroup per BM x BN output tile (BM = 32 TM CR, BN = 32 TN (4 /
-// CR)), its 12 waves split by role, three per SIMD:
+// CR)), its 4 + NPW waves split by role (12, three per SIMD; 8 with 64 x 64
+// tiles):
 //   * waves 0-3 (consumers) only read MFMA fragments from LDS and issue the
 //     MFMAs, each over 32 TM rows and 32 TN columns of the tile (TM x TN
 //     accumulator tiles of 32 x 32): with CR = 1 all four share the BM rows
@@ -320,7 +321,7 @@ __device__ __forceinline__ f16x8 dequant8(uint32_t d0, uint32_t d1, f16x2 s2) {
 //     tile dequantizes half the weights per flop of a 128 x 256 one for the
 //     same LDS traffic (2048x14336x4096 and 512x16384x2048 about 3 % faster,
 //     the same bits);
-//   * waves 4-11 (producers) stream the tiles of later iterations
+//   * waves 4 .. 3 + NPW (producers) stream the tiles of later iterations
 //     (activations and codes PD iterations ahead, in registers), dequantize
 //     each weight once into binary16 q * s 2^-f_j and write both tiles into
 //     a double-buffered LDS stage.
@@ -560,7 +561,7 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float *__restr
   }
 }
 
-template <int G, int KIND, int TM, int TN, int CR = 1>
+template <int G, int KIND, int TM, int TN, int CR = 1, int NPW = kProducerWaves>
 hipError_t launch_t(const LinearArgs &a, const uint16_t *x16, const int *ex, const int *ew,
                        hipStream_t st) {
   constexpr int BM = 32 * TM * CR, BN = 32 * TN * (4 / CR);
@@ -575,8 +576,8 @@ hipError_t launch_t(const LinearArgs &a, const uint16_t *x16, const int *ex, con
       splits *= 2;
   }
   int64_t nit = (nit_all + splits - 1) / splits;
-  dim3 grid((unsigned)gx, (unsigned)gy, (unsigned)splits), block(64 * (4 + kProducerWaves));
-  hipLaunchKernelGGL((gemm_kernel<G, KIND, TM, TN, CR>), grid, block, 0, st, a.w, a.row_bytes,
+  dim3 grid((unsigned)gx, (unsigned)gy, (unsigned)splits), block(64 * (4 + NPW));
+  hipLaunchKernelGGL((gemm_kernel<G, KIND, TM, TN, CR, NPW>), grid, block, 0, st, a.w, a.row_bytes,
                      x16, ex, ew, a.y, a.s, a.m, a.n, (int)nit, a.ws);
   if (splits > 1) return launch_splitk_reduce(a.ws, a.y, a.s * a.n, (int)splits, st);
   return hipGetLastError();
@@ -605,6 +606,19 @@ hipError_t launch_g(const LinearArgs &a, uint16_t *x16, int *ex, int *ew, bool w
     const int64_t tiles_tall = (a.n + 127) / 128 * ((a.s + 255) / 256);
     if (tiles_tall >= 256) return launch_t<G, KIND, 4, 2, 2>(a, x16, ex, ew, st);
     if (tiles256 >= 256) return launch_t<G, KIND, 4, 2>(a, x16, ex, ew, st);
+    // Rows of at most 4096 codes: 64-row tiles rather than a K split, which
+    // costs a reduce launch (about 5 us here).  64 x 64 tiles (2 x 2
+    // consumer waves over one 32 x 32 tile each, 4 producer waves) when they
+    // give at most one workgroup per CU, else 64 x 128 ones if those do
+    // (1B prompt of 512 rows: o 512x2048x2048 25.0 -> 21.0 us, q|k|v
+    // 512x3072x2048 28.6 -> 24.8 us with their pre-pass and reduce).
+    // Longer rows keep 128 x 128 tiles: 64-row tiles read each weight tile
+    // for twice as many row blocks (down 512x2048x8192 42.7 -> 50.3 us).
+    if (a.m <= 4096) {
+      const int64_t rb64 = (a.s + 63) / 64;
+      if ((a.n + 63) / 64 * rb64 <= 256) return launch_t<G, KIND, 1, 1, 2, 4>(a, x16, ex, ew, st);
+      if ((a.n + 127) / 128 * rb64 <= 256) return launch_t<G, KIND, 2, 1>(a, x16, ex, ew, st);
+    }
     return launch_t<G, KIND, 4, 1>(a, x16, ex, ew, st);
   }
   return launch_t<G, KIND, 2, 1>(a, x16, ex, ew, st);
