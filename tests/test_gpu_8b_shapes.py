@@ -16,7 +16,9 @@ rows; the dequant-GEMM's 256-column tiles and its K = 14336 pre-pass; the
 prompt-row attention at 2048 rows.
 
 Bars (written in each test): the f32 GEMV / few-row / small-batch paths
-within 1e-5 normwise of float64 (exact products, f32 sums); the fused GEMV
+within 1e-5 normwise of float64 (f32 products on the GEMV and few-row
+paths, x as bf16 hi + lo with a residual below 2^-17 |x| on the small-batch
+path; f32 sums); the fused GEMV
 within 1e-5 of float64 rmsnorm / swiglu / residual around the float64
 linear; the f16-MFMA GEMM within 1e-3 (the product contract), also per
 activation row, and per output column at 2e-3 for small weights; attention
