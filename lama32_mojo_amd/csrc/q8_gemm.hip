@@ -29,8 +29,8 @@
 // Cost per weight (dequantized once per workgroup, used by BM rows): 1.75
 // VALU operations (one xor per 4 codes, then per 2 codes a v_perm that
 // builds binary16 1024 + (q + 128), a packed subtract of 1152 and a packed
-// multiply by the scale) and one 2-byte LDS write, read back by 4 consumer
-// waves.
+// multiply by the scale) and one 2-byte LDS write, read back by the one
+// consumer wave that owns its column (two when the consumers sit 2 x 2).
 #include "q8_device.h"
 #include "q8_launch.h"
 
