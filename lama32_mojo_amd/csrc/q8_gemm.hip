@@ -327,9 +327,9 @@ __device__ __forceinline__ f16x8 dequant8(uint32_t d0, uint32_t d1, f16x2 s2) {
 //     a double-buffered LDS stage.
 // So the dequantizing VALU work runs beside the matrix core instead of in
 // the MFMA waves' instruction stream; one barrier per iteration hands the
-// stages over.  Tiles hold KS = 64 codes of K; LDS rows are padded by 16
-// bytes (the 16-byte fragment reads of 8 neighbouring rows fall on
-// different banks).
+// stages over.  Tiles hold KS = 64 codes of K (128 on the 64-row tiles);
+// LDS rows are padded by 16 bytes (the 16-byte fragment reads of 8
+// neighbouring rows fall on different banks).
 //
 // Measured on the 1B / 8B prefill shapes against one 8-wave role-free form
 // (every wave staging, dequantizing its own columns in registers and
@@ -341,12 +341,12 @@ __device__ __forceinline__ f16x8 dequant8(uint32_t d0, uint32_t d1, f16x2 s2) {
 // about 385 GB/s of 16-byte reads and 174 GB/s of 16-byte writes per CU
 // here), and 4 producer waves instead of 8, or 3-4 register stages instead
 // of 2, were slower or equal.
-constexpr int KS = 64;             // k per iteration
-constexpr int LDS_ROW = KS + 8;    // halves per LDS row
+constexpr int kIterCodes = 64;     // k per iteration (128 on 64-row tiles)
 constexpr int kProducerWaves = 8;
 constexpr int kStages = 2;         // register stages of the producers
 
-template <int G, int KIND, int TM, int TN, int CR = 1, int NPW = kProducerWaves, int PD = kStages>
+template <int G, int KIND, int TM, int TN, int CR = 1, int NPW = kProducerWaves, int PD = kStages,
+          int KSZ = kIterCodes>
 __global__ __launch_bounds__(64 * (4 + NPW)) __attribute__((amdgpu_waves_per_eu(1 + NPW / 4, 1 + NPW / 4)))
 void gemm_kernel(const uint8_t *__restrict__ w, int64_t row_bytes,
                     const uint16_t *__restrict__ x16, const int *__restrict__ ex,
@@ -357,6 +357,7 @@ void gemm_kernel(const uint8_t *__restrict__ w, int64_t row_bytes,
   constexpr int SB = ScaleTraits<KIND>::bytes;
   constexpr int NPT = 64 * NPW;                  // producer threads
   constexpr int NT = 256 + NPT;                  // threads
+  constexpr int KS = KSZ, LDS_ROW = KSZ + 8;     // k per iteration, halves per LDS row
   constexpr int AC = BM * (KS / 8) / NPT;        // 8-half activation chunks per producer
   constexpr int BC = BN * (KS / 16) / NPT;       // 16-code weight chunks per producer
   static_assert(AC >= 1 && BC >= 1, "tile too small for the producer waves");
@@ -390,15 +391,15 @@ void gemm_kernel(const uint8_t *__restrict__ w, int64_t row_bytes,
 #pragma unroll
     for (int u = 0; u < AC; ++u) {
       const int c = pt + NPT * u;
-      arow[u] = c >> 3;
-      akq[u] = c & 7;
+      arow[u] = c / (KS / 8);
+      akq[u] = c % (KS / 8);
       aoff[u] = (uint32_t)((arow[u] * m + kbase + 8 * akq[u]) * 2);
     }
 #pragma unroll
     for (int u = 0; u < BC; ++u) {
       const int c = pt + NPT * u;
-      brow[u] = c >> 2;
-      bkc[u] = c & 3;
+      brow[u] = c / (KS / 16);
+      bkc[u] = c % (KS / 16);
       boff[u] = (uint32_t)(brow[u] * row_bytes + (m / G) * SB + kbase + 16 * bkc[u]);
       soff[u] = (uint32_t)(brow[u] * row_bytes + ((kbase + 16 * bkc[u]) / G) * SB);
     }
@@ -561,23 +562,24 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float *__restr
   }
 }
 
-template <int G, int KIND, int TM, int TN, int CR = 1, int NPW = kProducerWaves>
+template <int G, int KIND, int TM, int TN, int CR = 1, int NPW = kProducerWaves,
+          int KS = kIterCodes>
 hipError_t launch_t(const LinearArgs &a, const uint16_t *x16, const int *ex, const int *ew,
                        hipStream_t st) {
   constexpr int BM = 32 * TM * CR, BN = 32 * TN * (4 / CR);
   const int64_t nit_all = (a.m + KS - 1) / KS;
   const int64_t gx = (a.n + BN - 1) / BN, gy = (a.s + BM - 1) / BM;
   // Split K when the output tiles alone leave CUs idle (256 CUs, one
-  // workgroup each); every split keeps at least 8 iterations.
+  // workgroup each); every split keeps at least 512 codes.
   int64_t splits = 1;
   if (a.ws) {
-    while (gx * gy * splits * 2 <= 256 && (nit_all + 2 * splits - 1) / (2 * splits) >= 8 &&
+    while (gx * gy * splits * 2 <= 256 && (nit_all + 2 * splits - 1) / (2 * splits) >= 512 / KS &&
            2 * splits * a.s * a.n <= a.ws_floats)
       splits *= 2;
   }
   int64_t nit = (nit_all + splits - 1) / splits;
   dim3 grid((unsigned)gx, (unsigned)gy, (unsigned)splits), block(64 * (4 + NPW));
-  hipLaunchKernelGGL((gemm_kernel<G, KIND, TM, TN, CR, NPW>), grid, block, 0, st, a.w, a.row_bytes,
+  hipLaunchKernelGGL((gemm_kernel<G, KIND, TM, TN, CR, NPW, kStages, KS>), grid, block, 0, st, a.w, a.row_bytes,
                      x16, ex, ew, a.y, a.s, a.m, a.n, (int)nit, a.ws);
   if (splits > 1) return launch_splitk_reduce(a.ws, a.y, a.s * a.n, (int)splits, st);
   return hipGetLastError();
@@ -611,13 +613,17 @@ hipError_t launch_g(const LinearArgs &a, uint16_t *x16, int *ex, int *ew, bool w
     // consumer waves over one 32 x 32 tile each, 4 producer waves) when they
     // give at most one workgroup per CU, else 64 x 128 ones if those do
     // (1B prompt of 512 rows: o 512x2048x2048 25.0 -> 21.0 us, q|k|v
-    // 512x3072x2048 28.6 -> 24.8 us with their pre-pass and reduce).
+    // 512x3072x2048 28.6 -> 24.8 us with their pre-pass and reduce).  Both
+    // take 128 codes of K per iteration, half the stage hand-overs of 64
+    // (o 21.9 -> 20.0-20.4 us, q|k|v 25.2 -> 24.1-24.3 us; 128 x 128 tiles
+    // lose with them: down 44.0 -> 44.7-45.2 us).
     // Longer rows keep 128 x 128 tiles: 64-row tiles read each weight tile
     // for twice as many row blocks (down 512x2048x8192 42.7 -> 50.3 us).
     if (a.m <= 4096) {
       const int64_t rb64 = (a.s + 63) / 64;
-      if ((a.n + 63) / 64 * rb64 <= 256) return launch_t<G, KIND, 1, 1, 2, 4>(a, x16, ex, ew, st);
-      if ((a.n + 127) / 128 * rb64 <= 256) return launch_t<G, KIND, 2, 1>(a, x16, ex, ew, st);
+      if ((a.n + 63) / 64 * rb64 <= 256) return launch_t<G, KIND, 1, 1, 2, 4, 128>(a, x16, ex, ew, st);
+      if ((a.n + 127) / 128 * rb64 <= 256)
+        return launch_t<G, KIND, 2, 1, 1, kProducerWaves, 128>(a, x16, ex, ew, st);
     }
     return launch_t<G, KIND, 4, 1>(a, x16, ex, ew, st);
   }
