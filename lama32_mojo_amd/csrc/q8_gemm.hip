@@ -312,8 +312,7 @@ __device__ __forceinline__ f16x8 dequant8(uint32_t d0, uint32_t d1, f16x2 s2) {
 }
 
 // One workgroup per BM x BN output tile (BM = 32 TM CR, BN = 32 TN (4 /
-// CR)), its 4 + NPW waves split by role (12, three per SIMD; 8 with 64 x 64
-// tiles):
+// CR)), its 4 + NPW waves split by role (12, three per SIMD):
 //   * waves 0-3 (consumers) only read MFMA fragments from LDS and issue the
 //     MFMAs, each over 32 TM rows and 32 TN columns of the tile (TM x TN
 //     accumulator tiles of 32 x 32): with CR = 1 all four share the BM rows
@@ -610,18 +609,19 @@ hipError_t launch_g(const LinearArgs &a, uint16_t *x16, int *ex, int *ew, bool w
     if (tiles256 >= 256) return launch_t<G, KIND, 4, 2>(a, x16, ex, ew, st);
     // Rows of at most 4096 codes: 64-row tiles rather than a K split, which
     // costs a reduce launch (about 5 us here).  64 x 64 tiles (2 x 2
-    // consumer waves over one 32 x 32 tile each, 4 producer waves) when they
-    // give at most one workgroup per CU, else 64 x 128 ones if those do
+    // consumer waves over one 32 x 32 tile each) when they give at most one
+    // workgroup per CU, else 64 x 128 ones if those do
     // (1B prompt of 512 rows: o 512x2048x2048 25.0 -> 21.0 us, q|k|v
     // 512x3072x2048 28.6 -> 24.8 us with their pre-pass and reduce).  Both
     // take 128 codes of K per iteration, half the stage hand-overs of 64
     // (o 21.9 -> 20.0-20.4 us, q|k|v 25.2 -> 24.1-24.3 us; 128 x 128 tiles
-    // lose with them: down 44.0 -> 44.7-45.2 us).
+    // lose with them: down 44.0 -> 44.7-45.2 us), and 8 producer waves (o
+    // with 4: 19.9 -> 18.0-18.2 us with 8; q|k|v 24.0 -> 27.2 us with 4).
     // Longer rows keep 128 x 128 tiles: 64-row tiles read each weight tile
     // for twice as many row blocks (down 512x2048x8192 42.7 -> 50.3 us).
     if (a.m <= 4096) {
       const int64_t rb64 = (a.s + 63) / 64;
-      if ((a.n + 63) / 64 * rb64 <= 256) return launch_t<G, KIND, 1, 1, 2, 4, 128>(a, x16, ex, ew, st);
+      if ((a.n + 63) / 64 * rb64 <= 256) return launch_t<G, KIND, 1, 1, 2, 8, 128>(a, x16, ex, ew, st);
       if ((a.n + 127) / 128 * rb64 <= 256)
         return launch_t<G, KIND, 2, 1, 1, kProducerWaves, 128>(a, x16, ex, ew, st);
     }
