@@ -3,7 +3,8 @@
 //
 // y[i, j] = sum_k x[i, k] * (q[j, k] * scale[j, k / G])
 // (k_mm_q8's product, src/llama_q8.mojo:73-84) as a dequant-GEMM on
-// v_mfma_f32_32x32x16_f16, in two launches:
+// v_mfma_f32_32x32x16_f16, in two launches (a third, splitk_reduce_kernel,
+// adds the partial sums when a grid with few output tiles splits K):
 //   1. act16_kernel (or norm16_kernel, which first forms the row's RMSNorm
 //      exactly as rmsnorm_kernel does): each activation row is scaled by a
 //      power of two 2^-e_i
