@@ -109,7 +109,9 @@ __global__ __launch_bounds__(1024) void argmax_finish_kernel(
   }
   if (!emb) return;
   __syncthreads();
-  const int64_t id = sid;
+  // (ids are logit rows, below vocab by construction; the clamp keeps the
+  // gather inside the table whatever the partials hold)
+  const int64_t id = sid < vocab ? sid : 0;
   const uint8_t *row = emb + id * row_bytes;
   const int8_t *codes = reinterpret_cast<const int8_t *>(row + (d / G) * SB);
   for (int64_t c = 4 * (int64_t)threadIdx.x; c < d; c += 4 * 1024) {

@@ -376,11 +376,6 @@ std::string json_escape(const std::string &s) {
   return o + "\"";
 }
 
-std::string dir_of(const std::string &path) {
-  const size_t k = path.rfind('/');
-  return k == std::string::npos ? std::string(".") : path.substr(0, k);
-}
-
 bool is_dir(const std::string &path) {
   struct stat sb;
   return stat(path.c_str(), &sb) == 0 && S_ISDIR(sb.st_mode);
