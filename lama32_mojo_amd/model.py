@@ -24,7 +24,6 @@ Differences from the reference host, on purpose:
 
 from __future__ import annotations
 
-import math
 from dataclasses import dataclass
 from typing import Mapping, Sequence
 

@@ -3,7 +3,6 @@ invariants -- no GPU.  Each check is chosen so a plausible slip (a sign in
 RoPE, a wrong GQA head map, a dropped causal mask, a missing eps) fails it."""
 
 import numpy as np
-import pytest
 
 from oracle import model_oracle as mo
 from oracle.q8_oracle import bf16_bits_to_f32, f32_to_bf16_bits, pack_q8_np, synth_weights_bf16
