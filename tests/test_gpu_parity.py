@@ -309,7 +309,7 @@ def test_linear_lm_head_full_size(ctx, cor):
 
 @pytest.mark.parametrize("G,scale,s,n,m", layout_shapes(
     [(512, 2048, 2048), (512, 512, 2048), (512, 8192, 2048), (512, 2048, 8192), (77, 200, 1024),
-     (130, 96, 96), (1, 64, 64), (512, 3072, 2048), (200, 1000, 4096)], 2))
+     (130, 96, 96), (1, 64, 64), (512, 3072, 2048), (200, 1000, 4096), (100, 200, 1056)], 2))
 def test_gemm_bf16act_matches_closed_form(ctx, cor, G, scale, s, n, m):
     say("gemm bf16", G, scale, s, n, m)
     pk = cor.pack_bf16(synth_weights_bf16(n, m, seed=n + 3 * m), G, scale)
