@@ -129,8 +129,11 @@ PROMPT_MODELS = {"llama-3.2-1b": (gm.LLAMA_32_1B, 80), "qwen3-0.6b": (gm.QWEN3_0
 # rounded to binary16, 2^-11 each), and the rounding errors build up layer
 # by layer: measured against float64, 1.6e-4 per layer on both Llama models
 # (Llama-3.2-1B 2.6e-3 over 16 layers, Llama-3.1-8B 5.1e-3 over 32 at 40
-# rows and 6.0e-3 at 80), Qwen3-0.6B 1.2e-3 over 28.  The bar is 3e-4 per
-# layer; a wrong offset, stride or weight gives errors of order one.
+# rows and 6.0e-3 at 80), Qwen3-0.6B 1.2e-3 over 28.  (The f32 paths of the
+# short prompt above sit at 2e-4 - 7e-4 already: random-sign dot products
+# of 2048 - 14336 terms lose about m times the f32 epsilon, relative to
+# their sum, and the layers compound it.)  The bar is 3e-4 per layer; a
+# wrong offset, stride or weight gives errors of order one.
 TOL_PROMPT_PER_LAYER = 3e-4
 
 
