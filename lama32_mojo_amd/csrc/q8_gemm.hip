@@ -373,9 +373,11 @@ void gemm_kernel(const uint8_t *__restrict__ w, int64_t row_bytes,
   const int64_t arows = s - m0 < BM ? s - m0 : BM;
   const int64_t nrows = n - n0 < BN ? n - n0 : BN;
 
+  // The row exponents are staged by the consumer threads (BM, BN <= 256)
+  // and published by the first barrier, which the producers pass only after
+  // issuing their first tile loads: the two memory round trips overlap.
   for (int t = tid; t < BM; t += NT) exs[t] = t < arows ? ex[m0 + t] : 0;
   for (int t = tid; t < BN; t += NT) ews[t] = KIND == SCALE_F32 && t < nrows ? ew[n0 + t] : 0;
-  __syncthreads();
 
   if (wid >= 4) {
     // ---- producers ----
@@ -451,6 +453,7 @@ void gemm_kernel(const uint8_t *__restrict__ w, int64_t row_bytes,
     Stage S[PD];
 #pragma unroll
     for (int u = 0; u < PD; ++u) load(S[u], u);
+    __syncthreads();             // the exponents are staged
     store(S[0], 0, 0);
     load(S[0], PD);
     __syncthreads();
@@ -481,7 +484,8 @@ void gemm_kernel(const uint8_t *__restrict__ w, int64_t row_bytes,
     for (int t = 0; t < TN; ++t)
 #pragma unroll
       for (int v = 0; v < 16; ++v) acc[i][t][v] = 0.0f;
-  __syncthreads();
+  __syncthreads();               // the exponents are staged
+  __syncthreads();               // the first stage is stored
   for (int it = 0; it < nit; ++it) {
     const _Float16 *at = As[it & 1];
     const _Float16 *bt = Bs[it & 1];
