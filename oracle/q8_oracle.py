@@ -79,7 +79,8 @@ def pack_q8_np(w: np.ndarray, G: int = 64, scale: str = "f16") -> np.ndarray:
     n, m = w.shape
     assert m % G == 0 and m % 2 == 0, (n, m, G)
     x = w.reshape(n, m // G, G)
-    with np.errstate(invalid="ignore", divide="ignore"):
+    # scales past binary16's range round to inf, as the reference's cast does
+    with np.errstate(invalid="ignore", divide="ignore", over="ignore"):
         s = np.abs(x).max(axis=2) / 127.0
         s = np.maximum(s, 1e-8)
         if scale == "f16":
