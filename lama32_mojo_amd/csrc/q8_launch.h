@@ -157,14 +157,19 @@ struct DecodeAttnArgs {
 // 0 .. pos0: one launch of nsplit x nkv blocks over
 // context splits, then (nsplit > 1) a merge launch.  Calls that share
 // `part` must not overlap.
-// Keys per chunk (one wave's unit of work), head slots of a block of 4 waves
-// and the split count.  Head slots: heads per wave GRP / slots, waves per
-// head 4 / slots.  With 64-dim heads (short rows, contexts of a chunk or so
-// per block) one head per wave; with 128-dim heads in groups of 4 or 8 a
-// wave serves 4 heads, so the K/V rows of a chunk are loaded once and the
-// block's waves work on different chunks (measured on the Llama-3.1-8B step
-// at 2300 cached tokens; slower on the 1B step).  Splits: one chunk per wave
-// (blocks of 4 / slots chunks) up to 32 blocks per KV head, then more chunks
+// Keys per chunk (one wave's unit of work), waves per block, head slots of
+// a block and the split count.  Head slots: heads per wave GRP / slots,
+// waves per head waves / slots (the chunks a block spans).  With 64-dim
+// heads (short rows, contexts of a chunk or so per block) 4 waves, one head
+// per wave; with 128-dim heads in groups of 8, 4 waves serving 4 heads each,
+// so the K/V rows of a chunk are loaded once and the block's waves work on
+// different chunks (measured on the Llama-3.1-8B step at 2300 cached
+// tokens; slower on the 1B step); in groups of 4, 8 waves, two per chunk
+// with 2 heads each, which halves each wave's chain of dot products and
+// softmax work for the same blocks (Llama-3.1-8B at 2300 tokens: 9.98 ->
+// 9.75 us per call, the same bits; 8 waves over 2 chunks at 64-dim heads
+// lose: 7.17 -> 7.73 us).  Splits: one chunk per wave and head slot (blocks
+// of waves / slots chunks) up to 32 blocks per KV head, then more chunks
 // per block.  Every launched block reads the position before it can leave
 // and a launch of 256 blocks takes about 1.4 us to start them all, so the
 // grid holds no more blocks than the longest context keeps busy.  A cache
@@ -174,12 +179,13 @@ struct DecodeAttnArgs {
 constexpr int kDecodeAttnOneBlockChunks = 4;
 constexpr int kDecodeAttnMaxSplit = 32;   // bound of the merge's per-thread loads
 constexpr int decode_attn_chunk(int head_dim) { return head_dim > 64 ? 32 : 64; }
+constexpr int decode_attn_waves(int hd, int grp) { return (hd >= 128 && grp == 4) ? 8 : 4; }
 constexpr int decode_head_slots(int hd, int grp) {
-  return (hd >= 128 && grp >= 4) ? grp / 4 : (grp < 4 ? grp : 4);
+  return (hd >= 128 && grp == 4) ? 2 : (hd >= 128 && grp > 4) ? grp / 4 : (grp < 4 ? grp : 4);
 }
 inline int decode_attn_nsplit(int64_t maxlen, int head_dim, int grp) {
   const int64_t kc = decode_attn_chunk(head_dim);
-  const int64_t wph = 4 / decode_head_slots(head_dim, grp);
+  const int64_t wph = decode_attn_waves(head_dim, grp) / decode_head_slots(head_dim, grp);
   const int64_t n = ((maxlen + kc - 1) / kc + wph - 1) / wph;
   return (int)(n <= kDecodeAttnOneBlockChunks ? 1 : n > 32 ? 32 : n);
 }

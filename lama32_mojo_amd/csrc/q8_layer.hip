@@ -501,12 +501,14 @@ __device__ __forceinline__ float lane_group_sum(float v) {
   return v;
 }
 
-// Grid (nsplit, nkv), 4 waves.  Block (split, g) serves KV head g and its GRP
-// query heads over the key chunks [split * cpb, (split + 1) * cpb) of 64
-// keys, cpb = max(waves per head, ceil(chunks / nsplit)).  A wave serves one
-// query head (two when GRP = 8; with GRP < 4 the waves of one head take
-// alternate chunks), so each wave's work per chunk is short and the block's
-// waves share the chunk's K and V rows through the cache.  Rows are read as
+// Grid (nsplit, nkv), NW = decode_attn_waves(HD, GRP) waves.  Block
+// (split, g) serves KV head g and its GRP query heads over the key chunks
+// [split * cpb, (split + 1) * cpb) of KC keys (64, or 32 at head_dim 128),
+// cpb = max(waves per head, ceil(chunks / nsplit)).  The waves form
+// decode_head_slots(HD, GRP) head slots: wave w serves the GRP / slots query
+// heads of slot w % slots over chunk w / slots of the block's chunks (then
+// every NW / slots-th after it), so the block's waves share each chunk's K
+// and V rows through the cache.  Rows are read as
 // 16-byte pieces, HD/8 lanes per row (full 128- or 256-byte runs): a lane
 // multiplies its 8 dims of a key by the query and the row's lanes sum with
 // DPP; for P V a lane accumulates its 8 dims over its rows.  Online softmax
@@ -522,12 +524,12 @@ __device__ __forceinline__ float lane_group_sum(float v) {
 // first chunk's loads are issued before the position is read, so the
 // prologue waits for one round trip, not one per dependent load.
 template <int HD, int GRP>
-__global__ __launch_bounds__(256) void attn_decode_kernel(
+__global__ __launch_bounds__(64 * decode_attn_waves(HD, GRP)) void attn_decode_kernel(
     const float *__restrict__ q, const float *__restrict__ k, const float *__restrict__ v,
     const float *__restrict__ inv, __half *__restrict__ kc, __half *__restrict__ vc,
     float *__restrict__ part, float *__restrict__ out, int nkv, const int *posp, int pos0_host,
     int maxlen, const uint16_t *__restrict__ qnw, const uint16_t *__restrict__ knw, float eps) {
-  constexpr int KC = decode_attn_chunk(HD), NW = 4;
+  constexpr int KC = decode_attn_chunk(HD), NW = decode_attn_waves(HD, GRP), NT = 64 * NW;
   constexpr int LPR = HD / 8;           // lanes per row (8 dims each)
   constexpr int RPI = 64 / LPR;         // rows per load instruction (row slots)
   constexpr int NI = KC / RPI;          // load instructions per chunk
@@ -567,10 +569,10 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(
   };
   // Prologue inputs, all issued ahead of the first chunk so that one wait
   // covers them: thread t's query pairs (d, half + d) of RoPE items
-  // t + 256 r, the new k pair (t < half) and v element (t < HD), the inverse
+  // t + NT r, the new k pair (t < half) and v element (t < HD), the inverse
   // frequencies, the norm weights (zeros when absent) and the two halves of
   // the rows whose squares this wave sums for the per-head norms.
-  constexpr int NQ = (GRP * half + 255) / 256;   // RoPE items per thread
+  constexpr int NQ = (GRP * half + NT - 1) / NT;   // RoPE items per thread
   constexpr int NR = (GRP + 1 + NW - 1) / NW;    // norm rows per wave
   const int t = threadIdx.x;
   const rsrc_t qrs = make_rsrc(q + (int64_t)g * GRP * HD, GRP * HD * 4);
@@ -582,7 +584,7 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(
   uint32_t wqa[NQ], wqb[NQ];
 #pragma unroll
   for (int r = 0; r < NQ; ++r) {
-    const int idx = t + 256 * r, hh = idx / half, d = idx % half;
+    const int idx = t + NT * r, hh = idx / half, d = idx % half;
     const bool ok = idx < GRP * half;
     qa[r] = bload4f(qrs, ok ? (uint32_t)(hh * HD + d) * 4u : kOutOfRange);
     qb[r] = bload4f(qrs, ok ? (uint32_t)(hh * HD + half + d) * 4u : kOutOfRange);
@@ -656,7 +658,7 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(
   }
 #pragma unroll
   for (int r = 0; r < NQ; ++r) {
-    const int idx = t + 256 * r, hh = idx / half, d = idx % half;
+    const int idx = t + NT * r, hh = idx / half, d = idx % half;
     if (idx < GRP * half) {
       float cs, sn;
       rope_cs((float)pos0 * fq[r], cs, sn);
@@ -806,7 +808,7 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(
   // and l = sum_w l_w f_w in wave order (a wave without keys adds l_w = 0
   // times f_w = 0, and its o_w is 0)
   float *rec = part + ((int64_t)g * nsplit + split) * (GRP * PR);
-  for (int t = threadIdx.x; t < GRP * HD; t += 256) {
+  for (int t = threadIdx.x; t < GRP * HD; t += NT) {
     const int hh = t / HD, d = t % HD;
     const int s0 = hh % HS, j = hh / HS;
     float o = 0.0f, l = 0.0f;
@@ -844,7 +846,7 @@ __global__ __launch_bounds__(HD) void attn_merge_kernel(const float *__restrict_
                                                         float *__restrict__ out, int nsplit,
                                                         const int *posp, int pos0_host,
                                                         int maxlen) {
-  constexpr int KC = decode_attn_chunk(HD), NW = 4;
+  constexpr int KC = decode_attn_chunk(HD), NW = decode_attn_waves(HD, GRP);
   constexpr int PR = HD + 2;
   constexpr int WPH = NW / decode_head_slots(HD, GRP);   // as attn_decode_kernel
   constexpr int NX = kDecodeAttnMaxSplit;
@@ -1029,7 +1031,7 @@ hipError_t launch_attention(const AttnArgs &a, hipStream_t st) {
 template <int HD, int GRP>
 hipError_t launch_decode_attn_t(const DecodeAttnArgs &a, hipStream_t st) {
   hipLaunchKernelGGL((attn_decode_kernel<HD, GRP>), dim3((unsigned)a.nsplit, (unsigned)a.nkv),
-                     dim3(256), 0, st, a.q, a.k, a.v, a.inv, a.kc, a.vc, a.part, a.out, a.nkv,
+                     dim3(64 * decode_attn_waves(HD, GRP)), 0, st, a.q, a.k, a.v, a.inv, a.kc, a.vc, a.part, a.out, a.nkv,
                      a.posp, a.pos0, a.maxlen, a.qnorm, a.knorm, a.eps);
   if (a.nsplit > 1)      // one split: its blocks wrote the output
     hipLaunchKernelGGL((attn_merge_kernel<HD, GRP>), dim3((unsigned)a.nheads), dim3(HD), 0, st,
