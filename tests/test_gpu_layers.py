@@ -247,8 +247,9 @@ def test_decode_attention_equals_rope_then_attention(ctx, head_dim, nh, nkv, pos
     matches q8_rope_kv + q8_attention within 2e-6 (it sums the splits in
     another order).  maxlen 1536 gives 24 splits of one 64-key chunk
     (head_dim 64, one head per wave) or, at head_dim 128, 12 splits of four
-    32-key chunks (groups of 4) or 24 of two (groups of 8), each wave one
-    chunk for 4 heads: small pos0 is served by one block per KV head,
+    32-key chunks (groups of 4: 8 waves, two per chunk with 2 heads each)
+    or 24 of two (groups of 8: each wave one chunk for 4 heads): small pos0
+    is served by one block per KV head,
     larger pos0 by several blocks whose records the merge launch combines;
     a second call must reproduce the first."""
     decode_attention_case(ctx, head_dim, nh, nkv, pos0, 1536)
@@ -724,7 +725,7 @@ def test_graph_replay_equals_eager(ctx):
 
 
 
-@pytest.mark.parametrize("head_dim,nh,nkv", [(128, 16, 8), (64, 8, 2)])
+@pytest.mark.parametrize("head_dim,nh,nkv", [(128, 16, 8), (64, 8, 2), (128, 32, 8)])
 @pytest.mark.parametrize("pos0", [0, 100, 700])
 def test_decode_attention_qk_norm_equals_rmsnorm_rope_attention(ctx, head_dim, nh, nkv, pos0):
     """With q/k norm weights the one-token step writes the cache bits of
