@@ -501,8 +501,8 @@ __device__ __forceinline__ float lane_group_sum(float v) {
   return v;
 }
 
-// Grid (nsplit, nkv), NW = decode_attn_waves(HD, GRP) waves.  Block
-// (split, g) serves KV head g and its GRP query heads over the key chunks
+// Grid (nkv, nsplit), NW = decode_attn_waves(HD, GRP) waves.  Block
+// (g, split) serves KV head g and its GRP query heads over the key chunks
 // [split * cpb, (split + 1) * cpb) of KC keys (64, or 32 at head_dim 128),
 // cpb = max(waves per head, ceil(chunks / nsplit)).  The waves form
 // decode_head_slots(HD, GRP) head slots: wave w serves the GRP / slots query
@@ -544,7 +544,10 @@ __global__ __launch_bounds__(64 * decode_attn_waves(HD, GRP)) void attn_decode_k
   __shared__ float wm[NW][HPW], wl[NW][HPW];
   __shared__ __align__(16) float wo[NW][HPW][RPI][HD];
   __shared__ float hinv[GRP + 1];
-  const int split = blockIdx.x, g = blockIdx.y, nsplit = gridDim.x;
+  // grid (nkv, nsplit): workgroups go to the 8 XCDs in turn, so with nkv a
+  // multiple of 8 every split of KV head g runs on one XCD, where
+  // attn_merge_kernel's blocks for g's query heads read the records
+  const int split = blockIdx.y, g = blockIdx.x, nsplit = gridDim.y;
   const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int hs = w % HS, kg = w / HS;
   const int kvdim = nkv * HD;
@@ -833,8 +836,8 @@ __global__ __launch_bounds__(64 * decode_attn_waves(HD, GRP)) void attn_decode_k
   }
 }
 
-// Merge of the partial records of attn_decode_kernel: block h (HD threads)
-// serves head h, thread d its output dim d.  Every load is issued before
+// Merge of the partial records of attn_decode_kernel: one block (HD threads)
+// per head h, thread d its output dim d.  Every load is issued before
 // the position is read: lane x takes split x's m and l, thread d split x's
 // o[d] for every split (offsets past the records read as zeros).  Each wave
 // then forms the active splits' factors exp(m_x - M) and l = sum_x l_x f_x
@@ -851,7 +854,11 @@ __global__ __launch_bounds__(HD) void attn_merge_kernel(const float *__restrict_
   constexpr int WPH = NW / decode_head_slots(HD, GRP);   // as attn_decode_kernel
   constexpr int NX = kDecodeAttnMaxSplit;
   static_assert(NX <= 64, "one lane per split");
-  const int h = blockIdx.x, g = h / GRP, hh = h % GRP;
+  // block b serves head h = (b % nkv) GRP + b / nkv: with nkv a multiple of
+  // 8 it runs on the XCD of the split blocks that wrote KV head h / GRP's
+  // records, so they are read from that XCD's L2
+  const int nkvb = (int)gridDim.x / GRP;
+  const int h = ((int)blockIdx.x % nkvb) * GRP + (int)blockIdx.x / nkvb, g = h / GRP, hh = h % GRP;
   const int d = threadIdx.x, lane = threadIdx.x & 63;
   const rsrc_t prs = make_rsrc(part + (int64_t)g * nsplit * (GRP * PR),
                                (uint32_t)(nsplit * GRP * PR) * 4u);
@@ -1030,7 +1037,7 @@ hipError_t launch_attention(const AttnArgs &a, hipStream_t st) {
 
 template <int HD, int GRP>
 hipError_t launch_decode_attn_t(const DecodeAttnArgs &a, hipStream_t st) {
-  hipLaunchKernelGGL((attn_decode_kernel<HD, GRP>), dim3((unsigned)a.nsplit, (unsigned)a.nkv),
+  hipLaunchKernelGGL((attn_decode_kernel<HD, GRP>), dim3((unsigned)a.nkv, (unsigned)a.nsplit),
                      dim3(64 * decode_attn_waves(HD, GRP)), 0, st, a.q, a.k, a.v, a.inv, a.kc, a.vc, a.part, a.out, a.nkv,
                      a.posp, a.pos0, a.maxlen, a.qnorm, a.knorm, a.eps);
   if (a.nsplit > 1)      // one split: its blocks wrote the output
