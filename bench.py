@@ -69,6 +69,8 @@ Other workloads (--workload) run one of these alone:
            3 copies of 1 GiB by torch's copy kernel (the calibration of
            known size), then 8 lm_head GEMVs 128256x2048 alternating over
            two tables / 32 fused gate|up GEMVs over the 16 layers
+  gemm-pmc  the launches the prefill-GEMM counter passes read: 4 eager Q8
+           GEMMs 2048x14336x4096 (bf16 x, G=32 f32) over two weight copies
 """
 
 from __future__ import annotations
@@ -101,7 +103,8 @@ def parse():
     p.add_argument("--warmup", type=int, default=5)
     p.add_argument("--workload", default="all",
                    choices=["all", "decode", "decode-linears", "linear", "prefill", "qwen8b",
-                            "e2e-8b", "lmhead-pmc", "gateup-pmc", "qwen3-06b", "calib"])
+                            "e2e-8b", "lmhead-pmc", "gateup-pmc", "gemm-pmc", "qwen3-06b",
+                            "calib"])
     p.add_argument("--layout", default=None, choices=["g64f16", "g32f32"],
                    help="packed layout (default: g64f16; g32f32 for --workload linear)")
     p.add_argument("--batch", type=int, default=1)
@@ -561,6 +564,27 @@ def run_gateup_pmc(B: Bench):
             "data": "synthetic", "config": {"workload": "3 x 1 GiB copy, 32 x fused gate|up "
                                                         f"GEMV {2 * cfg.inter}x{cfg.hidden}",
                                             "copy_bytes": nbytes, "gateup_bytes": nb}}
+
+
+def run_gemm_pmc(B: Bench, M: int = 2048, N: int = 14336, K: int = 4096, calls: int = 4):
+    """The launches the prefill-GEMM counter passes read: `calls` eager Q8
+    GEMMs MxNxK (bf16 x, the layout of --layout; by default G=32 f32) over
+    two packed weight copies, each after its binary16 pre-pass."""
+    q8hip, ctx, torch = B.q8hip, B.ctx, B.torch
+    w, offs = B.pack_arena([(N, K), (N, K)], [11, 12])
+    x = B.activations(M * K, 5, bf16=True)
+    y = torch.empty(M * N, device="cuda", dtype=torch.float32)
+    xb = q8hip.Buffer.wrap(ctx, x.data_ptr(), x.numel() * 2)
+    yb = q8hip.Buffer.wrap(ctx, y.data_ptr(), y.numel() * 4)
+    for i in range(calls):
+        q8hip.linear_bf16act(ctx, w, offs[i % 2], xb, 0, yb, 0, M, K, N, B.G, B.scale)
+    ctx.sync()
+    w.free()
+    return {"metric": "counter-pass launches (no timing)", "value": 0, "unit": "none",
+            "ms_per_step": 0.0, "higher_is_better": True, "dtype": "f16(q*s) x f16(x) -> f32",
+            "data": "synthetic", "config": {"workload": f"{calls} x Q8 GEMM {M}x{N}x{K} "
+                                                        "with its binary16 pre-pass, eager",
+                                            "flop_per_call": 2 * M * N * K}}
 
 
 def run_e2e_8b(B: Bench, prompt: int = 2048, gen: int = 256, rooflines: bool = True):
@@ -1062,6 +1086,8 @@ def main():
         res = run_decode_model(B, ctxlen=128, cfg=gm.QWEN3_06B, tok_metric=True)
     elif args.workload == "lmhead-pmc":
         res = run_lmhead_pmc(B)
+    elif args.workload == "gemm-pmc":
+        res = run_gemm_pmc(B)
     elif args.workload == "e2e-8b":
         res = run_e2e_8b(B)
     elif args.workload == "qwen8b":
