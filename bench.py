@@ -69,8 +69,10 @@ Other workloads (--workload) run one of these alone:
            3 copies of 1 GiB by torch's copy kernel (the calibration of
            known size), then 8 lm_head GEMVs 128256x2048 alternating over
            two tables / 32 fused gate|up GEMVs over the 16 layers
-  gemm-pmc  the launches the prefill-GEMM counter passes read: 4 eager Q8
-           GEMMs 2048x14336x4096 (bf16 x, G=32 f32) over two weight copies
+  gemm-pmc  the launches the Q8 linear counter passes read: 4 eager Q8
+           linears of --shape (default the GEMM 2048x14336x4096, bf16 x;
+           below 32 rows f32 x, the small-batch kernels), G=32 f32, over
+           two weight copies
 """
 
 from __future__ import annotations
@@ -108,6 +110,8 @@ def parse():
     p.add_argument("--layout", default=None, choices=["g64f16", "g32f32"],
                    help="packed layout (default: g64f16; g32f32 for --workload linear)")
     p.add_argument("--batch", type=int, default=1)
+    p.add_argument("--shape", default="2048x14336x4096",
+                   help="MxNxK of the gemm-pmc launches (rows x outputs x inputs)")
     p.add_argument("--no-graph", action="store_true", help="launch eagerly, no HIP graph")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     p.add_argument("--cpu-seconds", type=float, default=8.0,
@@ -566,24 +570,37 @@ def run_gateup_pmc(B: Bench):
                                             "copy_bytes": nbytes, "gateup_bytes": nb}}
 
 
-def run_gemm_pmc(B: Bench, M: int = 2048, N: int = 14336, K: int = 4096, calls: int = 4):
-    """The launches the prefill-GEMM counter passes read: `calls` eager Q8
-    GEMMs MxNxK (bf16 x, the layout of --layout; by default G=32 f32) over
-    two packed weight copies, each after its binary16 pre-pass."""
+def run_gemm_pmc(B: Bench, calls: int = 4):
+    """The launches the Q8 linear counter passes read: `calls` eager Q8
+    linears of --shape MxNxK (the layout of --layout; by default G=32 f32)
+    over two packed weight copies: from 32 rows bf16 x (the dequant-GEMM,
+    each call after its binary16 pre-pass), below that f32 x (the
+    small-batch kernels)."""
     q8hip, ctx, torch = B.q8hip, B.ctx, B.torch
+    M, N, K = (int(v) for v in B.args.shape.split("x"))
     w, offs = B.pack_arena([(N, K), (N, K)], [11, 12])
-    x = B.activations(M * K, 5, bf16=True)
-    y = torch.empty(M * N, device="cuda", dtype=torch.float32)
-    xb = q8hip.Buffer.wrap(ctx, x.data_ptr(), x.numel() * 2)
-    yb = q8hip.Buffer.wrap(ctx, y.data_ptr(), y.numel() * 4)
-    for i in range(calls):
-        q8hip.linear_bf16act(ctx, w, offs[i % 2], xb, 0, yb, 0, M, K, N, B.G, B.scale)
+    gemm = M >= 32
+    if gemm:
+        x = B.activations(M * K, 5, bf16=True)
+        y = torch.empty(M * N, device="cuda", dtype=torch.float32)
+        xb = q8hip.Buffer.wrap(ctx, x.data_ptr(), x.numel() * 2)
+        yb = q8hip.Buffer.wrap(ctx, y.data_ptr(), y.numel() * 4)
+        for i in range(calls):
+            q8hip.linear_bf16act(ctx, w, offs[i % 2], xb, 0, yb, 0, M, K, N, B.G, B.scale)
+    else:
+        a = torch.empty(M * K + M * N, device="cuda", dtype=torch.float32)
+        a[: M * K] = B.activations(M * K, 5)
+        ab = q8hip.Buffer.wrap(ctx, a.data_ptr(), a.numel() * 4)
+        for i in range(calls):
+            q8hip.linear(ctx, w, offs[i % 2], ab, 0, M * K, M, K, N, B.G, B.scale)
     ctx.sync()
     w.free()
+    kind = ("Q8 GEMM (bf16 x) with its binary16 pre-pass" if gemm
+            else "Q8 small-batch linear (f32 x)")
     return {"metric": "counter-pass launches (no timing)", "value": 0, "unit": "none",
-            "ms_per_step": 0.0, "higher_is_better": True, "dtype": "f16(q*s) x f16(x) -> f32",
-            "data": "synthetic", "config": {"workload": f"{calls} x Q8 GEMM {M}x{N}x{K} "
-                                                        "with its binary16 pre-pass, eager",
+            "ms_per_step": 0.0, "higher_is_better": True,
+            "dtype": "f16(q*s) x f16(x) -> f32" if gemm else "int8xf32",
+            "data": "synthetic", "config": {"workload": f"{calls} x {kind} {M}x{N}x{K}, eager",
                                             "flop_per_call": 2 * M * N * K}}
 
 
