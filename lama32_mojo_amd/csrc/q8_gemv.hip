@@ -33,11 +33,22 @@ namespace q8 {
 namespace {
 
 constexpr int kWaves = 4;               // wavefronts per workgroup
-constexpr int kLdsFloats = 16384;       // fused prologues stage x in LDS up to 64 KiB
+constexpr int kLdsFloats = 16384;       // fused prologues stage up to 16384 floats of x (80 KiB padded)
 // Plain x is staged only up to 32 KiB: a larger stage caps the workgroups
 // per CU (160 KiB of LDS) below what the grid needs for one round, and the
 // waves read x from L2 just as well.
 constexpr int kLdsStageFloats = 8192;
+// The fused launches (a prologue or an epilogue) stage x in LDS with 4
+// floats of padding after every 16: the 16-float slices that lanes read 64
+// bytes apart then start 80 bytes apart, so 8 (or 16) neighbouring lanes'
+// 16-byte reads fall on distinct banks (LDS bank-conflict cycles of the 1B
+// fused gate|up launch 1.18 M -> 0.39 M; Llama-3.1-8B step 1.958-1.962 ->
+// 1.947-1.952 ms, the same bits).  Plain launches keep x dense: there the
+// larger stage cost more than the conflicts (Qwen3-8B decode linears
+// 1.755 -> 1.777 ms padded, fewer workgroups per CU).
+__host__ __device__ constexpr int64_t xs_index(int64_t i) { return (i >> 4) * 20 + (i & 15); }
+__host__ __device__ constexpr int64_t xs_floats(int64_t n) { return (n + 15) / 16 * 20; }
+constexpr bool x_padded(int pre, int post) { return !(pre == PRE_NONE && post == POST_STORE); }
 
 template <int G, int KIND, int S, int R, int SPLITK, bool XLDS, int PRE = PRE_NONE,
           int POST = POST_STORE, int NPF = 1, int NW = kWaves>
@@ -57,6 +68,7 @@ __global__ __launch_bounds__(64 * NW) void gemv_kernel(
                 "the argmax epilogue keeps whole rows per wave");
   constexpr int SB = ScaleTraits<KIND>::bytes;
   constexpr int NT = 64 * NW;                   // threads
+  constexpr bool XPAD = XLDS && x_padded(PRE, POST);   // stage layout: xs_index
   const int lane = threadIdx.x & 63;
   // wave-uniform by construction, so row pointers and K ranges live in
   // scalar registers
@@ -216,7 +228,7 @@ __global__ __launch_bounds__(64 * NW) void gemv_kernel(
           o.z = bf16_bits_to_f32(wb[u].y & 0xffffu) * v4.z;
           o.w = bf16_bits_to_f32(wb[u].y >> 16) * v4.w;
         }
-        *reinterpret_cast<f32x4 *>(xs + i) = o;
+        *reinterpret_cast<f32x4 *>(xs + (XPAD ? xs_index(i) : i)) = o;
       }
     }
     if constexpr (PRE == PRE_RMSNORM) {
@@ -272,7 +284,8 @@ __global__ __launch_bounds__(64 * NW) void gemv_kernel(
           xc = xr[XREG ? p : 0][2];
           xd = xr[XREG ? p : 0][3];
         } else {
-          const f32x4 *xv4 = reinterpret_cast<const f32x4 *>(xp + b * m + kx);
+          const f32x4 *xv4 = reinterpret_cast<const f32x4 *>(
+              xp + (XPAD ? xs_index(b * m + kx) : b * m + kx));
           xa = xv4[0];
           xb = xv4[1];
           xc = xv4[2];
@@ -581,7 +594,8 @@ hipError_t launch_fused_npf(const FusedLinearArgs &f, int64_t cap, hipStream_t s
     }
   }
   hipLaunchKernelGGL((gemv_kernel<G, KIND, 1, R, SPLITK, true, PRE, POST, NPF, NW>), grid, block,
-                     (size_t)a.m * sizeof(float), st, a.w, a.row_bytes, a.n, x, a.m, a.y, f.wn,
+                     (size_t)(x_padded(PRE, POST) ? xs_floats(a.m) : a.m) * sizeof(float), st,
+                     a.w, a.row_bytes, a.n, x, a.m, a.y, f.wn,
                      f.eps, f.res, f.part);
   return hipGetLastError();
 }
