@@ -73,6 +73,9 @@ Other workloads (--workload) run one of these alone:
            linears of --shape (default the GEMM 2048x14336x4096, bf16 x;
            below 32 rows f32 x, the small-batch kernels), G=32 f32, over
            two weight copies
+  attn-pmc  the launches the attention counter passes read: 4 eager prompt
+           attentions of 2048 rows and 4 eager one-token steps at 2300
+           cached tokens (Llama-3.1-8B heads)
 """
 
 from __future__ import annotations
@@ -105,8 +108,8 @@ def parse():
     p.add_argument("--warmup", type=int, default=5)
     p.add_argument("--workload", default="all",
                    choices=["all", "decode", "decode-linears", "linear", "prefill", "qwen8b",
-                            "e2e-8b", "lmhead-pmc", "gateup-pmc", "gemm-pmc", "qwen3-06b",
-                            "calib"])
+                            "e2e-8b", "lmhead-pmc", "gateup-pmc", "gemm-pmc", "attn-pmc",
+                            "qwen3-06b", "calib"])
     p.add_argument("--layout", default=None, choices=["g64f16", "g32f32"],
                    help="packed layout (default: g64f16; g32f32 for --workload linear)")
     p.add_argument("--batch", type=int, default=1)
@@ -602,6 +605,47 @@ def run_gemm_pmc(B: Bench, calls: int = 4):
             "dtype": "f16(q*s) x f16(x) -> f32" if gemm else "int8xf32",
             "data": "synthetic", "config": {"workload": f"{calls} x {kind} {M}x{N}x{K}, eager",
                                             "flop_per_call": 2 * M * N * K}}
+
+
+def run_attn_pmc(B: Bench, s: int = 2048, ctxlen: int = 2300, calls: int = 4):
+    """The launches the attention counter passes read, at the Llama-3.1-8B
+    shape (32 query / 8 KV heads, head_dim 128): `calls` eager prompt
+    attentions of `s` rows over a fresh cache, then `calls` eager one-token
+    steps (RoPE + KV append + attention, and the merge launch) at `ctxlen`
+    cached tokens."""
+    q8hip, ctx, torch = B.q8hip, B.ctx, B.torch
+    nh, nkv, hd = 32, 8, 128
+    qd, kvd = nh * hd, nkv * hd
+    maxlen = max(s, ctxlen) + 8
+    kv = torch.empty(2 * maxlen * kvd, device="cuda", dtype=torch.float16).normal_()
+    kvb = q8hip.Buffer.wrap(ctx, kv.data_ptr(), kv.numel() * 2)
+    # prompt rows: q [s, qd], out [s, qd], scratch
+    scratch = q8hip.attention_scratch_floats(s, nh, hd, maxlen)
+    oq, oy = 0, s * qd
+    osc = 2 * s * qd
+    a = torch.empty(osc + scratch + 64, device="cuda", dtype=torch.float32)
+    a[: s * qd] = B.activations(s * qd, 7)
+    ab = q8hip.Buffer.wrap(ctx, a.data_ptr(), a.numel() * 4)
+    for _ in range(calls):
+        q8hip.attention(ctx, ab, oq, kvb, 0, maxlen * kvd, maxlen, oy, osc, s, 0, nh, nkv, hd)
+    ctx.sync()
+    # one new token: q, k, v, inverse frequencies, out
+    inv = 1.0 / (500000.0 ** (np.arange(0, hd, 2, dtype=np.float64) / hd))
+    dq, dk, dv, dinv, dy = 0, qd, qd + kvd, qd + 2 * kvd, qd + 2 * kvd + hd
+    d = torch.empty(dy + qd + 64, device="cuda", dtype=torch.float32)
+    d[:dinv] = B.activations(dinv, 8)
+    d[dinv:dinv + hd // 2] = torch.tensor(inv, dtype=torch.float32, device="cuda")
+    db = q8hip.Buffer.wrap(ctx, d.data_ptr(), d.numel() * 4)
+    for _ in range(calls):
+        q8hip.decode_attention(ctx, db, dq, dk, dv, dinv, kvb, 0, maxlen * kvd, maxlen, dy,
+                               ctxlen, nh, nkv, hd)
+    ctx.sync()
+    return {"metric": "counter-pass launches (no timing)", "value": 0, "unit": "none",
+            "ms_per_step": 0.0, "higher_is_better": True, "dtype": "f32 (f16 cache)",
+            "data": "synthetic", "config": {"workload": f"{calls} x prompt attention of {s} "
+                                                        f"rows, {calls} x one-token step at "
+                                                        f"{ctxlen} cached tokens, 32/8 heads "
+                                                        "of 128, eager"}}
 
 
 def run_e2e_8b(B: Bench, prompt: int = 2048, gen: int = 256, rooflines: bool = True):
@@ -1105,6 +1149,8 @@ def main():
         res = run_lmhead_pmc(B)
     elif args.workload == "gemm-pmc":
         res = run_gemm_pmc(B)
+    elif args.workload == "attn-pmc":
+        res = run_attn_pmc(B)
     elif args.workload == "e2e-8b":
         res = run_e2e_8b(B)
     elif args.workload == "qwen8b":
