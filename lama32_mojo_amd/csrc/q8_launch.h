@@ -159,37 +159,44 @@ struct DecodeAttnArgs {
 // `part` must not overlap.
 // Keys per chunk (one wave's unit of work), waves per block, head slots of
 // a block and the split count.  Head slots: heads per wave GRP / slots,
-// waves per head waves / slots (the chunks a block spans).  With 64-dim
-// heads (short rows, contexts of a chunk or so per block) 4 waves, one head
-// per wave; with 128-dim heads in groups of 8, 4 waves serving 4 heads each,
-// so the K/V rows of a chunk are loaded once and the block's waves work on
-// different chunks (measured on the Llama-3.1-8B step at 2300 cached
-// tokens; slower on the 1B step); in groups of 4, 8 waves, two per chunk
-// with 2 heads each, which halves each wave's chain of dot products and
-// softmax work for the same blocks (Llama-3.1-8B at 2300 tokens: 9.98 ->
-// 9.75 us per call, the same bits; 8 waves over 2 chunks at 64-dim heads
-// lose: 7.17 -> 7.73 us); in groups of 2, 8 waves of one head each over 4
-// chunks instead of 4 waves over 2 chunks each, so no wave walks a second
-// chunk (Qwen3-0.6B at 128 tokens: 7.29 -> 6.05 us per call, step 0.6525
-// -> 0.6179 ms).  Splits: one chunk per wave and head slot (blocks
-// of waves / slots chunks) up to 32 blocks per KV head, then more chunks
-// per block.  Every launched block reads the position before it can leave
-// and a launch of 256 blocks takes about 1.4 us to start them all, so the
-// grid holds no more blocks than the longest context keeps busy.  A cache
-// of at most 4 chunks per wave gets one block per KV head, which writes the
-// output itself, and no merge launch (the merge costs more than the
-// chunks: Qwen3-0.6B at 128 cached tokens).
+// waves per head waves / slots (the chunks a block spans).
+//   * 64-dim heads: one head per wave; in groups of 4, 8 waves over two
+//     32-key chunks (the 64 keys a block of 4 waves over one 64-key chunk
+//     took, each wave's chain halved: Llama-3.2-1B at 1030 tokens 7.02 ->
+//     6.99 us per call, at 6000 10.78 -> 10.19 us; step 0.5054-0.5063 ->
+//     0.5041-0.5054 ms), else 4 waves over 64-key chunks (8 waves over two
+//     64-key chunks lose: 7.17 -> 7.73 us);
+//   * 128-dim heads, 32-key chunks: in groups of 8, 4 waves serving 4 heads
+//     each, so the K/V rows of a chunk are loaded once and the block's
+//     waves work on different chunks (measured on the Llama-3.1-8B step at
+//     2300 cached tokens; slower on the 1B step); in groups of 4, 8 waves,
+//     two per chunk with 2 heads each, which halves each wave's chain of
+//     dot products and softmax work for the same blocks (Llama-3.1-8B at
+//     2300 tokens: 9.98 -> 9.75 us per call, the same bits); in groups of
+//     2, 8 waves of one head each over 4 chunks instead of 4 waves over 2
+//     chunks each, so no wave walks a second chunk (Qwen3-0.6B at 128
+//     tokens: 7.29 -> 6.05 us per call, step 0.6525 -> 0.6179 ms).
+// Splits: one chunk per wave and head slot (blocks of waves / slots
+// chunks) up to 32 blocks per KV head, then more chunks per block.  Every
+// launched block reads the position before it can leave and a launch of
+// 256 blocks takes about 1.4 us to start them all, so the grid holds no
+// more blocks than the longest context keeps busy.  A cache of at most 4
+// chunks per wave gets one block per KV head, which writes the output
+// itself, and no merge launch (the merge costs more than the chunks:
+// Qwen3-0.6B at 128 cached tokens).
 constexpr int kDecodeAttnOneBlockChunks = 4;
 constexpr int kDecodeAttnMaxSplit = 32;   // bound of the merge's per-thread loads
-constexpr int decode_attn_chunk(int head_dim) { return head_dim > 64 ? 32 : 64; }
+constexpr int decode_attn_chunk(int head_dim, int grp) {
+  return (head_dim > 64 || grp == 4) ? 32 : 64;
+}
 constexpr int decode_attn_waves(int hd, int grp) {
-  return (hd >= 128 && (grp == 4 || grp == 2)) ? 8 : 4;
+  return ((hd >= 128 && (grp == 4 || grp == 2)) || (hd == 64 && grp == 4)) ? 8 : 4;
 }
 constexpr int decode_head_slots(int hd, int grp) {
   return (hd >= 128 && grp == 4) ? 2 : (hd >= 128 && grp > 4) ? grp / 4 : (grp < 4 ? grp : 4);
 }
 inline int decode_attn_nsplit(int64_t maxlen, int head_dim, int grp) {
-  const int64_t kc = decode_attn_chunk(head_dim);
+  const int64_t kc = decode_attn_chunk(head_dim, grp);
   const int64_t wph = decode_attn_waves(head_dim, grp) / decode_head_slots(head_dim, grp);
   const int64_t n = ((maxlen + kc - 1) / kc + wph - 1) / wph;
   return (int)(n <= kDecodeAttnOneBlockChunks ? 1 : n > 32 ? 32 : n);

@@ -503,7 +503,7 @@ __device__ __forceinline__ float lane_group_sum(float v) {
 
 // Grid (nkv, nsplit), NW = decode_attn_waves(HD, GRP) waves.  Block
 // (g, split) serves KV head g and its GRP query heads over the key chunks
-// [split * cpb, (split + 1) * cpb) of KC keys (64, or 32 at head_dim 128),
+// [split * cpb, (split + 1) * cpb) of KC = decode_attn_chunk(HD, GRP) keys,
 // cpb = max(waves per head, ceil(chunks / nsplit)).  The waves form
 // decode_head_slots(HD, GRP) head slots: wave w serves the GRP / slots query
 // heads of slot w % slots over chunk w / slots of the block's chunks (then
@@ -529,7 +529,7 @@ __global__ __launch_bounds__(64 * decode_attn_waves(HD, GRP)) void attn_decode_k
     const float *__restrict__ inv, __half *__restrict__ kc, __half *__restrict__ vc,
     float *__restrict__ part, float *__restrict__ out, int nkv, const int *posp, int pos0_host,
     int maxlen, const uint16_t *__restrict__ qnw, const uint16_t *__restrict__ knw, float eps) {
-  constexpr int KC = decode_attn_chunk(HD), NW = decode_attn_waves(HD, GRP), NT = 64 * NW;
+  constexpr int KC = decode_attn_chunk(HD, GRP), NW = decode_attn_waves(HD, GRP), NT = 64 * NW;
   constexpr int LPR = HD / 8;           // lanes per row (8 dims each)
   constexpr int RPI = 64 / LPR;         // rows per load instruction (row slots)
   constexpr int NI = KC / RPI;          // load instructions per chunk
@@ -849,7 +849,7 @@ __global__ __launch_bounds__(HD) void attn_merge_kernel(const float *__restrict_
                                                         float *__restrict__ out, int nsplit,
                                                         const int *posp, int pos0_host,
                                                         int maxlen) {
-  constexpr int KC = decode_attn_chunk(HD), NW = decode_attn_waves(HD, GRP);
+  constexpr int KC = decode_attn_chunk(HD, GRP), NW = decode_attn_waves(HD, GRP);
   constexpr int PR = HD + 2;
   constexpr int WPH = NW / decode_head_slots(HD, GRP);   // as attn_decode_kernel
   constexpr int NX = kDecodeAttnMaxSplit;
@@ -858,7 +858,8 @@ __global__ __launch_bounds__(HD) void attn_merge_kernel(const float *__restrict_
   // 8 it runs on the XCD of the split blocks that wrote KV head h / GRP's
   // records, so they are read from that XCD's L2
   const int nkvb = (int)gridDim.x / GRP;
-  const int h = ((int)blockIdx.x % nkvb) * GRP + (int)blockIdx.x / nkvb, g = h / GRP, hh = h % GRP;
+  const int h = ((int)blockIdx.x % nkvb) * GRP + (int)blockIdx.x / nkvb;
+  const int g = h / GRP, hh = h % GRP;
   const int d = threadIdx.x, lane = threadIdx.x & 63;
   const rsrc_t prs = make_rsrc(part + (int64_t)g * nsplit * (GRP * PR),
                                (uint32_t)(nsplit * GRP * PR) * 4u);

@@ -245,8 +245,9 @@ def test_attention_prompt_rows_any_q_scale(ctx, head_dim, nh, nkv):
 def test_decode_attention_equals_rope_then_attention(ctx, head_dim, nh, nkv, pos0):
     """The one-launch token step writes the same cache bits as q8_rope_kv and
     matches q8_rope_kv + q8_attention within 2e-6 (it sums the splits in
-    another order).  maxlen 1536 gives 24 splits of one 64-key chunk
-    (head_dim 64, one head per wave) or, at head_dim 128, 12 splits of four
+    another order).  maxlen 1536 gives 24 splits of two 32-key chunks
+    (head_dim 64 in groups of 4: 8 waves of one head each; of one 64-key
+    chunk in the other groups, one head per wave) or, at head_dim 128, 12 splits of four
     32-key chunks (groups of 4: 8 waves, two per chunk with 2 heads each)
     or 24 of two (groups of 8: each wave one chunk for 4 heads): small pos0
     is served by one block per KV head,
