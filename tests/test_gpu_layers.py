@@ -241,7 +241,7 @@ def test_attention_prompt_rows_any_q_scale(ctx, head_dim, nh, nkv):
 
 
 @pytest.mark.parametrize("head_dim,nh,nkv", [(64, 32, 8), (128, 32, 8), (64, 16, 16), (128, 8, 1)])
-@pytest.mark.parametrize("pos0", [0, 1, 63, 64, 500, 1023, 1500])
+@pytest.mark.parametrize("pos0", [0, 1, 31, 32, 63, 64, 95, 96, 500, 1023, 1500])
 def test_decode_attention_equals_rope_then_attention(ctx, head_dim, nh, nkv, pos0):
     """The one-launch token step writes the same cache bits as q8_rope_kv and
     matches q8_rope_kv + q8_attention within 2e-6 (it sums the splits in
